@@ -1,0 +1,358 @@
+"""Benchmark of the MI355X decode hot path (one GPU).
+
+Headline (BASELINE.json metric): greedy decode tok/s of the Bonsai-1.7B-shaped
+config-5 model at batch 1 -- 28 layers, 1-bit gs128 linears, bf16 embeddings,
+512-token prompt prefilled through the dequant-GEMM, then decode steps, each a
+replay of one captured hipGraph with on-device argmax.  A "step" is one decode
+token.  W warm-up steps run in a separate pass; the K timed steps are the first
+K steps after a fresh 512-token prefill (positions 512..512+K-1), bracketed by
+stream synchronisation.
+
+Also reported (same JSON line):
+  roofline      the dominant decode kernel: algorithmic bytes / average launch
+                duration (HIP events on the library's stream, weights rotated
+                through >= 512 MB of copies so every launch streams from HBM);
+  qmv           configs 1-3 (4-bit QMV, 1-bit QMV, fused gate/up+SiLU) in the
+                same way;
+  cpu_baseline  the numpy oracle's decode step on this host, bounded sample.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--lm-head q1|tied] [--quick]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_HBM_GBS = 8000.0
+BASELINE_TOKS = 182.8  # reference decode tok/s, Bonsai-1.7B Q1 bs1 (README.md:71-77)
+ROTATE_BYTES = 640 << 20
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------- decode ----
+def bench_decode(args, dev):
+    from nnzap_amd import configs as cf
+    from nnzap_amd.model import DecoderModel
+
+    cfg = cf.DecoderConfig(**{**cf.BONSAI_1_7B.__dict__,
+                              "lm_head_kind": 1 if args.lm_head == "tied" else 0})
+    t = time.time()
+    w = cf.decoder_weights(cfg, norm_mode="small")
+    m = DecoderModel(dev, cfg)
+    m.load(w, embed_on_device=True)
+    log(f"model ready in {time.time() - t:.1f}s")
+    prompt = cf.prompt_ids(cfg, args.prompt)
+    # warm-up pass (separate prefill)
+    m.decode_begin(prompt, max(args.warmup, 1))
+    m.decode_steps(max(args.warmup, 1))
+    m.decode_read(1)
+    m.decode_end()
+    # measured pass: prefill (timed separately), then exactly K decode steps
+    dev.sync()
+    tp0 = time.perf_counter()
+    m.decode_begin(prompt, args.steps)
+    dev.sync()
+    tp1 = time.perf_counter()
+    m.decode_steps(args.steps)
+    dev.sync()
+    t1 = time.perf_counter()
+    toks, margins = m.decode_read(args.steps)
+    m.decode_end()
+    dt = t1 - tp1
+    out = {
+        "tok_s": args.steps / dt,
+        "ms_per_step": 1000.0 * dt / args.steps,
+        "prefill_ms_incl_capture": 1000.0 * (tp1 - tp0),
+        "min_margin": float(np.min(margins)),
+        "tokens_head": toks[:8].tolist(),
+    }
+    gold = os.path.join(ROOT, "tests", "golden", "config5_tokens.json")
+    if os.path.exists(gold) and args.lm_head == "q1" and args.prompt == 512:
+        g = json.load(open(gold))
+        n = min(len(g["tokens"]), args.steps)
+        out["tokens_match_golden"] = bool(np.array_equal(toks[:n], np.array(g["tokens"][:n])))
+        out["golden_compared"] = n
+    m.close()
+    return out
+
+
+# --------------------------------------------------------------- kernels ----
+class Rot:
+    """Distinct device copies of one quantised matrix (same values, distinct
+    addresses), enough to exceed the on-die caches when cycled."""
+
+    def __init__(self, dev, w, total_bytes):
+        import torch
+        from nnzap_amd import ops
+        base = ops.DeviceQWeight(dev, w)
+        self.n = max(2, int(total_bytes // max(1, w.nbytes)) + 1)
+        self.ws = [base]
+        for _ in range(self.n - 1):
+            c = object.__new__(ops.DeviceQWeight)
+            c.__dict__.update(base.__dict__)
+            c.codes, c.scales = base.codes.clone(), base.scales.clone()
+            c.biases = base.biases.clone() if base.biases is not None else None
+            from nnzap_amd import _lib as L
+            c.desc = L.QWeightDesc(c.codes.data_ptr(), c.scales.data_ptr(),
+                                   c.biases.data_ptr() if c.biases is not None else None,
+                                   w.M * w.K, w.group_size, w.bits, w.scale_dtype)
+            self.ws.append(c)
+        torch.cuda.synchronize()
+
+    def __getitem__(self, i):
+        return self.ws[i % self.n]
+
+
+def time_launches(dev, fn, n_iter, reps=3):
+    """Average duration of one launch: events around n_iter back-to-back
+    launches on the library stream, best of ``reps`` blocks."""
+    fn(0)
+    dev.sync()
+    best = None
+    for r in range(reps):
+        dev.mark(0)
+        for i in range(n_iter):
+            fn(i + 1 + r * n_iter)
+        dev.mark(1)
+        ms = dev.elapsed_ms(0, 1) / n_iter
+        best = ms if best is None else min(best, ms)
+    return best * 1000.0  # us
+
+
+def bench_kernels(dev, quick=False):
+    import torch
+    from nnzap_amd import _lib as L
+    from nnzap_amd import configs as cf
+    from nnzap_amd import ops
+
+    n_iter = 64 if quick else 256
+    res = {}
+
+    def rec(name, us, nbytes, per_token=None):
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[name] = {"us": round(us, 3), "bytes": int(nbytes), "GBs": round(gbs, 1),
+                     "frac": round(gbs / PEAK_HBM_GBS, 4)}
+        if per_token is not None:
+            res[name]["per_token"] = per_token
+        log(f"{name:28s} {us:8.2f} us  {gbs:8.1f} GB/s  ({nbytes} B)")
+
+    f32, f16 = torch.float32, torch.float16
+    # config 1: Q4 W[6144 x 2048] gs64, f32 x/y
+    w1, x1 = cf.config1()
+    r = Rot(dev, w1, ROTATE_BYTES)
+    xd = torch.from_numpy(x1).cuda()
+    y = torch.empty(6144, dtype=f32, device="cuda")
+    torch.cuda.synchronize()
+    us = time_launches(dev, lambda i: ops.dispatch_q4mv(dev, r[i], xd, y), n_iter)
+    rec("config1_q4mv", us, w1.nbytes + 2048 * 4 + 6144 * 4)
+    del r
+    # config 2: Q1 W[2048 x 6144] gs128, f32 x/y
+    w2, x2 = cf.config2()
+    r = Rot(dev, w2, ROTATE_BYTES)
+    xd = torch.from_numpy(x2).cuda()
+    y = torch.empty(2048, dtype=f32, device="cuda")
+    torch.cuda.synchronize()
+    us = time_launches(dev, lambda i: ops.dispatch_qmv(dev, r[i], xd, y), n_iter)
+    rec("config2_qmv", us, w2.nbytes + 6144 * 4 + 2048 * 4)
+    del r
+    # config 3: fused gate/up + SiLU (f32 I/O)
+    wg, wu, x3 = cf.config3()
+    rg, ru = Rot(dev, wg, ROTATE_BYTES // 2), Rot(dev, wu, ROTATE_BYTES // 2)
+    xd = torch.from_numpy(x3).cuda()
+    y = torch.empty(6144, dtype=f32, device="cuda")
+    torch.cuda.synchronize()
+    us = time_launches(dev, lambda i: ops.dispatch_qmv_fused_pair_silu(dev, rg[i], ru[i], xd, y), n_iter)
+    rec("config3_gate_up_silu", us, wg.nbytes + wu.nbytes + 2048 * 4 + 6144 * 4)
+    del rg, ru
+
+    # decode-step kernels at config-5 shapes (counts per token in parentheses)
+    H, I, QD, KVD, V = 2048, 6144, 2048, 1024, 151936
+    res_d = torch.from_numpy(np.random.default_rng(0).standard_normal(H).astype(np.float32)).cuda()
+    nw = torch.ones(H, dtype=f32, device="cuda")
+    x16 = torch.randn(I, dtype=f16, device="cuda") * 0.05
+    o16a = torch.empty(I, dtype=f16, device="cuda")
+    o16b = torch.empty(I, dtype=f16, device="cuda")
+    resid = torch.zeros(H, dtype=f32, device="cuda")
+
+    wq = cf.q1_matrix(QD, H, 128, 500, 501)
+    r = Rot(dev, wq, ROTATE_BYTES)
+    torch.cuda.synchronize()
+    us = time_launches(dev, lambda i: ops.dispatch_fused_norm_qmv_f16io(dev, r[i], res_d, o16a, nw), n_iter)
+    rec("dec_q_norm_qmv", us, wq.nbytes + H * 8 + QD * 2, per_token=28)
+    del r
+    wk, wv = cf.q1_matrix(KVD, H, 128, 502, 503), cf.q1_matrix(KVD, H, 128, 504, 505)
+    rk, rv = Rot(dev, wk, ROTATE_BYTES // 2), Rot(dev, wv, ROTATE_BYTES // 2)
+    torch.cuda.synchronize()
+    us = time_launches(dev, lambda i: ops.dispatch_fused_norm_pair_qmv_f16io(
+        dev, rk[i], rv[i], res_d, o16a, o16b, nw), n_iter)
+    rec("dec_kv_norm_pair", us, wk.nbytes + wv.nbytes + H * 8 + KVD * 4, per_token=28)
+    del rk, rv
+    wo = cf.q1_matrix(H, QD, 128, 506, 507)
+    r = Rot(dev, wo, ROTATE_BYTES)
+    torch.cuda.synchronize()
+    us = time_launches(dev, lambda i: ops.dispatch_qmv_f16io_resadd(dev, r[i], x16[:QD], resid), n_iter)
+    rec("dec_o_resadd", us, wo.nbytes + QD * 2 + H * 8, per_token=28)
+    del r
+    wg5, wu5 = cf.q1_matrix(I, H, 128, 508, 509), cf.q1_matrix(I, H, 128, 510, 511)
+    rg, ru = Rot(dev, wg5, ROTATE_BYTES // 2), Rot(dev, wu5, ROTATE_BYTES // 2)
+    torch.cuda.synchronize()
+    us = time_launches(dev, lambda i: ops.dispatch_fused_norm_pair_silu_f16io(
+        dev, rg[i], ru[i], res_d, o16a, nw), n_iter)
+    rec("dec_gate_up_norm_silu", us, wg5.nbytes + wu5.nbytes + H * 8 + I * 2, per_token=28)
+    del rg, ru
+    wd = cf.q1_matrix(H, I, 128, 512, 513)
+    r = Rot(dev, wd, ROTATE_BYTES)
+    torch.cuda.synchronize()
+    us = time_launches(dev, lambda i: ops.dispatch_qmv_f16io_resadd(dev, r[i], x16, resid), n_iter)
+    rec("dec_down_resadd", us, wd.nbytes + I * 2 + H * 8, per_token=28)
+    del r
+    wl = cf.q1_matrix(V, H, 128, 514, 515)
+    r = Rot(dev, wl, ROTATE_BYTES)
+    logits = torch.empty(V, dtype=f32, device="cuda")
+    torch.cuda.synchronize()
+    us = time_launches(dev, lambda i: ops.dispatch_qmv_f16in(dev, r[i], x16[:H], logits),
+                       max(16, n_iter // 8))
+    rec("dec_lm_head_q1", us, wl.nbytes + H * 2 + V * 4, per_token=1)
+    del r
+    # attention over the average decode context of the timed steps (640)
+    seq, max_ctx = 640, 1024
+    kc = torch.randn(8, max_ctx, 128, device="cuda").to(f16)
+    vc = torch.randn(8, 128, max_ctx, device="cuda").to(f16)
+    qf = torch.randn(16, 128, device="cuda")
+    att = torch.empty(16, 128, dtype=f16, device="cuda")
+    dims = L.GQADims(16, 8, 128, seq, max_ctx, 2)
+    scr = torch.empty(ops.gqa_scratch_bytes(dims) // 4 + 64, dtype=f32, device="cuda")
+    torch.cuda.synchronize()
+    us = time_launches(dev, lambda i: ops.dispatch_gqa_attention(dev, qf, kc, vc, att, scr, dims), n_iter)
+    rec("dec_attention_seq640", us, 2 * 8 * seq * 128 * 2 + 16 * 128 * 6, per_token=28)
+    # config 4 (attention, bf16 KV [8, L, 128], q roped at L)
+    for L_ in (512, 4096, 32768):
+        kb = torch.randn(8, L_, 128, device="cuda").to(torch.bfloat16)
+        vb = torch.randn(8, L_, 128, device="cuda").to(torch.bfloat16)
+        qb = torch.randn(16, 128, device="cuda").to(torch.bfloat16)
+        ob = torch.empty(16, 128, dtype=f32, device="cuda")
+        d4 = L.GQADims(16, 8, 128, L_, L_, 2)
+        s4 = torch.empty(ops.gqa_scratch_bytes(d4) // 4 + 64, dtype=f32, device="cuda")
+        torch.cuda.synchronize()
+        us = time_launches(dev, lambda i: ops.dispatch_gqa_attention(
+            dev, qb, kb, vb, ob, s4, d4, v_transposed=False, rope_position=L_, rope_theta=1e6),
+            max(16, n_iter // 4))
+        rec(f"config4_attention_L{L_}", us, 4096 * L_ + 12288)
+        del kb, vb
+    return res
+
+
+# ------------------------------------------------------------ CPU baseline --
+def cpu_baseline(sample_layers=2, tokens=3):
+    """The numpy oracle's decode step on this host: `sample_layers` of the 28
+    layers (full shapes) + the full 1-bit LM head, `tokens` single-token
+    forwards after a 64-token prefill; tok/s extrapolated to 28 layers."""
+    from nnzap_amd import configs as cf
+    from oracle.decoder import OracleDecoder
+
+    cfg = cf.DecoderConfig(**{**cf.BONSAI_1_7B.__dict__, "num_layers": sample_layers,
+                              "max_context_length": 1024})
+    w = cf.decoder_weights(cfg, norm_mode="small")
+    od = OracleDecoder(w)
+    prompt = cf.prompt_ids(cfg, 64)
+    od.forward(list(prompt), 0)
+    xf = np.zeros((1, cfg.hidden_size))
+    t0 = time.perf_counter()
+    for _ in range(tokens):
+        od.lm_head(xf)
+    t_lm = (time.perf_counter() - t0) / tokens
+    t0 = time.perf_counter()
+    for i in range(tokens):
+        od.forward([int(prompt[i])], 64 + i)
+    t_tok = (time.perf_counter() - t0) / tokens
+    t_layer = max(t_tok - t_lm, 1e-9) / sample_layers
+    per_token = t_lm + 28 * t_layer
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(1.0 / per_token, 4), "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": (f"numpy float64 oracle (OracleDecoder), {tokens} single-token decode steps "
+                       f"through {sample_layers} full-size layers + 1-bit LM head at position 64+; "
+                       f"per-token time = LM head + 28 x measured per-layer time")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=256)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--prompt", type=int, default=512)
+    ap.add_argument("--lm-head", choices=("q1", "tied"), default="q1")
+    ap.add_argument("--quick", action="store_true", help="fewer kernel timing iterations")
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-kernels", action="store_true")
+    ap.add_argument("--details", default=None, help="write the full result dict here")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE {world}); "
+              "the decode path has no multi-GPU mode in this build", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from nnzap_amd.ops import Device
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = Device(0, own_stream=True)
+    log(f"device: {torch.cuda.get_device_name(0)}")
+    dec = bench_decode(args, dev)
+    log(f"decode: {dec['tok_s']:.1f} tok/s ({dec['ms_per_step']:.3f} ms/step)")
+    kern = {} if args.skip_kernels else bench_kernels(dev, quick=args.quick)
+
+    roofline = None
+    dec_k = {k: v for k, v in kern.items() if "per_token" in v}
+    if dec_k:
+        dom = max(dec_k, key=lambda k: dec_k[k]["us"] * dec_k[k]["per_token"])
+        d = dec_k[dom]
+        roofline = {"kernel": dom, "bound": "hbm", "achieved": d["GBs"], "peak": PEAK_HBM_GBS,
+                    "unit": "GB/s", "frac": round(d["GBs"] / PEAK_HBM_GBS, 4), "traffic": None,
+                    "avg_launch_us": d["us"], "algorithmic_bytes": d["bytes"]}
+    cpu = None if args.skip_cpu else cpu_baseline()
+
+    line = {
+        "metric": "decode tok/s (Bonsai-1.7B, bs1) + QMV achieved HBM GB/s vs peak",
+        "value": round(dec["tok_s"], 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(dec["tok_s"] / BASELINE_TOKS, 2),
+        "dtype": "q1-weights/f16-act/f32-acc",
+        "data": "synthetic: seeded random-init weights, uniform random prompt ids",
+        "config": {"workload": "config5 Bonsai-1.7B-shaped decoder: 28 layers, hidden 2048, "
+                               "MLP 6144, 16Q/8KV x 128, vocab 151936, 1-bit gs128 linears, "
+                               "bf16 embeddings/norms, 512-token GEMM prefill, greedy decode",
+                   "lm_head": args.lm_head, "prompt": args.prompt, "batch": 1,
+                   "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "decode": dec,
+        "qmv": {k: v for k, v in kern.items() if k.startswith("config")},
+        "decode_kernels": dec_k,
+    }
+    if args.details:
+        with open(args.details, "w") as f:
+            json.dump(line, f, indent=1)
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,36 @@
+// Internal (non-exported) entry points shared between the library's sources.
+#pragma once
+
+#include "common.h"
+
+// One attention launch with full control over chunking and batching.
+struct NnzAttnCall {
+    const void *q = nullptr;
+    int qdt = NNZ_F32;
+    uint32_t q_stride = 0;       // elements between queries (0: Hq*D)
+    const void *kc = nullptr;
+    const void *vc = nullptr;
+    int kvdt = NNZ_F16;
+    bool vt = true;              // V stored [Hkv][D][max_ctx]
+    void *out = nullptr;
+    int odt = NNZ_F16;
+    uint32_t o_stride = 0;       // elements between outputs (0: Hq*D)
+    float *part_o = nullptr;     // [nq][Hq][nchunks][D]
+    float *part_ml = nullptr;    // [nq][Hq][nchunks][2]
+    const uint32_t *d_seq = nullptr;  // device seq_len of query 0 (overrides dims.seq_len)
+    uint32_t chunk = 0, nchunks = 0, nq = 1;
+    int32_t rope_pos = -1;
+    float rope_theta = 0.f;
+    nnz_gqa_dims dims{};
+};
+
+uint32_t nnz_attn_chunk(uint32_t seq_len, uint32_t hkv);
+int nnz_attn_launch_ex(nnz_ctx *ctx, const NnzAttnCall &c);
+int nnz_attn_prep_launch(nnz_ctx *ctx, const void *q, const void *kr, const void *vr,
+                         const float *qn, const float *kn, float *qout, void *kc, void *vc,
+                         uint32_t hq, uint32_t hkv, uint32_t head_dim, uint32_t pos,
+                         const uint32_t *d_pos, uint32_t nq, uint32_t max_ctx, float eps,
+                         float theta);
+int nnz_argmax_launch(nnz_ctx *ctx, const float *x, uint32_t n, uint32_t *oi, float *ov);
+int nnz_gemm_launch(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, const void *a,
+                    uint32_t P, void *out, int mode, const nnz_qmv_dims &d);

@@ -1,0 +1,750 @@
+// Decoder model: Model(Config) state, forwardDecode, batched prefill and the
+// greedy generate loop on one MI355X.
+//
+// Replaces nnmetal/src/model.zig:38-777 (Model: weights, KV caches and
+// activation scratch allocated once), transformer.zig:2389-3646 (the decode
+// graph: embed -> 28 x (attention half, MLP half) -> final norm -> LM head)
+// and transformer.zig:3942-4123 (generate / decodeOneToken).
+//
+// MI355X-first differences:
+//   * Every buffer lives in HBM (hipMalloc), uploaded once; nothing is shared
+//     with the host on the hot path.
+//   * The decode step reads token id, position and sequence length from a
+//     small device state block, so the whole step is captured once as a HIP
+//     graph and replayed for every token.  Greedy argmax runs on the device
+//     and writes the next token into that state block, so consecutive steps
+//     are queued back to back with no host round trip (the reference reads
+//     607 KB of logits to the CPU and spin-waits on a flag per token,
+//     transformer.zig:4072-4122, metal.zig:1325-1352).
+//   * Prefill runs the prompt as one batch through the MFMA dequant-GEMM and a
+//     causal batched attention instead of P sequential decode steps
+//     (transformer.zig:4032-4068).  Storage rounding points are the same as
+//     the decode step: f16 activations and KV cache, f32 residual stream.
+#include "internal.h"
+
+#include <vector>
+
+// Public launchers implemented in qmv.hip / transformer.hip.
+extern "C" {
+int nnz_dispatch_fused_norm_qmv_f16io(nnz_ctx *, const nnz_qweight *, const float *, void *,
+                                      const float *, nnz_qmv_dims);
+int nnz_dispatch_fused_norm_pair_qmv_f16io(nnz_ctx *, const nnz_qweight *, const nnz_qweight *,
+                                           const float *, void *, void *, const float *,
+                                           nnz_qmv_dims);
+int nnz_dispatch_fused_norm_pair_silu_f16io(nnz_ctx *, const nnz_qweight *, const nnz_qweight *,
+                                            const float *, void *, const float *, nnz_qmv_dims);
+int nnz_dispatch_qmv_f16io_resadd(nnz_ctx *, const nnz_qweight *, const void *, float *,
+                                  nnz_qmv_dims);
+int nnz_dispatch_qmv_f16in(nnz_ctx *, const nnz_qweight *, const void *, float *, nnz_qmv_dims);
+}
+
+namespace {
+
+// Device state block: token id, position, visible sequence length, step.
+enum { ST_TOKEN = 0, ST_POS = 1, ST_SEQ = 2, ST_STEP = 3 };
+
+__global__ void embed_state_q1_kernel(const uint32_t *state, const uint8_t *bits,
+                                      const uint16_t *scales, float *out, uint32_t hidden,
+                                      uint32_t gs, uint32_t vocab) {
+    const uint32_t d = blockIdx.x * blockDim.x + threadIdx.x;
+    if (d >= hidden) return;
+    uint32_t row = state[ST_TOKEN];
+    if (row >= vocab) row = vocab - 1;
+    const uint64_t flat = (uint64_t)row * hidden + d;
+    const bool bit = (bits[flat >> 3] >> (flat & 7)) & 1;
+    const float s = (float)__builtin_bit_cast(f16_t, scales[flat / gs]);
+    out[d] = bit ? s : -s;
+}
+
+__global__ void embed_state_bf16_kernel(const uint32_t *state, const uint16_t *table, float *out,
+                                        uint32_t hidden, uint32_t vocab) {
+    const uint32_t d = blockIdx.x * blockDim.x + threadIdx.x;
+    if (d >= hidden) return;
+    uint32_t row = state[ST_TOKEN];
+    if (row >= vocab) row = vocab - 1;
+    out[d] = bf16_to_f32(table[(size_t)row * hidden + d]);
+}
+
+__global__ void embed_ids_q1_kernel(const uint32_t *ids, const uint8_t *bits, const uint16_t *scales,
+                                    float *out, uint32_t hidden, uint32_t ntok, uint32_t gs,
+                                    uint32_t vocab) {
+    const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= ntok * hidden) return;
+    const uint32_t t = gid / hidden, d = gid % hidden;
+    uint32_t row = ids[t];
+    if (row >= vocab) row = vocab - 1;
+    const uint64_t flat = (uint64_t)row * hidden + d;
+    const bool bit = (bits[flat >> 3] >> (flat & 7)) & 1;
+    const float s = (float)__builtin_bit_cast(f16_t, scales[flat / gs]);
+    out[gid] = bit ? s : -s;
+}
+
+__global__ void embed_ids_bf16_kernel(const uint32_t *ids, const uint16_t *table, float *out,
+                                      uint32_t hidden, uint32_t ntok, uint32_t vocab) {
+    const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= ntok * hidden) return;
+    const uint32_t t = gid / hidden, d = gid % hidden;
+    uint32_t row = ids[t];
+    if (row >= vocab) row = vocab - 1;
+    out[gid] = bf16_to_f32(table[(size_t)row * hidden + d]);
+}
+
+// Dense bf16 LM head (tied embedding table): y[v] = sum_k E[v][k] x[k], x f16.
+// Same lane layout as the QMV kernels: a lane owns 32-column units of the
+// row (64 bytes = four 16-byte loads), x slice in registers, rows reduced
+// across the lane group.
+template <int NV>
+__global__ __launch_bounds__(256) void dense_bf16_gemv_kernel(const uint16_t *E, const f16_t *x,
+                                                              float *y, uint32_t M, uint32_t K,
+                                                              uint32_t lpr_log2) {
+    const int lane = threadIdx.x & 63;
+    const int LPR = 1 << lpr_log2, RPW = 64 >> lpr_log2;
+    const int rr = lane >> lpr_log2, ll = lane & (LPR - 1);
+    const uint32_t units = K / 32;
+    float xr[NV][32];
+    bool uv[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const uint32_t u = ll + LPR * j;
+        uv[j] = u < units;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) xr[j][i] = uv[j] ? (float)x[u * 32 + i] : 0.f;
+    }
+    const uint32_t wave = blockIdx.x * 4 + (threadIdx.x >> 6), nw = gridDim.x * 4;
+    for (uint32_t row = wave * RPW + rr; row < M + rr; row += nw * RPW) {
+        const bool ok = row < M;
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const uint32_t u = ll + LPR * j;
+            if (!(ok && uv[j])) continue;
+            const uint4 *p = (const uint4 *)(E + (size_t)row * K + u * 32);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const uint4 w = p[v];
+                const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    acc = fmaf(bf16_to_f32((uint16_t)(wv[e] & 0xFFFFu)), xr[j][8 * v + 2 * e], acc);
+                    acc = fmaf(bf16_to_f32((uint16_t)(wv[e] >> 16)), xr[j][8 * v + 2 * e + 1], acc);
+                }
+            }
+        }
+        acc = group_sum(acc, LPR);
+        if (ok && ll == 0) y[row] = acc;
+    }
+}
+
+// Greedy step: argmax (first maximum wins, transformer.zig:3694-3707), record
+// the token and its top-2 margin, then advance token/position/step.
+__global__ __launch_bounds__(1024) void argmax_advance_kernel(const float *x, uint32_t n,
+                                                              uint32_t *state, uint32_t *tokens,
+                                                              float *margins, uint32_t cap) {
+    __shared__ float sv[1024], sv2[1024];
+    __shared__ uint32_t si[1024];
+    float best = -INFINITY, second = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    for (uint32_t i = threadIdx.x; i < n; i += 1024) {
+        const float v = x[i];
+        if (v > best) { second = best; best = v; bi = i; }
+        else if (v > second) second = v;
+    }
+    sv[threadIdx.x] = best; sv2[threadIdx.x] = second; si[threadIdx.x] = bi;
+    __syncthreads();
+    for (uint32_t s = 512; s > 0; s >>= 1) {
+        if (threadIdx.x < s) {
+            const float a = sv[threadIdx.x], b = sv[threadIdx.x + s];
+            const uint32_t ia = si[threadIdx.x], ib = si[threadIdx.x + s];
+            const bool take_b = (b > a) || (b == a && ib < ia);
+            const float lo = take_b ? a : b;
+            sv2[threadIdx.x] = fmaxf(fmaxf(sv2[threadIdx.x], sv2[threadIdx.x + s]), lo);
+            sv[threadIdx.x] = take_b ? b : a;
+            si[threadIdx.x] = take_b ? ib : ia;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const uint32_t tok = si[0] == 0xFFFFFFFFu ? 0u : si[0];
+        const uint32_t step = state[ST_STEP];
+        if (step < cap) {
+            tokens[step] = tok;
+            margins[step] = sv[0] - sv2[0];
+        }
+        state[ST_TOKEN] = tok;
+        state[ST_POS] += 1;
+        state[ST_SEQ] += 1;
+        state[ST_STEP] = step + 1;
+    }
+}
+
+struct Proj {
+    void *codes = nullptr, *scales = nullptr;
+    uint32_t M = 0, K = 0;
+    nnz_qweight w{};
+};
+
+struct Layer {
+    Proj q, k, v, o, gate, up, down;
+    float *attn_norm = nullptr, *ffn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr;
+    void *kc = nullptr, *vc = nullptr;
+};
+
+}  // namespace
+
+struct nnz_model {
+    nnz_ctx *ctx = nullptr;
+    nnz_model_config c{};
+    uint32_t qdim = 0, kvdim = 0, G = 0;
+    std::vector<Layer> L;
+    void *emb = nullptr, *emb_scales = nullptr;
+    Proj lm;
+    float *final_norm = nullptr;
+    // decode activations
+    float *residual = nullptr, *logits = nullptr, *qf = nullptr;
+    f16_t *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *h = nullptr;
+    float *part_o = nullptr, *part_ml = nullptr;
+    uint32_t part_chunks = 0;  // capacity in chunks per query head
+    uint32_t *state = nullptr;
+    uint32_t *tokens_out = nullptr;
+    float *margins_out = nullptr;
+    uint32_t out_cap = 0;
+    // prefill activations (allocated on first use, sized for max_prefill_length)
+    float *p_res = nullptr, *p_qf = nullptr, *p_part_o = nullptr, *p_part_ml = nullptr;
+    size_t p_part_floats = 0;
+    f16_t *p_xn = nullptr, *p_q = nullptr, *p_k = nullptr, *p_v = nullptr, *p_att = nullptr,
+          *p_h = nullptr;
+    uint32_t *p_ids = nullptr;
+    std::vector<void *> allocs;
+    // streaming decode (decode_begin / steps / read / end)
+    nnz_graph *step_graph = nullptr;
+    uint32_t stream_steps_left = 0;
+    uint32_t stream_emitted = 0;
+};
+
+namespace {
+
+int model_alloc(nnz_model *m, size_t bytes, void **out) {
+    void *p = nullptr;
+    if (hipMalloc(&p, bytes) != hipSuccess)
+        return nnz_fail(m->ctx, NNZ_ENOMEM, "model: hipMalloc(%zu) failed", bytes);
+    m->allocs.push_back(p);
+    if (hipMemsetAsync(p, 0, bytes, m->ctx->stream) != hipSuccess)
+        return nnz_fail(m->ctx, NNZ_EHIP, "model: memset failed");
+    *out = p;
+    return NNZ_OK;
+}
+
+#define MALLOC(ptr, bytes)                                                   \
+    do {                                                                     \
+        void *p_;                                                            \
+        int rc_ = model_alloc(m, (bytes), &p_);                              \
+        if (rc_) return rc_;                                                 \
+        (ptr) = (decltype(ptr))p_;                                           \
+    } while (0)
+
+int alloc_proj(nnz_model *m, Proj &p, uint32_t M, uint32_t K) {
+    p.M = M;
+    p.K = K;
+    MALLOC(p.codes, (size_t)M * K / 8);
+    MALLOC(p.scales, (size_t)M * K / m->c.group_size * 2);
+    p.w.codes = p.codes;
+    p.w.scales = p.scales;
+    p.w.biases = nullptr;
+    p.w.packed_count = M * K;
+    p.w.group_size = m->c.group_size;
+    p.w.bits = 1;
+    p.w.scale_dtype = NNZ_F16;
+    return NNZ_OK;
+}
+
+nnz_qmv_dims dims_of(const nnz_model *m, const Proj &p) { return {p.M, p.K, m->c.group_size}; }
+
+nnz_gqa_dims gqa_dims(const nnz_model *m, uint32_t seq) {
+    return {m->c.num_query_heads, m->c.num_kv_heads, m->c.head_dim, seq, m->c.max_context_length,
+            m->G};
+}
+
+int lm_head(nnz_model *m, const f16_t *x, float *logits) {
+    if (m->c.lm_head_kind == NNZ_LMHEAD_Q1)
+        return nnz_dispatch_qmv_f16in(m->ctx, &m->lm.w, x, logits, dims_of(m, m->lm));
+    const uint32_t K = m->c.hidden_size, units = K / 32;
+    uint32_t lpr = 1;
+    while (lpr < units && lpr < 64) lpr <<= 1;
+    int lg = 0;
+    while ((1u << lg) < lpr) ++lg;
+    const uint32_t nv = ceil_div(units, lpr);
+    const uint32_t rows_per_block = 4 * (64 / lpr);
+    uint32_t blocks = ceil_div(m->c.vocab_size, rows_per_block);
+    if (blocks > 4096) blocks = 4096;
+    if (nv == 1)
+        dense_bf16_gemv_kernel<1><<<blocks, 256, 0, m->ctx->stream>>>(
+            (const uint16_t *)m->emb, x, logits, m->c.vocab_size, K, lg);
+    else if (nv == 2)
+        dense_bf16_gemv_kernel<2><<<blocks, 256, 0, m->ctx->stream>>>(
+            (const uint16_t *)m->emb, x, logits, m->c.vocab_size, K, lg);
+    else
+        return nnz_fail(m->ctx, NNZ_EUNSUPPORTED, "tied bf16 LM head: hidden %u > 4096", K);
+    NNZ_LAUNCHED(m->ctx);
+    return NNZ_OK;
+}
+
+#define RC(x)                  \
+    do {                       \
+        int rc_ = (x);         \
+        if (rc_) return rc_;   \
+    } while (0)
+
+// One decode step for the token/position held in the device state block.
+// `chunk`/`nchunks` fix the attention grid for every position this step may
+// be replayed at (sequence length up to chunk * nchunks).
+int enqueue_decode_step(nnz_model *m, uint32_t chunk, uint32_t nchunks) {
+    nnz_ctx *ctx = m->ctx;
+    const nnz_model_config &c = m->c;
+    const uint32_t H = c.hidden_size;
+    if (c.embed_kind == NNZ_EMBED_Q1)
+        embed_state_q1_kernel<<<ceil_div(H, 256), 256, 0, ctx->stream>>>(
+            m->state, (const uint8_t *)m->emb, (const uint16_t *)m->emb_scales, m->residual, H,
+            c.group_size, c.vocab_size);
+    else
+        embed_state_bf16_kernel<<<ceil_div(H, 256), 256, 0, ctx->stream>>>(
+            m->state, (const uint16_t *)m->emb, m->residual, H, c.vocab_size);
+    NNZ_LAUNCHED(ctx);
+
+    for (uint32_t l = 0; l < c.num_layers; ++l) {
+        Layer &Ly = m->L[l];
+        // transformer.zig:3024-3083 encodeAttnProjFusedNorm
+        RC(nnz_dispatch_fused_norm_qmv_f16io(ctx, &Ly.q.w, m->residual, m->q, Ly.attn_norm,
+                                             dims_of(m, Ly.q)));
+        RC(nnz_dispatch_fused_norm_pair_qmv_f16io(ctx, &Ly.k.w, &Ly.v.w, m->residual, m->k, m->v,
+                                                  Ly.attn_norm, dims_of(m, Ly.k)));
+        // transformer.zig:3244-3370 encodeAttentionGather (fused Q/K norm, RoPE,
+        // KV append, attention), then O-proj with residual +=.
+        RC(nnz_attn_prep_launch(ctx, m->q, m->k, m->v, Ly.q_norm, Ly.k_norm, m->qf, Ly.kc, Ly.vc,
+                                c.num_query_heads, c.num_kv_heads, c.head_dim, 0,
+                                m->state + ST_POS, 1, c.max_context_length, c.rms_eps,
+                                c.rope_theta));
+        NnzAttnCall ac{};
+        ac.q = m->qf;
+        ac.qdt = NNZ_F32;
+        ac.kc = Ly.kc;
+        ac.vc = Ly.vc;
+        ac.kvdt = NNZ_F16;
+        ac.vt = true;
+        ac.out = m->att;
+        ac.odt = NNZ_F16;
+        ac.part_o = m->part_o;
+        ac.part_ml = m->part_ml;
+        ac.d_seq = m->state + ST_SEQ;
+        ac.chunk = chunk;
+        ac.nchunks = nchunks;
+        ac.nq = 1;
+        ac.dims = gqa_dims(m, 0);
+        RC(nnz_attn_launch_ex(ctx, ac));
+        RC(nnz_dispatch_qmv_f16io_resadd(ctx, &Ly.o.w, m->att, m->residual, dims_of(m, Ly.o)));
+        // transformer.zig:3372-3646 encodeMLPHalf (fused norm + gate/up + SiLU, down += )
+        RC(nnz_dispatch_fused_norm_pair_silu_f16io(ctx, &Ly.gate.w, &Ly.up.w, m->residual, m->h,
+                                                   Ly.ffn_norm, dims_of(m, Ly.gate)));
+        RC(nnz_dispatch_qmv_f16io_resadd(ctx, &Ly.down.w, m->h, m->residual, dims_of(m, Ly.down)));
+    }
+    // transformer.zig:2730-2785 encodeFinalNormAndLMHead
+    RC(nnz_dispatch_rms_norm(ctx, m->residual, m->final_norm, m->xn, NNZ_F16, 0,
+                             {H, 1, c.rms_eps}));
+    return lm_head(m, m->xn, m->logits);
+}
+
+void decode_plan(const nnz_model *m, uint32_t max_seq, uint32_t *chunk, uint32_t *nch) {
+    *chunk = nnz_attn_chunk(max_seq, m->c.num_kv_heads);
+    *nch = ceil_div(max_seq, *chunk);
+}
+
+int ensure_prefill_buffers(nnz_model *m, uint32_t n, uint32_t start) {
+    const nnz_model_config &c = m->c;
+    const uint32_t P = c.max_prefill_length;
+    if (!m->p_res) {
+        MALLOC(m->p_res, (size_t)P * c.hidden_size * 4);
+        MALLOC(m->p_xn, (size_t)P * c.hidden_size * 2);
+        MALLOC(m->p_q, (size_t)P * m->qdim * 2);
+        MALLOC(m->p_k, (size_t)P * m->kvdim * 2);
+        MALLOC(m->p_v, (size_t)P * m->kvdim * 2);
+        MALLOC(m->p_att, (size_t)P * m->qdim * 2);
+        MALLOC(m->p_h, (size_t)P * c.intermediate_size * 2);
+        MALLOC(m->p_qf, (size_t)P * m->qdim * 4);
+        MALLOC(m->p_ids, (size_t)P * 4);
+    }
+    const uint32_t nch = ceil_div(start + n, 512);
+    const size_t need = (size_t)n * c.num_query_heads * nch * (c.head_dim + 2) + 64;
+    if (need > m->p_part_floats) {
+        float *p;
+        MALLOC(p, need * 4);
+        m->p_part_o = p;
+        m->p_part_ml = p + (size_t)n * c.num_query_heads * nch * c.head_dim;
+        m->p_part_floats = need;
+    }
+    return NNZ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int nnz_model_create(nnz_ctx *ctx, const nnz_model_config *cfg, nnz_model **out) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, cfg && out, NNZ_EINVAL, "model_create: null argument");
+    NNZ_REQUIRE(ctx, !ctx->capturing, NNZ_ESTATE, "model_create: not allowed during capture");
+    const nnz_model_config &c = *cfg;
+    NNZ_REQUIRE(ctx, c.vocab_size && c.hidden_size && c.intermediate_size && c.num_layers &&
+                         c.num_query_heads && c.num_kv_heads && c.head_dim && c.max_context_length &&
+                         c.max_prefill_length && c.group_size,
+                NNZ_EINVAL, "model_create: zero field in config");
+    NNZ_REQUIRE(ctx, c.num_query_heads % c.num_kv_heads == 0, NNZ_EINVAL,
+                "model_create: query heads not a multiple of KV heads");
+    NNZ_REQUIRE(ctx, c.max_prefill_length <= c.max_context_length, NNZ_EINVAL,
+                "model_create: max_prefill_length > max_context_length");
+    NNZ_REQUIRE(ctx, c.hidden_size % 64 == 0 && c.intermediate_size % 64 == 0 &&
+                         (c.num_query_heads * c.head_dim) % 64 == 0 &&
+                         (c.num_kv_heads * c.head_dim) % 64 == 0 && c.group_size % 64 == 0 &&
+                         c.hidden_size % c.group_size == 0 &&
+                         c.intermediate_size % c.group_size == 0 &&
+                         (c.num_query_heads * c.head_dim) % c.group_size == 0,
+                NNZ_EUNSUPPORTED, "model_create: dims must be multiples of 64 and of group_size");
+    NNZ_REQUIRE(ctx, c.max_context_length % 8 == 0, NNZ_EUNSUPPORTED,
+                "model_create: max_context_length must be a multiple of 8");
+    NNZ_REQUIRE(ctx, (uint64_t)c.vocab_size * c.hidden_size < (1ull << 32), NNZ_EUNSUPPORTED,
+                "model_create: vocab*hidden must fit in 32 bits");
+    NNZ_REQUIRE(ctx, c.embed_kind <= NNZ_EMBED_BF16 && c.lm_head_kind <= NNZ_LMHEAD_TIED_BF16 &&
+                         !(c.lm_head_kind == NNZ_LMHEAD_TIED_BF16 && c.embed_kind != NNZ_EMBED_BF16),
+                NNZ_EINVAL, "model_create: bad embed/lm_head kind");
+
+    nnz_model *m = new nnz_model();
+    m->ctx = ctx;
+    m->c = c;
+    m->qdim = c.num_query_heads * c.head_dim;
+    m->kvdim = c.num_kv_heads * c.head_dim;
+    m->G = c.num_query_heads / c.num_kv_heads;
+    auto fail = [&](int rc) {
+        nnz_model_destroy(m);
+        return rc;
+    };
+    auto body = [&]() -> int {
+        const size_t VH = (size_t)c.vocab_size * c.hidden_size;
+        if (c.embed_kind == NNZ_EMBED_Q1) {
+            MALLOC(m->emb, VH / 8 + 4);
+            MALLOC(m->emb_scales, ceil_div((uint32_t)VH, c.group_size) * 2);
+        } else {
+            MALLOC(m->emb, VH * 2);
+        }
+        if (c.lm_head_kind == NNZ_LMHEAD_Q1) RC(alloc_proj(m, m->lm, c.vocab_size, c.hidden_size));
+        MALLOC(m->final_norm, c.hidden_size * 4);
+        m->L.resize(c.num_layers);
+        const size_t kv_bytes = (size_t)c.num_kv_heads * c.max_context_length * c.head_dim * 2;
+        for (auto &Ly : m->L) {
+            RC(alloc_proj(m, Ly.q, m->qdim, c.hidden_size));
+            RC(alloc_proj(m, Ly.k, m->kvdim, c.hidden_size));
+            RC(alloc_proj(m, Ly.v, m->kvdim, c.hidden_size));
+            RC(alloc_proj(m, Ly.o, c.hidden_size, m->qdim));
+            RC(alloc_proj(m, Ly.gate, c.intermediate_size, c.hidden_size));
+            RC(alloc_proj(m, Ly.up, c.intermediate_size, c.hidden_size));
+            RC(alloc_proj(m, Ly.down, c.hidden_size, c.intermediate_size));
+            MALLOC(Ly.attn_norm, c.hidden_size * 4);
+            MALLOC(Ly.ffn_norm, c.hidden_size * 4);
+            MALLOC(Ly.q_norm, c.head_dim * 4);
+            MALLOC(Ly.k_norm, c.head_dim * 4);
+            MALLOC(Ly.kc, kv_bytes);
+            MALLOC(Ly.vc, kv_bytes);
+        }
+        MALLOC(m->residual, c.hidden_size * 4);
+        MALLOC(m->logits, (size_t)c.vocab_size * 4);
+        MALLOC(m->qf, m->qdim * 4);
+        MALLOC(m->xn, c.hidden_size * 2);
+        MALLOC(m->q, m->qdim * 2);
+        MALLOC(m->k, m->kvdim * 2);
+        MALLOC(m->v, m->kvdim * 2);
+        MALLOC(m->att, m->qdim * 2);
+        MALLOC(m->h, c.intermediate_size * 2);
+        // Worst-case attention partials: chunk >= 64 tokens at any length.
+        m->part_chunks = ceil_div(c.max_context_length, 64);
+        float *parts;
+        MALLOC(parts, (size_t)c.num_query_heads * m->part_chunks * (c.head_dim + 2) * 4);
+        m->part_o = parts;
+        m->part_ml = parts + (size_t)c.num_query_heads * m->part_chunks * c.head_dim;
+        MALLOC(m->state, 64);
+        m->out_cap = c.max_context_length + 1;
+        MALLOC(m->tokens_out, (size_t)m->out_cap * 4);
+        MALLOC(m->margins_out, (size_t)m->out_cap * 4);
+        NNZ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        return NNZ_OK;
+    };
+    int rc = body();
+    if (rc) return fail(rc);
+    *out = m;
+    return NNZ_OK;
+}
+
+int nnz_model_destroy(nnz_model *m) {
+    if (!m) return NNZ_EINVAL;
+    hipStreamSynchronize(m->ctx->stream);
+    if (m->step_graph) nnz_graph_destroy(m->step_graph);
+    for (void *p : m->allocs) hipFree(p);
+    delete m;
+    return NNZ_OK;
+}
+
+int nnz_model_tensor(nnz_model *m, int id, uint32_t layer, void **ptr, size_t *bytes) {
+    if (!m || !ptr || !bytes) return NNZ_EINVAL;
+    nnz_ctx *ctx = m->ctx;
+    const nnz_model_config &c = m->c;
+    const size_t VH = (size_t)c.vocab_size * c.hidden_size;
+    auto set = [&](void *p, size_t b) {
+        *ptr = p;
+        *bytes = b;
+        return p ? NNZ_OK : nnz_fail(ctx, NNZ_ESTATE, "tensor %d not present in this config", id);
+    };
+    if (id < 10 || id >= 40) {
+        switch (id) {
+        case NNZ_T_EMBED_CODES:
+            return set(m->emb, c.embed_kind == NNZ_EMBED_Q1 ? VH / 8 : VH * 2);
+        case NNZ_T_EMBED_SCALES:
+            return set(m->emb_scales, c.embed_kind == NNZ_EMBED_Q1 ? ceil_div((uint32_t)VH, c.group_size) * 2 : 0);
+        case NNZ_T_LM_CODES: return set(m->lm.codes, VH / 8);
+        case NNZ_T_LM_SCALES: return set(m->lm.scales, VH / c.group_size * 2);
+        case NNZ_T_FINAL_NORM: return set(m->final_norm, c.hidden_size * 4);
+        case NNZ_T_LOGITS: return set(m->logits, (size_t)c.vocab_size * 4);
+        case NNZ_T_RESIDUAL: return set(m->residual, c.hidden_size * 4);
+        default: return nnz_fail(ctx, NNZ_EINVAL, "unknown tensor id %d", id);
+        }
+    }
+    NNZ_REQUIRE(ctx, layer < c.num_layers, NNZ_EINVAL, "layer %u out of range", layer);
+    Layer &Ly = m->L[layer];
+    const size_t kv_bytes = (size_t)c.num_kv_heads * c.max_context_length * c.head_dim * 2;
+    auto codes = [&](Proj &p) { return set(p.codes, (size_t)p.M * p.K / 8); };
+    auto scales = [&](Proj &p) { return set(p.scales, (size_t)p.M * p.K / c.group_size * 2); };
+    switch (id) {
+    case NNZ_T_Q_CODES: return codes(Ly.q);
+    case NNZ_T_Q_SCALES: return scales(Ly.q);
+    case NNZ_T_K_CODES: return codes(Ly.k);
+    case NNZ_T_K_SCALES: return scales(Ly.k);
+    case NNZ_T_V_CODES: return codes(Ly.v);
+    case NNZ_T_V_SCALES: return scales(Ly.v);
+    case NNZ_T_O_CODES: return codes(Ly.o);
+    case NNZ_T_O_SCALES: return scales(Ly.o);
+    case NNZ_T_GATE_CODES: return codes(Ly.gate);
+    case NNZ_T_GATE_SCALES: return scales(Ly.gate);
+    case NNZ_T_UP_CODES: return codes(Ly.up);
+    case NNZ_T_UP_SCALES: return scales(Ly.up);
+    case NNZ_T_DOWN_CODES: return codes(Ly.down);
+    case NNZ_T_DOWN_SCALES: return scales(Ly.down);
+    case NNZ_T_ATTN_NORM: return set(Ly.attn_norm, c.hidden_size * 4);
+    case NNZ_T_FFN_NORM: return set(Ly.ffn_norm, c.hidden_size * 4);
+    case NNZ_T_Q_NORM: return set(Ly.q_norm, c.head_dim * 4);
+    case NNZ_T_K_NORM: return set(Ly.k_norm, c.head_dim * 4);
+    case NNZ_T_K_CACHE: return set(Ly.kc, kv_bytes);
+    case NNZ_T_V_CACHE: return set(Ly.vc, kv_bytes);
+    default: return nnz_fail(ctx, NNZ_EINVAL, "unknown tensor id %d", id);
+    }
+}
+
+int nnz_model_forward_decode(nnz_model *m, uint32_t token_id, uint32_t position) {
+    if (!m) return NNZ_EINVAL;
+    nnz_ctx *ctx = m->ctx;
+    NNZ_REQUIRE(ctx, position < m->c.max_context_length, NNZ_EINVAL,
+                "forward_decode: position %u >= max_context_length", position);
+    NNZ_REQUIRE(ctx, token_id < m->c.vocab_size, NNZ_EINVAL, "forward_decode: token id out of range");
+    NNZ_REQUIRE(ctx, !ctx->capturing, NNZ_ESTATE, "forward_decode: use generate() for graphs");
+    const uint32_t st[4] = {token_id, position, position + 1, 0};
+    NNZ_HIP(ctx, hipMemcpyAsync(m->state, st, sizeof(st), hipMemcpyHostToDevice, ctx->stream));
+    NNZ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    uint32_t chunk, nch;
+    decode_plan(m, position + 1, &chunk, &nch);
+    return enqueue_decode_step(m, chunk, nch);
+}
+
+int nnz_model_prefill(nnz_model *m, const uint32_t *tokens_host, uint32_t n, uint32_t start) {
+    if (!m) return NNZ_EINVAL;
+    nnz_ctx *ctx = m->ctx;
+    const nnz_model_config &c = m->c;
+    NNZ_REQUIRE(ctx, tokens_host && n > 0 && n <= c.max_prefill_length, NNZ_EINVAL,
+                "prefill: need 1 <= n <= max_prefill_length");
+    NNZ_REQUIRE(ctx, (uint64_t)start + n <= c.max_context_length, NNZ_EINVAL,
+                "prefill: positions exceed max_context_length");
+    NNZ_REQUIRE(ctx, !ctx->capturing, NNZ_ESTATE, "prefill: not capturable");
+    for (uint32_t i = 0; i < n; ++i)
+        NNZ_REQUIRE(ctx, tokens_host[i] < c.vocab_size, NNZ_EINVAL, "prefill: token id out of range");
+    RC(ensure_prefill_buffers(m, n, start));
+    NNZ_HIP(ctx, hipMemcpyAsync(m->p_ids, tokens_host, (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
+    const uint32_t H = c.hidden_size;
+    if (c.embed_kind == NNZ_EMBED_Q1)
+        embed_ids_q1_kernel<<<ceil_div(n * H, 256), 256, 0, ctx->stream>>>(
+            m->p_ids, (const uint8_t *)m->emb, (const uint16_t *)m->emb_scales, m->p_res, H, n,
+            c.group_size, c.vocab_size);
+    else
+        embed_ids_bf16_kernel<<<ceil_div(n * H, 256), 256, 0, ctx->stream>>>(
+            m->p_ids, (const uint16_t *)m->emb, m->p_res, H, n, c.vocab_size);
+    NNZ_LAUNCHED(ctx);
+    const uint32_t nch = ceil_div(start + n, 512);
+    for (uint32_t l = 0; l < c.num_layers; ++l) {
+        Layer &Ly = m->L[l];
+        RC(nnz_dispatch_rms_norm(ctx, m->p_res, Ly.attn_norm, m->p_xn, NNZ_F16, 0, {H, n, c.rms_eps}));
+        RC(nnz_gemm_launch(ctx, &Ly.q.w, nullptr, m->p_xn, n, m->p_q, NNZ_GEMM_STORE_F16, dims_of(m, Ly.q)));
+        RC(nnz_gemm_launch(ctx, &Ly.k.w, nullptr, m->p_xn, n, m->p_k, NNZ_GEMM_STORE_F16, dims_of(m, Ly.k)));
+        RC(nnz_gemm_launch(ctx, &Ly.v.w, nullptr, m->p_xn, n, m->p_v, NNZ_GEMM_STORE_F16, dims_of(m, Ly.v)));
+        RC(nnz_attn_prep_launch(ctx, m->p_q, m->p_k, m->p_v, Ly.q_norm, Ly.k_norm, m->p_qf, Ly.kc,
+                                Ly.vc, c.num_query_heads, c.num_kv_heads, c.head_dim, start, nullptr,
+                                n, c.max_context_length, c.rms_eps, c.rope_theta));
+        NnzAttnCall ac{};
+        ac.q = m->p_qf;
+        ac.qdt = NNZ_F32;
+        ac.kc = Ly.kc;
+        ac.vc = Ly.vc;
+        ac.kvdt = NNZ_F16;
+        ac.vt = true;
+        ac.out = m->p_att;
+        ac.odt = NNZ_F16;
+        ac.part_o = m->p_part_o;
+        ac.part_ml = m->p_part_ml;
+        ac.chunk = 512;
+        ac.nchunks = nch;
+        ac.nq = n;
+        ac.dims = gqa_dims(m, start + 1);
+        RC(nnz_attn_launch_ex(ctx, ac));
+        RC(nnz_gemm_launch(ctx, &Ly.o.w, nullptr, m->p_att, n, m->p_res, NNZ_GEMM_RESADD, dims_of(m, Ly.o)));
+        RC(nnz_dispatch_rms_norm(ctx, m->p_res, Ly.ffn_norm, m->p_xn, NNZ_F16, 0, {H, n, c.rms_eps}));
+        RC(nnz_gemm_launch(ctx, &Ly.gate.w, &Ly.up.w, m->p_xn, n, m->p_h, NNZ_GEMM_SILU_PAIR,
+                           dims_of(m, Ly.gate)));
+        RC(nnz_gemm_launch(ctx, &Ly.down.w, nullptr, m->p_h, n, m->p_res, NNZ_GEMM_RESADD,
+                           dims_of(m, Ly.down)));
+    }
+    RC(nnz_dispatch_rms_norm(ctx, m->p_res + (size_t)(n - 1) * H, m->final_norm, m->xn, NNZ_F16, 0,
+                             {H, 1, c.rms_eps}));
+    NNZ_HIP(ctx, hipMemcpyAsync(m->residual, m->p_res + (size_t)(n - 1) * H, (size_t)H * 4,
+                                hipMemcpyDeviceToDevice, ctx->stream));
+    return lm_head(m, m->xn, m->logits);
+}
+
+}  // extern "C"
+
+namespace {
+
+// Prefill the prompt (in max_prefill_length batches), take the greedy first
+// token into the state block and pick the attention plan for max_new steps.
+int begin_decode(nnz_model *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t max_new,
+                 uint32_t *chunk, uint32_t *nch) {
+    nnz_ctx *ctx = m->ctx;
+    const nnz_model_config &c = m->c;
+    NNZ_REQUIRE(ctx, prompt && n_prompt > 0 && max_new > 0, NNZ_EINVAL, "decode: bad arguments");
+    NNZ_REQUIRE(ctx, (uint64_t)n_prompt + max_new <= c.max_context_length, NNZ_EINVAL,
+                "decode: prompt + new tokens exceed max_context_length");
+    NNZ_REQUIRE(ctx, max_new + 1 <= m->out_cap, NNZ_EINVAL, "decode: too many tokens");
+    for (uint32_t s = 0; s < n_prompt; s += c.max_prefill_length) {
+        const uint32_t n = n_prompt - s < c.max_prefill_length ? n_prompt - s : c.max_prefill_length;
+        RC(nnz_model_prefill(m, prompt + s, n, s));
+    }
+    // state = (-, n_prompt - 1, n_prompt, 0); the advance kernel stores t0 and
+    // moves to (t0, n_prompt, n_prompt + 1, 1).
+    const uint32_t st[4] = {0, n_prompt - 1, n_prompt, 0};
+    NNZ_HIP(ctx, hipMemcpyAsync(m->state, st, sizeof(st), hipMemcpyHostToDevice, ctx->stream));
+    argmax_advance_kernel<<<1, 1024, 0, ctx->stream>>>(m->logits, c.vocab_size, m->state,
+                                                       m->tokens_out, m->margins_out, m->out_cap);
+    NNZ_LAUNCHED(ctx);
+    decode_plan(m, n_prompt + max_new, chunk, nch);
+    NNZ_REQUIRE(ctx, *nch <= m->part_chunks, NNZ_EINVAL, "decode: attention plan exceeds scratch");
+    return NNZ_OK;
+}
+
+// One greedy decode step: forwardDecode of the state's token, then argmax
+// and state advance.  Graph-capturable (no host data, no allocation).
+int greedy_step(nnz_model *m, uint32_t chunk, uint32_t nch) {
+    RC(enqueue_decode_step(m, chunk, nch));
+    argmax_advance_kernel<<<1, 1024, 0, m->ctx->stream>>>(m->logits, m->c.vocab_size, m->state,
+                                                          m->tokens_out, m->margins_out, m->out_cap);
+    NNZ_LAUNCHED(m->ctx);
+    return NNZ_OK;
+}
+
+int capture_step(nnz_model *m, uint32_t chunk, uint32_t nch, nnz_graph **g) {
+    RC(nnz_graph_begin(m->ctx));
+    const int brc = greedy_step(m, chunk, nch);
+    const int erc = nnz_graph_end(m->ctx, g);
+    return brc ? brc : erc;
+}
+
+}  // namespace
+
+extern "C" {
+
+int nnz_model_generate(nnz_model *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_new,
+                       uint32_t *out_tokens, float *out_margins, float *out_step_ms, int use_graph) {
+    if (!m) return NNZ_EINVAL;
+    nnz_ctx *ctx = m->ctx;
+    NNZ_REQUIRE(ctx, out_tokens, NNZ_EINVAL, "generate: null output");
+    uint32_t chunk, nch;
+    RC(begin_decode(m, prompt, n_prompt, n_new, &chunk, &nch));
+    std::vector<hipEvent_t> ev;
+    int rc = NNZ_OK;
+    if (out_step_ms) {
+        ev.resize(n_new + 1);
+        for (auto &e : ev)
+            if (!rc && hipEventCreate(&e) != hipSuccess) rc = NNZ_EHIP;
+    }
+    // The reference decodes every emitted token (transformer.zig:3982-4016):
+    // n_new forward passes for n_new output tokens.
+    nnz_graph *g = nullptr;
+    if (!rc && use_graph) rc = capture_step(m, chunk, nch, &g);
+    if (!rc && out_step_ms && hipEventRecord(ev[0], ctx->stream) != hipSuccess) rc = NNZ_EHIP;
+    for (uint32_t i = 0; i < n_new && !rc; ++i) {
+        rc = use_graph ? nnz_graph_replay(ctx, g) : greedy_step(m, chunk, nch);
+        if (!rc && out_step_ms && hipEventRecord(ev[i + 1], ctx->stream) != hipSuccess) rc = NNZ_EHIP;
+    }
+    if (!rc) rc = nnz_stream_sync(ctx, 600000);
+    if (!rc && out_step_ms)
+        for (uint32_t i = 0; i < n_new; ++i) hipEventElapsedTime(&out_step_ms[i], ev[i], ev[i + 1]);
+    for (auto &e : ev)
+        if (e) hipEventDestroy(e);
+    if (g) nnz_graph_destroy(g);
+    if (rc) return rc;
+    return nnz_model_decode_read(m, n_new, out_tokens, out_margins);
+}
+
+int nnz_model_decode_begin(nnz_model *m, const uint32_t *prompt, uint32_t n_prompt,
+                           uint32_t max_new) {
+    if (!m) return NNZ_EINVAL;
+    NNZ_REQUIRE(m->ctx, !m->step_graph, NNZ_ESTATE, "decode_begin: a decode stream is active");
+    uint32_t chunk, nch;
+    RC(begin_decode(m, prompt, n_prompt, max_new, &chunk, &nch));
+    RC(capture_step(m, chunk, nch, &m->step_graph));
+    m->stream_steps_left = max_new;
+    return NNZ_OK;
+}
+
+int nnz_model_decode_steps(nnz_model *m, uint32_t n) {
+    if (!m) return NNZ_EINVAL;
+    NNZ_REQUIRE(m->ctx, m->step_graph, NNZ_ESTATE, "decode_steps: call decode_begin first");
+    NNZ_REQUIRE(m->ctx, n <= m->stream_steps_left, NNZ_EINVAL,
+                "decode_steps: %u steps requested, %u left in the plan", n, m->stream_steps_left);
+    for (uint32_t i = 0; i < n; ++i) RC(nnz_graph_replay(m->ctx, m->step_graph));
+    m->stream_steps_left -= n;
+    return NNZ_OK;
+}
+
+int nnz_model_decode_read(nnz_model *m, uint32_t n, uint32_t *out_tokens, float *out_margins) {
+    if (!m) return NNZ_EINVAL;
+    nnz_ctx *ctx = m->ctx;
+    NNZ_REQUIRE(ctx, out_tokens && n <= m->out_cap, NNZ_EINVAL, "decode_read: bad arguments");
+    RC(nnz_stream_sync(ctx, 600000));
+    NNZ_HIP(ctx, hipMemcpy(out_tokens, m->tokens_out, (size_t)n * 4, hipMemcpyDeviceToHost));
+    if (out_margins)
+        NNZ_HIP(ctx, hipMemcpy(out_margins, m->margins_out, (size_t)n * 4, hipMemcpyDeviceToHost));
+    return NNZ_OK;
+}
+
+int nnz_model_decode_end(nnz_model *m) {
+    if (!m) return NNZ_EINVAL;
+    if (m->step_graph) {
+        RC(nnz_stream_sync(m->ctx, 600000));
+        nnz_graph_destroy(m->step_graph);
+        m->step_graph = nullptr;
+    }
+    m->stream_steps_left = 0;
+    return NNZ_OK;
+}
+
+}  // extern "C"

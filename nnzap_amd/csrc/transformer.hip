@@ -1,0 +1,956 @@
+// Transformer kernels for the decode path on gfx950: RMSNorm, SiLU, RoPE,
+// KV-cache append, GQA decode attention, embedding gathers, residual add,
+// on-device argmax and the dequantisation artefact.
+//
+// Semantics follow nnmetal/src/shaders/transformer.metal; the decomposition
+// does not.  In particular decode attention splits the sequence across
+// workgroups (flash-decoding partials + a combine kernel) instead of the
+// reference's one-threadgroup-per-query-head kernels, so a 32k context keeps
+// every CU busy.
+#include "internal.h"
+
+#include <math.h>
+
+namespace {
+
+// theta^(-2p/d), evaluated in double and rounded once to float.
+__device__ __forceinline__ float rope_inv_freq(int pair, int head_dim, float theta) {
+    return (float)exp2(-(2.0 * (double)pair / (double)head_dim) * log2((double)theta));
+}
+
+// Rotate element d of a head given its partner (d^1); consecutive-pair RoPE
+// (transformer.metal:154-202).
+__device__ __forceinline__ float rope_rotate(float self, float partner, int d, uint32_t position,
+                                             int head_dim, float theta) {
+    const float ang = (float)position * rope_inv_freq(d >> 1, head_dim, theta);
+    float s, c;
+    sincosf(ang, &s, &c);
+    return (d & 1) ? fmaf(partner, s, self * c) : fmaf(self, c, -partner * s);
+}
+
+__device__ __forceinline__ float block_sum_256(float v, float *red) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) t += red[i];
+    return t;
+}
+
+__device__ __forceinline__ float block_max_256(float v, float *red) {
+    v = wave_max(v);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float t = -INFINITY;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) t = fmaxf(t, red[i]);
+    return t;
+}
+
+// ---------------------------------------------------------------- RMSNorm --
+// transformer.metal:49-104 (rms_norm), :551-608 (rms_norm_f16out),
+// :610-677 (rms_norm_bf16_f16out).  One 256-thread block per row.
+template <int ODT, bool TRUNC>
+__global__ __launch_bounds__(256) void rms_norm_kernel(const float *in, const float *scale,
+                                                       void *out, uint32_t n, float eps) {
+    __shared__ float red[4];
+    const float *x = in + (size_t)blockIdx.x * n;
+    float ss = 0.f;
+    for (uint32_t i = threadIdx.x; i < n; i += 256) ss += x[i] * x[i];
+    ss = block_sum_256(ss, red);
+    const float rms = rsqrtf(ss / (float)n + eps);
+    for (uint32_t i = threadIdx.x; i < n; i += 256) {
+        float v = x[i] * rms * scale[i];
+        if constexpr (TRUNC) v = bf16_trunc(v);
+        store_from_f32<ODT>(out, (size_t)blockIdx.x * n + i, v);
+    }
+}
+
+// ------------------------------------------------------------------- SiLU --
+__global__ void silu_kernel(const float *in, float *out, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) { const float x = in[i]; out[i] = x / (1.f + expf(-x)); }
+}
+
+template <int DT>
+__global__ void silu_mul_kernel(const void *gate, const void *up, void *out, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) {
+        const float g = load_as_f32<DT>(gate, i);
+        store_from_f32<DT>(out, i, g / (1.f + expf(-g)) * load_as_f32<DT>(up, i));
+    }
+}
+
+// ------------------------------------------------------------------- RoPE --
+// One thread per (head, pair), in place.
+template <int DT>
+__global__ void rope_kernel(void *data, uint32_t heads, uint32_t head_dim, uint32_t position,
+                            float theta) {
+    const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
+    const uint32_t half = head_dim / 2;
+    if (gid >= heads * half) return;
+    const uint32_t h = gid / half, p = gid % half;
+    const size_t base = (size_t)h * head_dim + 2 * p;
+    const float a = load_as_f32<DT>(data, base), b = load_as_f32<DT>(data, base + 1);
+    const float ang = (float)position * rope_inv_freq((int)p, (int)head_dim, theta);
+    float s, c;
+    sincosf(ang, &s, &c);
+    store_from_f32<DT>(data, base, fmaf(a, c, -b * s));
+    store_from_f32<DT>(data, base + 1, fmaf(b, c, a * s));
+}
+
+// ------------------------------------------------------------ KV append ----
+// transformer.metal:204-257: K[h][pos][d], V[h][d][pos].
+template <int PDT, int CDT>
+__global__ void kv_update_kernel(const void *kp, const void *vp, void *kc, void *vc,
+                                 uint32_t heads, uint32_t head_dim, uint32_t pos, uint32_t max_ctx) {
+    const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= heads * head_dim) return;
+    const uint32_t h = gid / head_dim, d = gid % head_dim;
+    const size_t stride = (size_t)max_ctx * head_dim;
+    store_from_f32<CDT>(kc, h * stride + (size_t)pos * head_dim + d, load_as_f32<PDT>(kp, gid));
+    store_from_f32<CDT>(vc, h * stride + (size_t)d * max_ctx + pos, load_as_f32<PDT>(vp, gid));
+}
+
+// Per-head RMSNorm (+ optional scale) and RoPE of one head held by a block of
+// head_dim threads (<= 256).  Returns this thread's rotated element.
+__device__ __forceinline__ float head_norm_rope(float v, const float *scale, uint32_t head_dim,
+                                                uint32_t pos, float eps, float theta,
+                                                bool do_norm, float *red) {
+    const int d = threadIdx.x;
+    if (do_norm) {
+        const float ss = block_sum_256(d < (int)head_dim ? v * v : 0.f, red);
+        const float rms = rsqrtf(ss / (float)head_dim + eps);
+        v = v * rms * (d < (int)head_dim ? scale[d] : 0.f);
+    }
+    const float partner = __shfl_xor(v, 1, 64);
+    return rope_rotate(v, partner, d, pos, (int)head_dim, theta);
+}
+
+// transformer.metal:1032-1113 fused_rope_k_kv_cache_update_f16: grid = kv heads.
+__global__ __launch_bounds__(256) void fused_rope_kv_kernel(const f16_t *kp, const f16_t *vp,
+                                                            f16_t *kc, f16_t *vc, uint32_t head_dim,
+                                                            uint32_t pos, uint32_t max_ctx,
+                                                            float theta) {
+    __shared__ float red[4];
+    const uint32_t h = blockIdx.x, d = threadIdx.x;
+    const float k = d < head_dim ? (float)kp[h * head_dim + d] : 0.f;
+    const float kr = head_norm_rope(k, nullptr, head_dim, pos, 0.f, theta, false, red);
+    if (d < head_dim) {
+        const size_t stride = (size_t)max_ctx * head_dim;
+        kc[h * stride + (size_t)pos * head_dim + d] = (f16_t)kr;
+        vc[h * stride + (size_t)d * max_ctx + pos] = vp[h * head_dim + d];
+    }
+}
+
+// transformer.metal:817-912 fused_norm_rope_f16: per-head RMSNorm + RoPE in place.
+__global__ __launch_bounds__(256) void fused_norm_rope_kernel(f16_t *data, const float *scale,
+                                                              uint32_t head_dim, uint32_t pos,
+                                                              float eps, float theta) {
+    __shared__ float red[4];
+    const uint32_t h = blockIdx.x, d = threadIdx.x;
+    const float v = d < head_dim ? (float)data[h * head_dim + d] : 0.f;
+    const float r = head_norm_rope(v, scale, head_dim, pos, eps, theta, true, red);
+    if (d < head_dim) data[h * head_dim + d] = (f16_t)r;
+}
+
+// transformer.metal:914-1030 fused_k_norm_rope_kv_cache_f16.
+__global__ __launch_bounds__(256) void fused_k_norm_rope_kv_kernel(
+    const f16_t *kp, const f16_t *vp, f16_t *kc, f16_t *vc, const float *kscale,
+    uint32_t head_dim, uint32_t pos, uint32_t max_ctx, float eps, float theta) {
+    __shared__ float red[4];
+    const uint32_t h = blockIdx.x, d = threadIdx.x;
+    const float k = d < head_dim ? (float)kp[h * head_dim + d] : 0.f;
+    const float kr = head_norm_rope(k, kscale, head_dim, pos, eps, theta, true, red);
+    if (d < head_dim) {
+        const size_t stride = (size_t)max_ctx * head_dim;
+        kc[h * stride + (size_t)pos * head_dim + d] = (f16_t)kr;
+        vc[h * stride + (size_t)d * max_ctx + pos] = vp[h * head_dim + d];
+    }
+}
+
+// Attention prologue of the fused decode kernel (transformer.metal:1506-1589):
+// blocks [0, Hq) normalise+rotate a query head into f32 `qout`; blocks
+// [Hq, Hq+Hkv) normalise+rotate a key head into the cache at `pos` and copy V.
+// Each KV entry is written by exactly one block.
+__global__ __launch_bounds__(256) void attn_prep_kernel(
+    const f16_t *q, const f16_t *kr, const f16_t *vr, const float *qn, const float *kn,
+    float *qout, f16_t *kc, f16_t *vc, uint32_t hq, uint32_t hkv, uint32_t head_dim, uint32_t pos0,
+    const uint32_t *d_pos, uint32_t max_ctx, float eps, float theta) {
+    __shared__ float red[4];
+    const uint32_t b = blockIdx.x, d = threadIdx.x, z = blockIdx.y;
+    const uint32_t pos = (d_pos ? *d_pos : pos0) + z;
+    q += (size_t)z * hq * head_dim;
+    qout += (size_t)z * hq * head_dim;
+    kr += (size_t)z * hkv * head_dim;
+    vr += (size_t)z * hkv * head_dim;
+    if (b < hq) {
+        const float v = d < head_dim ? (float)q[b * head_dim + d] : 0.f;
+        const float r = head_norm_rope(v, qn, head_dim, pos, eps, theta, true, red);
+        if (d < head_dim) qout[b * head_dim + d] = r;
+    } else {
+        const uint32_t h = b - hq;
+        const float v = d < head_dim ? (float)kr[h * head_dim + d] : 0.f;
+        const float r = head_norm_rope(v, kn, head_dim, pos, eps, theta, true, red);
+        if (d < head_dim) {
+            const size_t stride = (size_t)max_ctx * head_dim;
+            kc[h * stride + (size_t)pos * head_dim + d] = (f16_t)r;
+            vc[h * stride + (size_t)d * max_ctx + pos] = vr[h * head_dim + d];
+        }
+    }
+}
+
+// ------------------------------------------------------ decode attention ---
+// Split-sequence GQA decode.  Grid (num_chunks, Hkv); block 256 threads.
+// Each block serves the G query heads of one KV head over one chunk of
+// `chunk` tokens: scores -> chunk max / exp-sum -> unnormalised P.V partial.
+// If the whole sequence is one chunk the block writes the final output.
+struct AttnArgs {
+    const void *q;        // [Hq][D] in qdt (already normed/roped unless rope_pos >= 0)
+    const void *kc;       // [Hkv][max_ctx][D]
+    const void *vc;       // [Hkv][D][max_ctx] (VT) or [Hkv][max_ctx][D]
+    void *out;            // [Hq][D] in odt (single-chunk case)
+    float *part_o;        // [Z][Hq][nchunks][D]
+    float *part_ml;       // [Z][Hq][nchunks][2]
+    const uint32_t *d_seq;  // if set, seq_len of query 0 is read from device memory
+    uint32_t seq_len;     // tokens visible to query 0; query z sees seq_len + z (causal)
+    uint32_t max_ctx, chunk, nchunks, hq;
+    uint32_t q_stride, o_stride;  // elements between consecutive queries
+    int32_t rope_pos;
+    int qdt, odt;
+    float rope_theta, scale;
+};
+
+constexpr int ATT_MAX_CHUNK = 512;
+
+__device__ __forceinline__ float load_dt(const void *p, size_t i, int dt) {
+    if (dt == NNZ_F32) return ((const float *)p)[i];
+    if (dt == NNZ_F16) return (float)((const f16_t *)p)[i];
+    return bf16_to_f32(((const uint16_t *)p)[i]);
+}
+
+__device__ __forceinline__ void store_dt(void *p, size_t i, float v, int dt) {
+    if (dt == NNZ_F32) ((float *)p)[i] = v;
+    else if (dt == NNZ_F16) ((f16_t *)p)[i] = (f16_t)v;
+    else ((uint16_t *)p)[i] = f32_to_bf16_rne(v);
+}
+
+template <int KVDT>
+__device__ __forceinline__ void unpack2(uint32_t w, float &lo, float &hi) {
+    if constexpr (KVDT == NNZ_F16) {
+        lo = (float)__builtin_bit_cast(f16_t, (uint16_t)(w & 0xFFFFu));
+        hi = (float)__builtin_bit_cast(f16_t, (uint16_t)(w >> 16));
+    } else {
+        lo = bf16_to_f32((uint16_t)(w & 0xFFFFu));
+        hi = bf16_to_f32((uint16_t)(w >> 16));
+    }
+}
+
+template <int D, int G, int KVDT, bool VT>
+__global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
+    constexpr int NQ = (G * D + 255) / 256;   // q elements per thread
+    __shared__ float qs[G][D];
+    __shared__ float ps[G][ATT_MAX_CHUNK];
+    __shared__ float red[4];
+    __shared__ float ored[4][G][D];
+
+    const int tid = threadIdx.x;
+    const uint32_t c = blockIdx.x, h = blockIdx.y, z = blockIdx.z;
+    const uint32_t seq = (a.d_seq ? *a.d_seq : a.seq_len) + z;
+    const uint32_t t0 = c * a.chunk;
+    if (t0 >= seq) return;  // the combine step only reads chunks < ceil(seq/chunk)
+    const uint32_t len = min(a.chunk, seq - t0);
+
+    // q of the G heads that share this KV head; optional RoPE (config 4).
+    float qv[NQ];
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+        const int i = tid + 256 * k;
+        qv[k] = (i < G * D) ? load_dt(a.q, (size_t)z * a.q_stride + (size_t)h * G * D + i, a.qdt) : 0.f;
+    }
+    if (a.rope_pos >= 0) {
+#pragma unroll
+        for (int k = 0; k < NQ; ++k) {
+            const int i = tid + 256 * k;
+            const float partner = __shfl_xor(qv[k], 1, 64);
+            qv[k] = rope_rotate(qv[k], partner, i % D, (uint32_t)a.rope_pos, D, a.rope_theta);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+        const int i = tid + 256 * k;
+        if (i < G * D) qs[i / D][i % D] = qv[k];
+    }
+    __syncthreads();
+
+    // Scores: one thread per token; each streams its K row with 16-byte loads.
+    const size_t kv_stride = (size_t)a.max_ctx * D;
+    const uint16_t *kb = (const uint16_t *)a.kc + h * kv_stride;
+    for (uint32_t t = tid; t < len; t += 256) {
+        float dot[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) dot[g] = 0.f;
+        const uint4 *kr = (const uint4 *)(kb + (size_t)(t0 + t) * D);
+#pragma unroll 4
+        for (int v = 0; v < D / 8; ++v) {
+            const uint4 w = kr[v];
+            const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float k0, k1;
+                unpack2<KVDT>(wv[e], k0, k1);
+                const int d = v * 8 + 2 * e;
+#pragma unroll
+                for (int g = 0; g < G; ++g) dot[g] = fmaf(qs[g][d + 1], k1, fmaf(qs[g][d], k0, dot[g]));
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) ps[g][t] = dot[g] * a.scale;
+    }
+    __syncthreads();
+
+    // Chunk max and exp-sum per head; P overwrites the scores.
+    float mval[G], lval[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float m = -INFINITY;
+        for (uint32_t t = tid; t < len; t += 256) m = fmaxf(m, ps[g][t]);
+        m = block_max_256(m, red);
+        float l = 0.f;
+        for (uint32_t t = tid; t < len; t += 256) {
+            const float e = expf(ps[g][t] - m);
+            ps[g][t] = e;
+            l += e;
+        }
+        l = block_sum_256(l, red);
+        mval[g] = m;
+        lval[g] = l;
+    }
+    __syncthreads();
+
+    const uint16_t *vb = (const uint16_t *)a.vc + h * kv_stride;
+    float o[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
+    int part;  // which of the 4 partial slots this thread contributes to
+    if constexpr (!VT) {
+        // V is [t][D]: 16 lanes cover one 256-byte row, 16 token groups.
+        constexpr int DP = D / 8, TG = 256 / DP;
+        const int dp = tid % DP, tg = tid / DP;
+        for (uint32_t t = tg; t < len; t += TG) {
+            const uint4 w = *(const uint4 *)(vb + (size_t)(t0 + t) * D + dp * 8);
+            const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float v0, v1;
+                unpack2<KVDT>(wv[e], v0, v1);
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    const float p = ps[g][t];
+                    o[g][2 * e] = fmaf(p, v0, o[g][2 * e]);
+                    o[g][2 * e + 1] = fmaf(p, v1, o[g][2 * e + 1]);
+                }
+            }
+        }
+        // Fold the token groups inside the wave (lanes that differ in tg).
+#pragma unroll
+        for (int off = DP; off < 64; off <<= 1)
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[g][e] += __shfl_xor(o[g][e], off, 64);
+        part = tid >> 6;
+        if ((tid & 63) < DP) {
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ored[part][g][dp * 8 + e] = o[g][e];
+        }
+    } else {
+        // V is [D][max_ctx]: a thread owns one d and streams 8 tokens per
+        // 16-byte load over its share of the chunk.
+        constexpr int PARTS = 256 / D;
+        const int d = tid % D;
+        part = tid / D;
+        const uint32_t ngroups = len / 8;
+        const uint32_t per = ceil_div(ngroups, PARTS);
+        const uint32_t k0 = part * per, k1 = min(ngroups, k0 + per);
+        const uint16_t *row = vb + (size_t)d * a.max_ctx + t0;
+        for (uint32_t k = k0; k < k1; ++k) {
+            const uint4 w = *(const uint4 *)(row + 8 * k);
+            const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float v0, v1;
+                unpack2<KVDT>(wv[e], v0, v1);
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+                    o[g][0] = fmaf(ps[g][8 * k + 2 * e + 1], v1, fmaf(ps[g][8 * k + 2 * e], v0, o[g][0]));
+            }
+        }
+        if (part == PARTS - 1) {  // ragged tail of the chunk
+            for (uint32_t t = ngroups * 8; t < len; ++t) {
+                float v;
+                if constexpr (KVDT == NNZ_F16) v = (float)__builtin_bit_cast(f16_t, row[t]);
+                else v = bf16_to_f32(row[t]);
+#pragma unroll
+                for (int g = 0; g < G; ++g) o[g][0] = fmaf(ps[g][t], v, o[g][0]);
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) ored[part][g][d] = o[g][0];
+    }
+    __syncthreads();
+
+    constexpr int NPART = VT ? 256 / D : 4;
+    for (int i = tid; i < G * D; i += 256) {
+        const int g = i / D, d = i % D;
+        float s = 0.f;
+#pragma unroll
+        for (int p = 0; p < NPART; ++p) s += ored[p][g][d];
+        const uint32_t qh = h * G + g;
+        if (a.nchunks == 1) {
+            store_dt(a.out, (size_t)z * a.o_stride + (size_t)qh * D + d, s / lval[g], a.odt);
+        } else {
+            const size_t slot = ((size_t)z * a.hq + qh) * a.nchunks + c;
+            a.part_o[slot * D + d] = s;
+            if (d == 0) {
+                a.part_ml[slot * 2 + 0] = mval[g];
+                a.part_ml[slot * 2 + 1] = lval[g];
+            }
+        }
+    }
+}
+
+// Combine the per-chunk partials of one query head (grid = (Hq, Z), block = D).
+__global__ __launch_bounds__(128) void attn_combine_kernel(AttnArgs a, uint32_t D) {
+    const uint32_t qh = blockIdx.x, z = blockIdx.y, d = threadIdx.x;
+    if (d >= D) return;
+    const uint32_t seq = (a.d_seq ? *a.d_seq : a.seq_len) + z;
+    const uint32_t nch = min(a.nchunks, ceil_div(seq, a.chunk));
+    const size_t base = ((size_t)z * a.hq + qh) * a.nchunks;
+    const float *ml = a.part_ml + base * 2;
+    float M = -INFINITY;
+    for (uint32_t c = 0; c < nch; ++c) M = fmaxf(M, ml[2 * c]);
+    float num = 0.f, den = 0.f;
+    for (uint32_t c = 0; c < nch; ++c) {
+        const float w = expf(ml[2 * c] - M);
+        den = fmaf(w, ml[2 * c + 1], den);
+        num = fmaf(w, a.part_o[(base + c) * D + d], num);
+    }
+    store_dt(a.out, (size_t)z * a.o_stride + (size_t)qh * D + d, num / den, a.odt);
+}
+
+// -------------------------------------------------------------- embedding --
+// transformer.metal:428-481: flat bit index row*hidden + d, group flat/gs.
+__global__ void embed_q1_kernel(const uint32_t *ids, const uint8_t *bits, const uint16_t *scales,
+                                float *out, uint32_t hidden, uint32_t ntok, uint32_t gs,
+                                uint32_t vocab) {
+    const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= ntok * hidden) return;
+    const uint32_t t = gid / hidden, d = gid % hidden;
+    uint32_t row = ids[t];
+    if (row >= vocab) row = vocab - 1;  // the host validates ids; never read out of bounds
+    const uint64_t flat = (uint64_t)row * hidden + d;
+    const bool bit = (bits[flat >> 3] >> (flat & 7)) & 1;
+    const float s = (float)__builtin_bit_cast(f16_t, scales[flat / gs]);
+    out[gid] = bit ? s : -s;
+}
+
+// transformer.metal:505-549 embedding_lookup_q4 (BF16 scales/biases, output
+// BF16-truncated).
+__global__ void embed_q4_kernel(const uint32_t *ids, const uint32_t *words, const uint16_t *scales,
+                                const uint16_t *biases, float *out, uint32_t hidden, uint32_t ntok,
+                                uint32_t gs, uint32_t vocab) {
+    const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= ntok * hidden) return;
+    const uint32_t t = gid / hidden, d = gid % hidden;
+    uint32_t row = ids[t];
+    if (row >= vocab) row = vocab - 1;
+    const uint64_t flat = (uint64_t)row * hidden + d;
+    const uint32_t n = (words[flat >> 3] >> ((flat & 7) * 4)) & 0xFu;
+    const uint64_t g = flat / gs;
+    out[gid] = bf16_trunc(bf16_to_f32(scales[g]) * (float)n + bf16_to_f32(biases[g]));
+}
+
+__global__ void embed_bf16_kernel(const uint32_t *ids, const uint16_t *table, float *out,
+                                  uint32_t hidden, uint32_t ntok, uint32_t vocab) {
+    const uint32_t gid = blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= ntok * hidden) return;
+    const uint32_t t = gid / hidden, d = gid % hidden;
+    uint32_t row = ids[t];
+    if (row >= vocab) row = vocab - 1;
+    out[gid] = bf16_to_f32(table[(size_t)row * hidden + d]);
+}
+
+__global__ void residual_add_kernel(float *r, const float *a, uint32_t n) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) r[i] += a[i];
+}
+
+// ----------------------------------------------------------------- argmax --
+// First maximum wins (transformer.zig:3694-3707); NaN never wins.  One block
+// of 1024 threads; also reports the runner-up value for margin logging.
+__global__ __launch_bounds__(1024) void argmax_kernel(const float *x, uint32_t n, uint32_t *oi,
+                                                      float *ov) {
+    __shared__ float sv[1024], sv2[1024];
+    __shared__ uint32_t si[1024];
+    float best = -INFINITY, second = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    for (uint32_t i = threadIdx.x; i < n; i += 1024) {
+        const float v = x[i];
+        if (v > best) { second = best; best = v; bi = i; }
+        else if (v > second) second = v;
+    }
+    sv[threadIdx.x] = best; sv2[threadIdx.x] = second; si[threadIdx.x] = bi;
+    __syncthreads();
+    for (uint32_t s = 512; s > 0; s >>= 1) {
+        if (threadIdx.x < s) {
+            const float a = sv[threadIdx.x], b = sv[threadIdx.x + s];
+            const uint32_t ia = si[threadIdx.x], ib = si[threadIdx.x + s];
+            const bool take_b = (b > a) || (b == a && ib < ia);
+            const float lo = take_b ? a : b;
+            const float s2 = fmaxf(fmaxf(sv2[threadIdx.x], sv2[threadIdx.x + s]), lo);
+            sv[threadIdx.x] = take_b ? b : a;
+            si[threadIdx.x] = take_b ? ib : ia;
+            sv2[threadIdx.x] = s2;
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        oi[0] = si[0] == 0xFFFFFFFFu ? 0u : si[0];
+        if (ov) { ov[0] = sv[0]; ov[1] = sv2[0]; }
+    }
+}
+
+// ---------------------------------------------------------------- dequant --
+__global__ void dequant_kernel(const uint32_t *codes, const uint16_t *scales, const uint16_t *biases,
+                               float *out, uint32_t M, uint32_t K, uint32_t gs, int bits, int sdt) {
+    const uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (uint64_t)M * K) return;
+    const uint64_t r = gid / K, c = gid % K;
+    const uint64_t g = r * (K / gs) + c / gs;
+    if (bits == 1) {
+        const uint32_t w = codes[r * (K / 32) + c / 32];
+        const float s = (float)__builtin_bit_cast(f16_t, scales[g]);
+        out[gid] = ((w >> (c & 31)) & 1) ? s : -s;
+    } else {
+        const uint32_t w = codes[r * (K / 8) + c / 8];
+        const float n = (float)((w >> ((c & 7) * 4)) & 0xFu);
+        out[gid] = fmaf(scale_to_f32(scales[g], sdt), n, scale_to_f32(biases[g], sdt));
+    }
+}
+
+inline uint32_t grid1d(uint64_t n, uint32_t block) { return (uint32_t)((n + block - 1) / block); }
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Attention host helpers shared with the model code.
+// ---------------------------------------------------------------------------
+
+// Choose the chunk length: small enough to give >= ~2 blocks per CU at long
+// context, >= 64 tokens, a multiple of 8, and <= ATT_MAX_CHUNK.
+uint32_t nnz_attn_chunk(uint32_t seq_len, uint32_t hkv) {
+    const uint32_t want_blocks = 512;
+    const uint32_t per = ceil_div(seq_len * hkv, want_blocks);
+    uint32_t chunk = 64;
+    while (chunk < per && chunk < (uint32_t)ATT_MAX_CHUNK) chunk <<= 1;
+    return chunk;
+}
+
+size_t nnz_attn_scratch_bytes_impl(uint32_t hq, uint32_t head_dim, uint32_t seq_len,
+                                   uint32_t hkv) {
+    const uint32_t chunk = nnz_attn_chunk(seq_len, hkv);
+    const uint32_t nch = ceil_div(seq_len, chunk);
+    // partial outputs + (m, l) pairs + one f32 q buffer for the fused path
+    return ((size_t)hq * nch * head_dim + (size_t)hq * nch * 2 + (size_t)hq * head_dim) * 4 + 256;
+}
+
+template <int D, int G, int KVDT, bool VT>
+static int launch_attn_t(nnz_ctx *ctx, const AttnArgs &a, uint32_t hkv, uint32_t nq) {
+    dim3 grid(a.nchunks, hkv, nq);
+    attn_split_kernel<D, G, KVDT, VT><<<grid, 256, 0, ctx->stream>>>(a);
+    NNZ_LAUNCHED(ctx);
+    if (a.nchunks > 1) {
+        attn_combine_kernel<<<dim3(a.hq, nq), 128, 0, ctx->stream>>>(a, D);
+        NNZ_LAUNCHED(ctx);
+    }
+    return NNZ_OK;
+}
+
+template <int D, int G>
+static int launch_attn_g(nnz_ctx *ctx, const AttnArgs &a, uint32_t hkv, uint32_t nq, int kvdt, bool vt) {
+    if (kvdt == NNZ_F16)
+        return vt ? launch_attn_t<D, G, NNZ_F16, true>(ctx, a, hkv, nq)
+                  : launch_attn_t<D, G, NNZ_F16, false>(ctx, a, hkv, nq);
+    return vt ? launch_attn_t<D, G, NNZ_BF16, true>(ctx, a, hkv, nq)
+              : launch_attn_t<D, G, NNZ_BF16, false>(ctx, a, hkv, nq);
+}
+
+template <int D>
+static int launch_attn_d(nnz_ctx *ctx, const AttnArgs &a, uint32_t hkv, uint32_t nq, uint32_t g, int kvdt,
+                         bool vt) {
+    switch (g) {
+    case 1: return launch_attn_g<D, 1>(ctx, a, hkv, nq, kvdt, vt);
+    case 2: return launch_attn_g<D, 2>(ctx, a, hkv, nq, kvdt, vt);
+    case 4: return launch_attn_g<D, 4>(ctx, a, hkv, nq, kvdt, vt);
+    default: return launch_attn_g<D, 8>(ctx, a, hkv, nq, kvdt, vt);
+    }
+}
+
+// Full-control attention launch used by the public entry points and by the
+// decoder (prefill: nq causal queries; decode graph: seq_len read from d_seq).
+int nnz_attn_launch_ex(nnz_ctx *ctx, const NnzAttnCall &c) {
+    const nnz_gqa_dims &d = c.dims;
+    NNZ_REQUIRE(ctx, c.q && c.kc && c.vc && c.out && c.part_o && c.part_ml, NNZ_EINVAL,
+                "gqa: null buffer");
+    NNZ_REQUIRE(ctx, d.num_query_heads > 0 && d.num_kv_heads > 0 && (d.seq_len > 0 || c.d_seq),
+                NNZ_EINVAL, "gqa: zero dims");
+    NNZ_REQUIRE(ctx, d.num_query_heads % d.num_kv_heads == 0 &&
+                         d.heads_per_kv_group == d.num_query_heads / d.num_kv_heads,
+                NNZ_EINVAL, "gqa: heads_per_kv_group mismatch");
+    NNZ_REQUIRE(ctx, d.heads_per_kv_group == 1 || d.heads_per_kv_group == 2 ||
+                         d.heads_per_kv_group == 4 || d.heads_per_kv_group == 8,
+                NNZ_EUNSUPPORTED, "gqa: heads_per_kv_group %u (supported: 1, 2, 4, 8)",
+                d.heads_per_kv_group);
+    NNZ_REQUIRE(ctx, d.head_dim == 64 || d.head_dim == 128, NNZ_EUNSUPPORTED,
+                "gqa: head_dim %u (supported: 64, 128)", d.head_dim);
+    NNZ_REQUIRE(ctx, d.max_context_length % 8 == 0, NNZ_EUNSUPPORTED,
+                "gqa: max_context_length must be a multiple of 8");
+    NNZ_REQUIRE(ctx, nnz_dtype_ok(c.qdt) && nnz_dtype_ok(c.odt) &&
+                         (c.kvdt == NNZ_F16 || c.kvdt == NNZ_BF16),
+                NNZ_EINVAL, "gqa: bad dtype");
+    NNZ_REQUIRE(ctx, ((uintptr_t)c.kc & 15) == 0 && ((uintptr_t)c.vc & 15) == 0, NNZ_EINVAL,
+                "gqa: caches must be 16-byte aligned");
+    NNZ_REQUIRE(ctx, c.chunk >= 8 && c.chunk % 8 == 0 && c.chunk <= (uint32_t)ATT_MAX_CHUNK &&
+                         c.nchunks >= 1 && c.nq >= 1,
+                NNZ_EINVAL, "gqa: bad chunking");
+    NNZ_REQUIRE(ctx, c.d_seq || ((uint64_t)d.seq_len + c.nq - 1 <= d.max_context_length &&
+                                 (uint64_t)d.seq_len + c.nq - 1 <= (uint64_t)c.chunk * c.nchunks),
+                NNZ_EINVAL, "gqa: sequence exceeds max_context_length or the chunk plan");
+    AttnArgs a{};
+    a.q = c.q;
+    a.kc = c.kc;
+    a.vc = c.vc;
+    a.out = c.out;
+    a.part_o = c.part_o;
+    a.part_ml = c.part_ml;
+    a.d_seq = c.d_seq;
+    a.seq_len = d.seq_len;
+    a.max_ctx = d.max_context_length;
+    a.chunk = c.chunk;
+    a.nchunks = c.nchunks;
+    a.hq = d.num_query_heads;
+    a.q_stride = c.q_stride ? c.q_stride : d.num_query_heads * d.head_dim;
+    a.o_stride = c.o_stride ? c.o_stride : d.num_query_heads * d.head_dim;
+    a.qdt = c.qdt;
+    a.odt = c.odt;
+    a.rope_pos = c.rope_pos;
+    a.rope_theta = c.rope_theta;
+    a.scale = 1.0f / sqrtf((float)d.head_dim);
+    if (d.head_dim == 128)
+        return launch_attn_d<128>(ctx, a, d.num_kv_heads, c.nq, d.heads_per_kv_group, c.kvdt, c.vt);
+    return launch_attn_d<64>(ctx, a, d.num_kv_heads, c.nq, d.heads_per_kv_group, c.kvdt, c.vt);
+}
+
+// Single-query launch with the partials carved out of a caller scratch buffer.
+int nnz_attn_launch(nnz_ctx *ctx, const void *q, int qdt, const void *kc, const void *vc, int kvdt,
+                    bool vt, void *out, int odt, void *scratch, size_t scratch_bytes,
+                    int32_t rope_pos, float theta, const nnz_gqa_dims &d) {
+    NNZ_REQUIRE(ctx, d.num_kv_heads > 0 && d.seq_len > 0 && d.seq_len <= d.max_context_length,
+                NNZ_EINVAL, "gqa: bad seq_len/num_kv_heads");
+    const size_t need = nnz_attn_scratch_bytes_impl(d.num_query_heads, d.head_dim, d.seq_len,
+                                                    d.num_kv_heads);
+    NNZ_REQUIRE(ctx, scratch && scratch_bytes >= need, NNZ_EINVAL,
+                "gqa: scratch of %zu bytes needed, %zu given", need, scratch_bytes);
+    NnzAttnCall c{};
+    c.q = q;
+    c.qdt = qdt;
+    c.kc = kc;
+    c.vc = vc;
+    c.kvdt = kvdt;
+    c.vt = vt;
+    c.out = out;
+    c.odt = odt;
+    c.chunk = nnz_attn_chunk(d.seq_len, d.num_kv_heads);
+    c.nchunks = ceil_div(d.seq_len, c.chunk);
+    float *base = (float *)(((uintptr_t)scratch + 255) & ~(uintptr_t)255);
+    c.part_o = base;
+    c.part_ml = base + (size_t)d.num_query_heads * c.nchunks * d.head_dim;
+    c.nq = 1;
+    c.rope_pos = rope_pos;
+    c.rope_theta = theta;
+    c.dims = d;
+    return nnz_attn_launch_ex(ctx, c);
+}
+
+// q buffer (f32) inside the attention scratch, used by the fused path.
+float *nnz_attn_scratch_q(void *scratch, const nnz_gqa_dims &d) {
+    const uint32_t chunk = nnz_attn_chunk(d.seq_len, d.num_kv_heads);
+    const uint32_t nch = ceil_div(d.seq_len, chunk);
+    float *base = (float *)(((uintptr_t)scratch + 255) & ~(uintptr_t)255);
+    return base + (size_t)d.num_query_heads * nch * d.head_dim + (size_t)d.num_query_heads * nch * 2;
+}
+
+// Batched attention prologue: nq tokens at positions (d_pos ? *d_pos : pos) + z.
+int nnz_attn_prep_launch(nnz_ctx *ctx, const void *q, const void *kr, const void *vr,
+                         const float *qn, const float *kn, float *qout, void *kc, void *vc,
+                         uint32_t hq, uint32_t hkv, uint32_t head_dim, uint32_t pos,
+                         const uint32_t *d_pos, uint32_t nq, uint32_t max_ctx, float eps,
+                         float theta) {
+    attn_prep_kernel<<<dim3(hq + hkv, nq), 256, 0, ctx->stream>>>(
+        (const f16_t *)q, (const f16_t *)kr, (const f16_t *)vr, qn, kn, qout, (f16_t *)kc,
+        (f16_t *)vc, hq, hkv, head_dim, pos, d_pos, max_ctx, eps, theta);
+    NNZ_LAUNCHED(ctx);
+    return NNZ_OK;
+}
+
+int nnz_argmax_launch(nnz_ctx *ctx, const float *x, uint32_t n, uint32_t *oi, float *ov) {
+    argmax_kernel<<<1, 1024, 0, ctx->stream>>>(x, n, oi, ov);
+    NNZ_LAUNCHED(ctx);
+    return NNZ_OK;
+}
+
+extern "C" {
+
+int nnz_dispatch_rms_norm(nnz_ctx *ctx, const float *input, const float *scale, void *output,
+                          int out_dtype, int trunc, nnz_rmsnorm_dims d) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, input && scale && output, NNZ_EINVAL, "rms_norm: null buffer");
+    NNZ_REQUIRE(ctx, d.hidden_size > 0 && d.num_tokens > 0, NNZ_EINVAL, "rms_norm: zero dims");
+    dim3 g(d.num_tokens);
+    if (out_dtype == NNZ_F32 && !trunc)
+        rms_norm_kernel<NNZ_F32, false><<<g, 256, 0, ctx->stream>>>(input, scale, output, d.hidden_size, d.eps);
+    else if (out_dtype == NNZ_F16 && !trunc)
+        rms_norm_kernel<NNZ_F16, false><<<g, 256, 0, ctx->stream>>>(input, scale, output, d.hidden_size, d.eps);
+    else if (out_dtype == NNZ_F16 && trunc)
+        rms_norm_kernel<NNZ_F16, true><<<g, 256, 0, ctx->stream>>>(input, scale, output, d.hidden_size, d.eps);
+    else
+        return nnz_fail(ctx, NNZ_EINVAL, "rms_norm: unsupported output variant");
+    NNZ_LAUNCHED(ctx);
+    return NNZ_OK;
+}
+
+int nnz_dispatch_silu(nnz_ctx *ctx, const float *input, float *output, uint32_t count) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, input && output && count > 0, NNZ_EINVAL, "silu: bad arguments");
+    silu_kernel<<<grid1d(count, 256), 256, 0, ctx->stream>>>(input, output, count);
+    NNZ_LAUNCHED(ctx);
+    return NNZ_OK;
+}
+
+int nnz_dispatch_silu_elementwise_mul(nnz_ctx *ctx, const void *gate, const void *up, void *output,
+                                      int dtype, uint32_t count) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, gate && up && output && count > 0, NNZ_EINVAL, "silu_mul: bad arguments");
+    if (dtype == NNZ_F32)
+        silu_mul_kernel<NNZ_F32><<<grid1d(count, 256), 256, 0, ctx->stream>>>(gate, up, output, count);
+    else if (dtype == NNZ_F16)
+        silu_mul_kernel<NNZ_F16><<<grid1d(count, 256), 256, 0, ctx->stream>>>(gate, up, output, count);
+    else
+        return nnz_fail(ctx, NNZ_EINVAL, "silu_mul: dtype must be f32 or f16");
+    NNZ_LAUNCHED(ctx);
+    return NNZ_OK;
+}
+
+int nnz_dispatch_rope(nnz_ctx *ctx, void *data, int dtype, nnz_rope_dims d) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, data && d.num_heads > 0 && d.head_dim >= 2 && d.head_dim % 2 == 0, NNZ_EINVAL,
+                "rope: bad arguments");
+    const uint32_t n = d.num_heads * d.head_dim / 2;
+    if (dtype == NNZ_F32)
+        rope_kernel<NNZ_F32><<<grid1d(n, 256), 256, 0, ctx->stream>>>(data, d.num_heads, d.head_dim, d.position, d.rope_theta);
+    else if (dtype == NNZ_F16)
+        rope_kernel<NNZ_F16><<<grid1d(n, 256), 256, 0, ctx->stream>>>(data, d.num_heads, d.head_dim, d.position, d.rope_theta);
+    else if (dtype == NNZ_BF16)
+        rope_kernel<NNZ_BF16><<<grid1d(n, 256), 256, 0, ctx->stream>>>(data, d.num_heads, d.head_dim, d.position, d.rope_theta);
+    else
+        return nnz_fail(ctx, NNZ_EINVAL, "rope: bad dtype");
+    NNZ_LAUNCHED(ctx);
+    return NNZ_OK;
+}
+
+int nnz_dispatch_kv_cache_update(nnz_ctx *ctx, const void *k_proj, const void *v_proj, int pdt,
+                                 void *k_cache, void *v_cache, int cdt, nnz_kv_update_dims d) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, k_proj && v_proj && k_cache && v_cache, NNZ_EINVAL, "kv_update: null buffer");
+    NNZ_REQUIRE(ctx, d.num_kv_heads > 0 && d.head_dim > 0 && d.position < d.max_context_length,
+                NNZ_EINVAL, "kv_update: bad dims");
+    const uint32_t n = d.num_kv_heads * d.head_dim;
+    const uint32_t g = grid1d(n, 256);
+#define KVU(P, C) kv_update_kernel<P, C><<<g, 256, 0, ctx->stream>>>(k_proj, v_proj, k_cache, v_cache, d.num_kv_heads, d.head_dim, d.position, d.max_context_length)
+    if (pdt == NNZ_F32 && cdt == NNZ_F16) KVU(NNZ_F32, NNZ_F16);
+    else if (pdt == NNZ_F16 && cdt == NNZ_F16) KVU(NNZ_F16, NNZ_F16);
+    else if (pdt == NNZ_F32 && cdt == NNZ_BF16) KVU(NNZ_F32, NNZ_BF16);
+    else if (pdt == NNZ_BF16 && cdt == NNZ_BF16) KVU(NNZ_BF16, NNZ_BF16);
+    else return nnz_fail(ctx, NNZ_EINVAL, "kv_update: unsupported dtype pair");
+#undef KVU
+    NNZ_LAUNCHED(ctx);
+    return NNZ_OK;
+}
+
+int nnz_dispatch_fused_rope_kv_cache(nnz_ctx *ctx, const void *k_proj, const void *v_proj,
+                                     void *k_cache, void *v_cache, nnz_fused_rope_kv_dims d) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, k_proj && v_proj && k_cache && v_cache, NNZ_EINVAL, "fused_rope_kv: null buffer");
+    NNZ_REQUIRE(ctx, d.num_kv_heads > 0 && d.head_dim >= 2 && d.head_dim <= 256 && d.head_dim % 2 == 0 &&
+                         d.position < d.max_context_length,
+                NNZ_EINVAL, "fused_rope_kv: bad dims");
+    fused_rope_kv_kernel<<<d.num_kv_heads, 256, 0, ctx->stream>>>(
+        (const f16_t *)k_proj, (const f16_t *)v_proj, (f16_t *)k_cache, (f16_t *)v_cache, d.head_dim,
+        d.position, d.max_context_length, d.rope_theta);
+    NNZ_LAUNCHED(ctx);
+    return NNZ_OK;
+}
+
+int nnz_dispatch_fused_norm_rope(nnz_ctx *ctx, void *data, const float *scale,
+                                 nnz_fused_norm_rope_dims d) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, data && scale, NNZ_EINVAL, "fused_norm_rope: null buffer");
+    NNZ_REQUIRE(ctx, d.num_heads > 0 && d.head_dim >= 2 && d.head_dim <= 256 && d.head_dim % 2 == 0,
+                NNZ_EINVAL, "fused_norm_rope: bad dims");
+    fused_norm_rope_kernel<<<d.num_heads, 256, 0, ctx->stream>>>((f16_t *)data, scale, d.head_dim,
+                                                                 d.position, d.eps, d.rope_theta);
+    NNZ_LAUNCHED(ctx);
+    return NNZ_OK;
+}
+
+int nnz_dispatch_fused_k_norm_rope_kv_cache(nnz_ctx *ctx, const void *k_proj, const void *v_proj,
+                                            void *k_cache, void *v_cache, const float *k_scale,
+                                            nnz_fused_k_norm_rope_kv_dims d) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, k_proj && v_proj && k_cache && v_cache && k_scale, NNZ_EINVAL,
+                "fused_k_norm_rope_kv: null buffer");
+    NNZ_REQUIRE(ctx, d.num_kv_heads > 0 && d.head_dim >= 2 && d.head_dim <= 256 && d.head_dim % 2 == 0 &&
+                         d.position < d.max_context_length,
+                NNZ_EINVAL, "fused_k_norm_rope_kv: bad dims");
+    fused_k_norm_rope_kv_kernel<<<d.num_kv_heads, 256, 0, ctx->stream>>>(
+        (const f16_t *)k_proj, (const f16_t *)v_proj, (f16_t *)k_cache, (f16_t *)v_cache, k_scale,
+        d.head_dim, d.position, d.max_context_length, d.eps, d.rope_theta);
+    NNZ_LAUNCHED(ctx);
+    return NNZ_OK;
+}
+
+size_t nnz_gqa_scratch_bytes(nnz_gqa_dims d) {
+    if (!d.num_kv_heads || !d.seq_len) return 0;
+    return nnz_attn_scratch_bytes_impl(d.num_query_heads, d.head_dim, d.seq_len, d.num_kv_heads);
+}
+
+int nnz_dispatch_gqa_attention(nnz_ctx *ctx, const void *q, int q_dtype, const void *k_cache,
+                               const void *v_cache, int kv_dtype, int v_transposed, void *output,
+                               int out_dtype, void *scratch, size_t scratch_bytes,
+                               int32_t rope_position, float rope_theta, nnz_gqa_dims dims) {
+    NNZ_CHECK_CTX(ctx);
+    return nnz_attn_launch(ctx, q, q_dtype, k_cache, v_cache, kv_dtype, v_transposed != 0, output,
+                           out_dtype, scratch, scratch_bytes, rope_position, rope_theta, dims);
+}
+
+int nnz_dispatch_gqa_attention_fused(nnz_ctx *ctx, const void *q, void *k_cache, void *v_cache,
+                                     void *output, const void *k_raw, const void *v_raw,
+                                     const float *q_norm_scale, const float *k_norm_scale,
+                                     void *scratch, size_t scratch_bytes, nnz_gqa_fused_dims fd) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, q && k_cache && v_cache && output && k_raw && v_raw && q_norm_scale && k_norm_scale,
+                NNZ_EINVAL, "gqa_fused: null buffer");
+    NNZ_REQUIRE(ctx, fd.position < fd.max_context_length && fd.seq_len == fd.position + 1, NNZ_EINVAL,
+                "gqa_fused: seq_len must be position + 1 (< max_context_length)");
+    nnz_gqa_dims d{fd.num_query_heads, fd.num_kv_heads, fd.head_dim, fd.seq_len,
+                   fd.max_context_length, fd.heads_per_kv_group};
+    const size_t need = nnz_gqa_scratch_bytes(d);
+    NNZ_REQUIRE(ctx, scratch && scratch_bytes >= need, NNZ_EINVAL,
+                "gqa_fused: scratch of %zu bytes needed", need);
+    NNZ_REQUIRE(ctx, fd.head_dim == 64 || fd.head_dim == 128, NNZ_EUNSUPPORTED,
+                "gqa_fused: head_dim %u (supported: 64, 128)", fd.head_dim);
+    float *qf = nnz_attn_scratch_q(scratch, d);
+    int rc = nnz_attn_prep_launch(ctx, q, k_raw, v_raw, q_norm_scale, k_norm_scale, qf, k_cache,
+                                  v_cache, fd.num_query_heads, fd.num_kv_heads, fd.head_dim,
+                                  fd.position, nullptr, 1, fd.max_context_length, fd.eps,
+                                  fd.rope_theta);
+    if (rc) return rc;
+    return nnz_attn_launch(ctx, qf, NNZ_F32, k_cache, v_cache, NNZ_F16, true, output, NNZ_F16, scratch,
+                           scratch_bytes, -1, fd.rope_theta, d);
+}
+
+int nnz_dispatch_embedding_lookup(nnz_ctx *ctx, const uint32_t *ids, const void *bits,
+                                  const void *scales, float *out, nnz_embed_dims d) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, ids && bits && scales && out, NNZ_EINVAL, "embedding: null buffer");
+    NNZ_REQUIRE(ctx, d.num_tokens > 0 && d.hidden_size > 0 && d.vocab_size > 0 && d.group_size > 0,
+                NNZ_EINVAL, "embedding: zero dims");
+    const uint32_t n = d.num_tokens * d.hidden_size;
+    embed_q1_kernel<<<grid1d(n, 256), 256, 0, ctx->stream>>>(ids, (const uint8_t *)bits,
+                                                            (const uint16_t *)scales, out,
+                                                            d.hidden_size, d.num_tokens,
+                                                            d.group_size, d.vocab_size);
+    NNZ_LAUNCHED(ctx);
+    return NNZ_OK;
+}
+
+int nnz_dispatch_embedding_lookup_q4(nnz_ctx *ctx, const uint32_t *ids, const void *nibs,
+                                     const void *scales, const void *biases, float *out,
+                                     nnz_embed_dims d) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, ids && nibs && scales && biases && out, NNZ_EINVAL, "embedding_q4: null buffer");
+    NNZ_REQUIRE(ctx, d.num_tokens > 0 && d.hidden_size > 0 && d.vocab_size > 0 && d.group_size > 0,
+                NNZ_EINVAL, "embedding_q4: zero dims");
+    const uint32_t n = d.num_tokens * d.hidden_size;
+    embed_q4_kernel<<<grid1d(n, 256), 256, 0, ctx->stream>>>(
+        ids, (const uint32_t *)nibs, (const uint16_t *)scales, (const uint16_t *)biases, out,
+        d.hidden_size, d.num_tokens, d.group_size, d.vocab_size);
+    NNZ_LAUNCHED(ctx);
+    return NNZ_OK;
+}
+
+int nnz_dispatch_embedding_lookup_bf16(nnz_ctx *ctx, const uint32_t *ids, const void *table,
+                                       float *out, nnz_embed_dims d) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, ids && table && out, NNZ_EINVAL, "embedding_bf16: null buffer");
+    NNZ_REQUIRE(ctx, d.num_tokens > 0 && d.hidden_size > 0 && d.vocab_size > 0, NNZ_EINVAL,
+                "embedding_bf16: zero dims");
+    const uint32_t n = d.num_tokens * d.hidden_size;
+    embed_bf16_kernel<<<grid1d(n, 256), 256, 0, ctx->stream>>>(ids, (const uint16_t *)table, out,
+                                                              d.hidden_size, d.num_tokens,
+                                                              d.vocab_size);
+    NNZ_LAUNCHED(ctx);
+    return NNZ_OK;
+}
+
+int nnz_dispatch_residual_add(nnz_ctx *ctx, float *residual, const float *addition, uint32_t count) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, residual && addition && count > 0, NNZ_EINVAL, "residual_add: bad arguments");
+    residual_add_kernel<<<grid1d(count, 256), 256, 0, ctx->stream>>>(residual, addition, count);
+    NNZ_LAUNCHED(ctx);
+    return NNZ_OK;
+}
+
+int nnz_dispatch_argmax(nnz_ctx *ctx, const float *logits, uint32_t count, uint32_t *out_index,
+                        float *out_value) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, logits && out_index && count > 0, NNZ_EINVAL, "argmax: bad arguments");
+    return nnz_argmax_launch(ctx, logits, count, out_index, out_value);
+}
+
+int nnz_dispatch_dequant(nnz_ctx *ctx, const nnz_qweight *w, float *output, nnz_qmv_dims d) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, w && w->codes && w->scales && output, NNZ_EINVAL, "dequant: null buffer");
+    NNZ_REQUIRE(ctx, d.M > 0 && d.K > 0 && d.group_size > 0 && d.K % d.group_size == 0, NNZ_EINVAL,
+                "dequant: bad dims");
+    NNZ_REQUIRE(ctx, (w->bits == 1 && d.K % 32 == 0) || (w->bits == 4 && d.K % 8 == 0 && w->biases),
+                NNZ_EINVAL, "dequant: bad weight");
+    NNZ_REQUIRE(ctx, (uint64_t)w->packed_count == (uint64_t)d.M * d.K && w->group_size == d.group_size,
+                NNZ_EINVAL, "dequant: descriptor does not match dims");
+    const uint64_t n = (uint64_t)d.M * d.K;
+    dequant_kernel<<<grid1d(n, 256), 256, 0, ctx->stream>>>(
+        (const uint32_t *)w->codes, (const uint16_t *)w->scales, (const uint16_t *)w->biases, output,
+        d.M, d.K, d.group_size, (int)w->bits, (int)w->scale_dtype);
+    NNZ_LAUNCHED(ctx);
+    return NNZ_OK;
+}
+
+}  // extern "C"

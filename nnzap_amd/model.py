@@ -1,0 +1,139 @@
+"""Host wrapper of the C-ABI decoder model (Model(Config) + generate).
+
+Mirrors nnmetal/src/model.zig (Model: init + loadWeights) and
+nnmetal/src/transformer.zig:3942 (generate) for the synthetic BASELINE
+config-5 model.  All compute runs in libnnzap_amd.so.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import sys
+
+import numpy as np
+
+from . import _lib as L
+from . import synth as S
+from .configs import PROJS, DecoderConfig, DecoderWeights
+from .ops import Device
+
+_CODES = {"q": 10, "k": 12, "v": 14, "o": 16, "gate": 18, "up": 20, "down": 22}
+T_EMBED_CODES, T_EMBED_SCALES, T_LM_CODES, T_LM_SCALES, T_FINAL_NORM = 0, 1, 2, 3, 4
+T_ATTN_NORM, T_FFN_NORM, T_Q_NORM, T_K_NORM = 24, 25, 26, 27
+T_K_CACHE, T_V_CACHE, T_LOGITS, T_RESIDUAL = 30, 31, 40, 41
+
+
+class DecoderModel:
+    """One decoder instance resident in HBM on ``dev``."""
+
+    def __init__(self, dev: Device, cfg: DecoderConfig):
+        self.dev, self.cfg = dev, cfg
+        c = L.ModelConfig(cfg.vocab_size, cfg.hidden_size, cfg.intermediate_size, cfg.num_layers,
+                          cfg.num_query_heads, cfg.num_kv_heads, cfg.head_dim,
+                          cfg.max_context_length, cfg.max_prefill_length, cfg.group_size,
+                          cfg.rope_theta, cfg.rms_eps, cfg.embed_kind, cfg.lm_head_kind)
+        h = C.c_void_p()
+        dev.call("nnz_model_create", C.byref(c), C.byref(h))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            L.lib().nnz_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        if sys.is_finalizing():  # HIP runtime may be gone; see ops.Device
+            return
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _mcall(self, name, *args):
+        rc = getattr(L.lib(), name)(self.h, *args)
+        L.check(self.dev.ctx, name, rc)
+
+    def tensor(self, tid: int, layer: int = 0):
+        p, n = C.c_void_p(), C.c_size_t()
+        self._mcall("nnz_model_tensor", tid, layer, C.byref(p), C.byref(n))
+        return p.value, n.value
+
+    def upload(self, tid: int, layer: int, arr: np.ndarray) -> None:
+        ptr, nbytes = self.tensor(tid, layer)
+        arr = np.ascontiguousarray(arr)
+        if arr.nbytes != nbytes:
+            raise ValueError(f"tensor {tid}/{layer}: {arr.nbytes} bytes given, {nbytes} expected")
+        self.dev.call("nnz_upload", C.c_void_p(ptr), arr.ctypes.data_as(C.c_void_p), nbytes)
+
+    def download(self, tid: int, layer: int = 0, dtype=np.float32) -> np.ndarray:
+        ptr, nbytes = self.tensor(tid, layer)
+        out = np.empty(nbytes // np.dtype(dtype).itemsize, dtype=dtype)
+        self.dev.call("nnz_download", out.ctypes.data_as(C.c_void_p), C.c_void_p(ptr), nbytes)
+        return out
+
+    def load(self, w: DecoderWeights, embed_on_device: bool = False) -> None:
+        """Upload weights (model.zig:196-242 loadWeights).  With
+        ``embed_on_device`` the bf16 embedding table is generated on the GPU
+        from the same seeded stream instead of being uploaded."""
+        cfg = self.cfg
+        if cfg.embed_kind == L.EMBED_BF16:
+            if embed_on_device:
+                ptr, nbytes = self.tensor(T_EMBED_CODES)
+                self.dev.call("nnz_synth_normal_bf16", C.c_void_p(ptr), nbytes // 2,
+                              S.SEED_MODEL_BASE + 0, 0.02)
+            else:
+                self.upload(T_EMBED_CODES, 0, w.embed_bf16)
+        if cfg.lm_head_kind == L.LMHEAD_Q1:
+            self.upload(T_LM_CODES, 0, w.lm_head.codes)
+            self.upload(T_LM_SCALES, 0, w.lm_head.scales)
+        self.upload(T_FINAL_NORM, 0, w.final_norm)
+        for l, layer in enumerate(w.layers):
+            for name in PROJS:
+                cid = _CODES[name]
+                self.upload(cid, l, layer[name].codes)
+                self.upload(cid + 1, l, layer[name].scales)
+            self.upload(T_ATTN_NORM, l, layer["attn_norm"])
+            self.upload(T_FFN_NORM, l, layer["ffn_norm"])
+            self.upload(T_Q_NORM, l, layer["q_norm"])
+            self.upload(T_K_NORM, l, layer["k_norm"])
+        self.dev.sync()
+
+    def forward_decode(self, token: int, position: int) -> np.ndarray:
+        self._mcall("nnz_model_forward_decode", token, position)
+        self.dev.sync()
+        return self.download(T_LOGITS)
+
+    def prefill(self, tokens: np.ndarray, start: int = 0) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        self._mcall("nnz_model_prefill", t.ctypes.data_as(C.c_void_p), len(t), start)
+        self.dev.sync()
+        return self.download(T_LOGITS)
+
+    # -- streaming decode: begin (prefill + capture), enqueue steps, read -----
+    def decode_begin(self, prompt: np.ndarray, max_new: int) -> None:
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        self._mcall("nnz_model_decode_begin", p.ctypes.data_as(C.c_void_p), len(p), max_new)
+
+    def decode_steps(self, n: int) -> None:
+        self._mcall("nnz_model_decode_steps", n)
+
+    def decode_read(self, n: int):
+        toks = np.zeros(n, dtype=np.uint32)
+        margins = np.zeros(n, dtype=np.float32)
+        self._mcall("nnz_model_decode_read", n, toks.ctypes.data_as(C.c_void_p),
+                    margins.ctypes.data_as(C.c_void_p))
+        return toks, margins
+
+    def decode_end(self) -> None:
+        self._mcall("nnz_model_decode_end")
+
+    def generate(self, prompt: np.ndarray, n_new: int, use_graph: bool = True,
+                 step_ms: bool = False):
+        """Greedy generate; returns (tokens, top-2 margins, per-step ms or None)."""
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        toks = np.zeros(n_new, dtype=np.uint32)
+        margins = np.zeros(n_new, dtype=np.float32)
+        ms = np.zeros(n_new, dtype=np.float32) if step_ms else None
+        self._mcall("nnz_model_generate", p.ctypes.data_as(C.c_void_p), len(p), n_new,
+                    toks.ctypes.data_as(C.c_void_p), margins.ctypes.data_as(C.c_void_p),
+                    ms.ctypes.data_as(C.c_void_p) if ms is not None else None, int(use_graph))
+        return toks, margins, ms

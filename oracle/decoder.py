@@ -1,0 +1,122 @@
+"""CPU oracle of the whole decode step -- TEST INFRASTRUCTURE ONLY.
+
+Restates nnmetal's forwardDecode (nnmetal/src/transformer.zig:2566-2785,
+blocks :2452-3646) and generate (:3942-4030) in numpy, float64 arithmetic,
+with the reference's storage rounding points:
+
+* residual stream: float32, rounded after every ``+=`` (model.zig:87-102);
+* fused-norm prologue output, Q/K/V projections, attention output, the
+  SiLU*mul activation and the final-norm output: float16
+  (qmv_specialized.metal:1137-1177, :1432, :1617, :1276; transformer.metal:1689);
+* normalised/rotated q kept unrounded (transformer.metal:1529-1557), the
+  normalised/rotated k and v stored as float16 in the KV cache (:1583-1592);
+* logits: float32 (qmv_spec_f16in, qmv_specialized.metal:735).
+
+Prefill is evaluated as a batch (all prompt tokens at once, causal mask):
+mathematically identical to the reference's token-by-token prefill
+(transformer.zig:4032-4068) because every token's computation only reads
+keys/values of earlier positions.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from nnzap_amd.configs import PROJS, DecoderConfig, DecoderWeights
+from nnzap_amd import synth as S
+
+from . import oracle as O
+
+
+def _f32(x):
+    return np.asarray(x, dtype=np.float64).astype(np.float32).astype(np.float64)
+
+
+class OracleDecoder:
+    def __init__(self, w: DecoderWeights, max_ctx: int | None = None):
+        cfg = w.cfg
+        self.cfg, self.w = cfg, w
+        self.W = [{n: O.dequant(layer[n]) for n in PROJS} for layer in w.layers]
+        self.lm = O.dequant(w.lm_head) if w.lm_head is not None else None
+        T = max_ctx or cfg.max_context_length
+        self.kc = np.zeros((cfg.num_layers, cfg.num_kv_heads, T, cfg.head_dim))
+        self.vc = np.zeros((cfg.num_layers, cfg.num_kv_heads, T, cfg.head_dim))
+        self._emb_cache = {}
+
+    # -- embedding (bf16 table, widened to f32) -------------------------------
+    def embed_rows(self, ids) -> np.ndarray:
+        cfg = self.cfg
+        ids = [int(i) for i in ids]
+        if self.w.embed_bf16 is not None:
+            return S.bf16_bits_to_f32(self.w.embed_bf16[ids]).astype(np.float64)
+        out = []
+        for t in ids:
+            if t not in self._emb_cache:
+                idx = np.arange(t * cfg.hidden_size, (t + 1) * cfg.hidden_size, dtype=np.uint64)
+                z = 0.02 * S.normal_at(S.SEED_MODEL_BASE + 0, idx)
+                self._emb_cache[t] = S.bf16_bits_to_f32(S.f64_to_bf16_bits(z)).astype(np.float64)
+            out.append(self._emb_cache[t])
+        return np.stack(out)
+
+    def lm_head(self, xf: np.ndarray) -> np.ndarray:
+        if self.lm is not None:
+            return _f32(xf @ self.lm.T)
+        table = S.bf16_bits_to_f32(self.w.embed_bf16).astype(np.float64)
+        return _f32(xf @ table.T)
+
+    # -- one batch of consecutive tokens (P >= 1) -------------------------------
+    def forward(self, ids, start: int) -> np.ndarray:
+        """Run tokens ``ids`` at positions start..start+P-1; returns the logits
+        of every token [P, vocab] (float32 values as float64)."""
+        cfg = self.cfg
+        P = len(ids)
+        D, Hq, Hkv = cfg.head_dim, cfg.num_query_heads, cfg.num_kv_heads
+        g = Hq // Hkv
+        res = _f32(self.embed_rows(ids))
+        positions = np.arange(start, start + P)
+        for l, layer in enumerate(self.w.layers):
+            W = self.W[l]
+            xn = O.f16(O.rmsnorm(res, layer["attn_norm"], cfg.rms_eps))
+            q = O.f16(xn @ W["q"].T)
+            k = O.f16(xn @ W["k"].T)
+            v = O.f16(xn @ W["v"].T)
+            qn = np.stack([O.head_norm_rope(q[p].reshape(Hq, D), layer["q_norm"], int(positions[p]),
+                                            cfg.rope_theta, cfg.rms_eps) for p in range(P)])
+            kn = np.stack([O.f16(O.head_norm_rope(k[p].reshape(Hkv, D), layer["k_norm"],
+                                                  int(positions[p]), cfg.rope_theta, cfg.rms_eps))
+                           for p in range(P)])
+            self.kc[l, :, start:start + P, :] = kn.transpose(1, 0, 2)
+            self.vc[l, :, start:start + P, :] = v.reshape(P, Hkv, D).transpose(1, 0, 2)
+            att = np.empty((P, Hq, D))
+            scale = 1.0 / np.sqrt(D)
+            T = start + P
+            K = self.kc[l, :, :T, :]
+            V = self.vc[l, :, :T, :]
+            mask = np.arange(T)[None, :] <= positions[:, None]  # [P, T]
+            for h in range(Hq):
+                s = qn[:, h, :] @ K[h // g].T * scale  # [P, T]
+                s = np.where(mask, s, -np.inf)
+                s = np.exp(s - s.max(axis=1, keepdims=True))
+                s /= s.sum(axis=1, keepdims=True)
+                att[:, h, :] = s @ V[h // g]
+            att = O.f16(att.reshape(P, Hq * D))
+            res = _f32(res + att @ W["o"].T)
+            xn2 = O.f16(O.rmsnorm(res, layer["ffn_norm"], cfg.rms_eps))
+            hmid = O.f16(O.silu(xn2 @ W["gate"].T) * (xn2 @ W["up"].T))
+            res = _f32(res + hmid @ W["down"].T)
+        xf = O.f16(O.rmsnorm(res, self.w.final_norm, cfg.rms_eps))
+        return self.lm_head(xf)
+
+    def generate(self, prompt, n_new: int):
+        """Greedy generate with the reference's loop (transformer.zig:3942-4030):
+        returns (tokens, top-2 margins) -- n_new tokens, n_new decode passes."""
+        logits = self.forward(list(prompt), 0)[-1]
+        pos = len(prompt)
+        toks, margins = [], []
+        for _ in range(n_new):
+            t = O.argmax_first(logits)
+            srt = np.sort(logits)
+            toks.append(t)
+            margins.append(float(srt[-1] - srt[-2]))
+            logits = self.forward([t], pos)[0]
+            pos += 1
+        return np.array(toks, dtype=np.uint32), np.array(margins)

@@ -1,0 +1,263 @@
+"""GPU parity of attention, norms, RoPE, KV append, embeddings, argmax and the
+prefill dequant-GEMM against the CPU oracle."""
+import numpy as np
+import pytest
+import torch
+
+from nnzap_amd import _lib as L
+from nnzap_amd import configs as cf
+from nnzap_amd import ops
+from nnzap_amd import synth as S
+from oracle import oracle as O
+
+from gpu_util import assert_close, from_bits16, host, tdev
+
+pytestmark = pytest.mark.gpu
+
+
+def _scratch(dims):
+    n = ops.gqa_scratch_bytes(dims)
+    return torch.empty((n + 3) // 4, dtype=torch.float32, device="cuda")
+
+
+# --------------------------------------------------------------- attention --
+@pytest.mark.parametrize("L_", [512, 4096, 32768])
+def test_config4_gqa_decode(dev, L_):
+    """q bf16 [16,128] roped at position L, KV bf16 [8,L,128],
+    scale 1/sqrt(128), fp32 accumulate; V given as [8, L, 128]."""
+    print(f"config4 L={L_}", flush=True)
+    q, k, v = cf.config4(L_)
+    qd, kd, vd = from_bits16(q, "bf16"), from_bits16(k, "bf16"), from_bits16(v, "bf16")
+    out = torch.empty(16, 128, dtype=torch.float32, device="cuda")
+    dims = L.GQADims(16, 8, 128, L_, L_, 2)
+    ops.dispatch_gqa_attention(dev, qd, kd, vd, out, _scratch(dims), dims, v_transposed=False,
+                               rope_position=L_, rope_theta=1e6)
+    dev.sync()
+    qf = O.rope(S.bf16_bits_to_f32(q).astype(np.float64), L_, 1e6)
+    ref = O.attention_decode(qf, S.bf16_bits_to_f32(k), S.bf16_bits_to_f32(v), L_, False)
+    assert_close(host(out), ref, what=f"config4 L={L_}")
+
+
+@pytest.mark.parametrize("L_,max_ctx,hq,hkv,d", [(1, 8, 4, 2, 64), (77, 128, 16, 8, 128),
+                                                 (700, 1024, 8, 8, 128), (3000, 4096, 16, 2, 64)])
+def test_gqa_transposed_v_f16(dev, L_, max_ctx, hq, hkv, d):
+    """Reference layout: f16 caches, V transposed [h][d][max_ctx], f16 q/out."""
+    rng_q = (0.3 * S.normal(400, hq * d)).astype(np.float16).reshape(hq, d)
+    kf = np.zeros((hkv, max_ctx, d), np.float16)
+    vf = np.zeros((hkv, d, max_ctx), np.float16)
+    kf[:, :L_] = S.normal(401, hkv * L_ * d).astype(np.float16).reshape(hkv, L_, d)
+    vf[:, :, :L_] = S.normal(402, hkv * L_ * d).astype(np.float16).reshape(hkv, d, L_)
+    out = torch.empty(hq, d, dtype=torch.float16, device="cuda")
+    dims = L.GQADims(hq, hkv, d, L_, max_ctx, hq // hkv)
+    ops.dispatch_gqa_attention(dev, tdev(rng_q), tdev(kf), tdev(vf), out, _scratch(dims), dims)
+    dev.sync()
+    ref = O.attention_decode(rng_q.astype(np.float64), kf.astype(np.float64), vf.astype(np.float64),
+                             L_, True)
+    assert_close(host(out), O.f16(ref), what=f"gqa L={L_}")
+
+
+@pytest.mark.parametrize("pos", [0, 5, 600, 1500])
+def test_gqa_fused_norm_rope_kv(dev, pos):
+    """transformer.metal:1467-1695 semantics: q/k per-head RMSNorm + RoPE, K/V
+    append at `pos`, attention over pos+1 tokens; cache contents checked too."""
+    hq, hkv, d, max_ctx, theta = 16, 8, 128, 2048, 1e6
+    q = S.normal(410, hq * d).astype(np.float16).reshape(hq, d)
+    kr = S.normal(411, hkv * d).astype(np.float16).reshape(hkv, d)
+    vr = S.normal(412, hkv * d).astype(np.float16).reshape(hkv, d)
+    qn = (1 + 0.1 * S.normal(413, d)).astype(np.float32)
+    kn = (1 + 0.1 * S.normal(414, d)).astype(np.float32)
+    kc = np.zeros((hkv, max_ctx, d), np.float16)
+    vc = np.zeros((hkv, d, max_ctx), np.float16)
+    if pos:
+        kc[:, :pos] = (0.5 * S.normal(415, hkv * pos * d)).astype(np.float16).reshape(hkv, pos, d)
+        vc[:, :, :pos] = S.normal(416, hkv * pos * d).astype(np.float16).reshape(hkv, d, pos)
+    kcd, vcd = tdev(kc), tdev(vc)
+    out = torch.empty(hq, d, dtype=torch.float16, device="cuda")
+    fd = L.GQAFusedDims(hq, hkv, d, pos + 1, max_ctx, hq // hkv, pos, 1e-6, theta)
+    dims = L.GQADims(hq, hkv, d, pos + 1, max_ctx, hq // hkv)
+    ops.dispatch_gqa_attention_fused(dev, tdev(q), kcd, vcd, out, tdev(kr), tdev(vr), tdev(qn),
+                                     tdev(kn), _scratch(dims), fd)
+    dev.sync()
+    kc_ref, vc_ref = kc.astype(np.float64), vc.astype(np.float64)
+    ref = O.gqa_fused_step(q.astype(np.float64), kr.astype(np.float64), vr.astype(np.float64),
+                           kc_ref, vc_ref, qn, kn, pos, theta, v_transposed=True)
+    kg = host(kcd)
+    assert_close(kg[:, pos], kc_ref[:, pos], what="k cache row")
+    assert np.array_equal(host(vcd)[:, :, pos], vc_ref[:, :, pos])
+    assert np.array_equal(kg[:, :pos], kc_ref[:, :pos])  # earlier rows untouched
+    assert_close(host(out), O.f16(ref), what=f"fused pos={pos}")
+
+
+# ------------------------------------------------------------------ norms ---
+@pytest.mark.parametrize("variant", ["f32", "f16", "bf16_f16"])
+def test_rms_norm_variants(dev, variant):
+    H, T = 2048, 3
+    x = S.normal(420, H * T).astype(np.float32)
+    w = (1 + 0.1 * S.normal(421, H)).astype(np.float32)
+    odt = torch.float32 if variant == "f32" else torch.float16
+    out = torch.empty(T * H, dtype=odt, device="cuda")
+    ops.dispatch_rms_norm(dev, tdev(x), tdev(w), out, H, T, bf16_trunc=(variant == "bf16_f16"))
+    dev.sync()
+    ref = O.rmsnorm(x.reshape(T, H), w).reshape(-1)
+    if variant == "f16":
+        ref = O.f16(ref)
+    elif variant == "bf16_f16":
+        ref = O.f16(O.bf16_trunc(ref))
+        assert_close(host(out), ref, rtol=1e-2, what=variant)  # 1 bf16 ulp band
+        return
+    assert_close(host(out), ref, what=variant)
+
+
+def test_rope_and_kv_update(dev):
+    """rope (transformer_test.zig:1185-1240 case) and kv_cache_update (:1242-1336)."""
+    vals = ((np.arange(16) + 1) * 0.1).astype(np.float32)
+    t = tdev(vals)
+    ops.dispatch_rope(dev, t, 2, 8, 3, 10000.0)
+    dev.sync()
+    assert_close(host(t), O.rope(vals.reshape(2, 8), 3, 10000.0).reshape(-1), rtol=1e-5, what="rope")
+    # large position, f16 in place
+    x = S.normal(430, 16 * 128).astype(np.float16)
+    t16 = tdev(x)
+    ops.dispatch_rope(dev, t16, 16, 128, 30000, 1e6)
+    dev.sync()
+    assert_close(host(t16), O.f16(O.rope(x.astype(np.float64).reshape(16, 128), 30000, 1e6).reshape(-1)),
+                 what="rope f16")
+    # kv update: K[h][pos][d], V[h][d][pos]
+    hkv, d, max_ctx, pos = 2, 4, 8, 2
+    k = (np.arange(hkv * d) * 0.5).astype(np.float32)
+    v = (np.arange(hkv * d) * -0.25).astype(np.float32)
+    kc = torch.zeros(hkv * max_ctx * d, dtype=torch.float16, device="cuda")
+    vc = torch.zeros(hkv * max_ctx * d, dtype=torch.float16, device="cuda")
+    ops.dispatch_kv_cache_update(dev, tdev(k), tdev(v), kc, vc, hkv, d, pos, max_ctx)
+    dev.sync()
+    K = host(kc).reshape(hkv, max_ctx, d)
+    V = host(vc).reshape(hkv, d, max_ctx)
+    assert np.array_equal(K[:, pos], k.reshape(hkv, d))
+    assert np.array_equal(V[:, :, pos], v.reshape(hkv, d))
+    K[:, pos] = 0
+    V[:, :, pos] = 0
+    assert not K.any() and not V.any()
+
+
+def test_fused_rope_kernels(dev):
+    hkv, hq, d, max_ctx, pos, theta = 8, 16, 128, 64, 17, 1e6
+    k = S.normal(440, hkv * d).astype(np.float16)
+    v = S.normal(441, hkv * d).astype(np.float16)
+    ks = (1 + 0.1 * S.normal(442, d)).astype(np.float32)
+    kc = torch.zeros(hkv, max_ctx, d, dtype=torch.float16, device="cuda")
+    vc = torch.zeros(hkv, d, max_ctx, dtype=torch.float16, device="cuda")
+    ops.dispatch_fused_rope_kv_cache(dev, tdev(k), tdev(v), kc, vc,
+                                     L.FusedRoPEKVDims(hkv, d, pos, max_ctx, theta))
+    dev.sync()
+    kr = O.f16(O.rope(k.astype(np.float64).reshape(hkv, d), pos, theta))
+    assert_close(host(kc)[:, pos], kr, what="fused rope kv")
+    assert np.array_equal(host(vc)[:, :, pos], v.reshape(hkv, d).astype(np.float64))
+    ops.dispatch_fused_k_norm_rope_kv_cache(dev, tdev(k), tdev(v), kc, vc, tdev(ks),
+                                            L.FusedKNormRoPEKVDims(hkv, d, pos + 1, max_ctx, 1e-6, theta))
+    dev.sync()
+    kr2 = O.f16(O.head_norm_rope(k.astype(np.float64).reshape(hkv, d), ks, pos + 1, theta))
+    assert_close(host(kc)[:, pos + 1], kr2, what="fused k norm rope kv")
+    q = S.normal(443, hq * d).astype(np.float16)
+    qd = tdev(q)
+    ops.dispatch_fused_norm_rope(dev, qd, tdev(ks), L.FusedNormRoPEDims(hq, d, pos, 1e-6, theta))
+    dev.sync()
+    assert_close(host(qd).reshape(hq, d),
+                 O.f16(O.head_norm_rope(q.astype(np.float64).reshape(hq, d), ks, pos, theta)),
+                 what="fused norm rope")
+
+
+# ------------------------------------------------------- embedding / misc ---
+def test_embedding_known_answer(dev):
+    """transformer_test.zig:1450-1541 (bits 0xAA, scale 0.5, tokens [1, 3])."""
+    ids = tdev(np.array([1, 3], np.int32))
+    bits = tdev(np.full(8, 0xAA, np.uint8))
+    sc = tdev(np.array([0.5], np.float16))
+    out = torch.empty(32, dtype=torch.float32, device="cuda")
+    ops.dispatch_embedding_lookup(dev, ids, bits, sc, out, L.EmbedDims(4, 16, 2, 128))
+    dev.sync()
+    assert np.array_equal(host(out), np.tile([-0.5, 0.5], 16))
+
+
+def test_embedding_q1_q4_bf16_random(dev):
+    V, H = 64, 256
+    w1 = cf.q1_matrix(V, H, 128, 450, 451)
+    ids = np.array([0, 63, 17, 17, 5], np.int32)
+    out = torch.empty(len(ids) * H, dtype=torch.float32, device="cuda")
+    ops.dispatch_embedding_lookup(dev, tdev(ids), tdev(w1.codes.view(np.uint8)),
+                                  tdev(w1.scales.view(np.float16)), out,
+                                  L.EmbedDims(V, H, len(ids), 128))
+    dev.sync()
+    ref = O.embed_q1(ids, w1.codes.view(np.uint8).reshape(-1), w1.scales.view(np.float16).reshape(-1), H, 128)
+    assert np.array_equal(host(out), ref.reshape(-1))
+    w4 = cf.q4_matrix(V, H, 64, 452, 453, 454, scale_dtype=1 + 1)
+    ops.dispatch_embedding_lookup_q4(dev, tdev(ids), tdev(w4.codes), tdev(w4.scales.view(np.int16)),
+                                     tdev(w4.biases.view(np.int16)), out, L.EmbedDims(V, H, len(ids), 64))
+    dev.sync()
+    ref4 = O.embed_q4(ids, w4.codes, w4.scales, w4.biases, H, 64, 2)
+    assert np.array_equal(host(out), ref4.reshape(-1))
+    tab = S.f64_to_bf16_bits(S.normal(455, V * H)).reshape(V, H)
+    ops.dispatch_embedding_lookup_bf16(dev, tdev(ids), tdev(tab.view(np.int16)), out,
+                                       L.EmbedDims(V, H, len(ids), 0))
+    dev.sync()
+    assert np.array_equal(host(out), S.bf16_bits_to_f32(tab[ids]).reshape(-1).astype(np.float64))
+
+
+def test_residual_silu_argmax(dev):
+    r = tdev(np.arange(1, 9, dtype=np.float32))
+    a = tdev((np.arange(1, 9) * 0.1).astype(np.float32))
+    ops.dispatch_residual_add(dev, r, a)
+    x = S.normal(460, 1000).astype(np.float32)
+    s = torch.empty(1000, dtype=torch.float32, device="cuda")
+    ops.dispatch_silu(dev, tdev(x), s)
+    g, u = S.normal(461, 1000).astype(np.float16), S.normal(462, 1000).astype(np.float16)
+    sm = torch.empty(1000, dtype=torch.float16, device="cuda")
+    ops.dispatch_silu_elementwise_mul(dev, tdev(g), tdev(u), sm)
+    logits = S.normal(463, 151936).astype(np.float32)
+    logits[[100, 90000]] = 9.0  # tie: the first maximum wins
+    idx = torch.zeros(1, dtype=torch.int32, device="cuda")
+    val = torch.zeros(2, dtype=torch.float32, device="cuda")
+    ops.dispatch_argmax(dev, tdev(logits), idx, val)
+    dev.sync()
+    assert np.allclose(host(r), np.arange(1, 9) * 1.1, rtol=1e-6)
+    assert_close(host(s), O.silu(x), rtol=1e-5, what="silu")
+    assert_close(host(sm), O.f16(O.silu(g.astype(np.float64)) * u), what="silu mul f16")
+    assert int(idx.item()) == 100
+    assert host(val)[0] == 9.0 and host(val)[1] == 9.0
+
+
+# ------------------------------------------------------------ prefill GEMM --
+@pytest.mark.parametrize("P", [1, 37, 512])
+def test_dequant_gemm_modes(dev, P):
+    M, K = 1024, 2048
+    wa, wb = cf.q1_matrix(M, K, 128, 470, 471), cf.q1_matrix(M, K, 128, 472, 473)
+    a16 = (0.5 * S.normal(474, P * K)).astype(np.float16).reshape(P, K)
+    A = a16.astype(np.float64)
+    da, db = ops.DeviceQWeight(dev, wa), ops.DeviceQWeight(dev, wb)
+    ad = tdev(a16)
+    ra, rb = A @ O.dequant(wa).T, A @ O.dequant(wb).T
+    out16 = torch.empty(P, M, dtype=torch.float16, device="cuda")
+    ops.dispatch_dequant_gemm(dev, da, ad, out16, L.GEMM_STORE_F16)
+    out32 = torch.empty(P, M, dtype=torch.float32, device="cuda")
+    ops.dispatch_dequant_gemm(dev, da, ad, out32, L.GEMM_STORE_F32)
+    res0 = S.normal(475, P * M).astype(np.float32).reshape(P, M)
+    res = tdev(res0)
+    ops.dispatch_dequant_gemm(dev, da, ad, res, L.GEMM_RESADD)
+    ops.dispatch_dequant_gemm(dev, da, ad, out16, L.GEMM_SILU_PAIR, wb=db)
+    dev.sync()
+    assert_close(host(out32), ra, what="gemm f32")
+    assert_close(host(res), res0 + ra, what="gemm resadd")
+    assert_close(host(out16), O.f16(O.silu(ra) * rb), what="gemm silu pair")
+
+
+def test_gemm_row_equals_decode_qmv(dev):
+    """Per-token equivalence: GEMM row p equals the decode QMV of token p."""
+    M, K, P = 512, 2048, 8
+    w = cf.q1_matrix(M, K, 128, 480, 481)
+    a16 = S.normal(482, P * K).astype(np.float16).reshape(P, K)
+    dw = ops.DeviceQWeight(dev, w)
+    out = torch.empty(P, M, dtype=torch.float32, device="cuda")
+    ops.dispatch_dequant_gemm(dev, dw, tdev(a16), out, L.GEMM_STORE_F32)
+    y = torch.empty(M, dtype=torch.float32, device="cuda")
+    ops.dispatch_qmv_f16in(dev, dw, tdev(a16[5]), y)
+    dev.sync()
+    assert_close(host(out)[5], host(y), rtol=1e-4, what="gemm row vs qmv")

@@ -49,7 +49,7 @@ def bench_decode(args, dev):
     cfg = cf.DecoderConfig(**{**cf.BONSAI_1_7B.__dict__,
                               "lm_head_kind": 1 if args.lm_head == "tied" else 0})
     t = time.time()
-    w = cf.decoder_weights(cfg, norm_mode="small")
+    w = cf.decoder_weights(cfg, norm_mode="small", host_embed=False)
     m = DecoderModel(dev, cfg)
     m.load(w, embed_on_device=True)
     log(f"model ready in {time.time() - t:.1f}s")
@@ -131,126 +131,162 @@ def time_launches(dev, fn, n_iter, reps=3):
     return best * 1000.0  # us
 
 
-def bench_kernels(dev, quick=False):
+def _kernel_cases():
+    """Named kernel timings: name -> fn(dev, n_iter) -> (us, algorithmic
+    bytes per launch, launches per decode token or None).  The decode cases
+    are the launches the captured decode step makes, at config-5 shapes."""
     import torch
     from nnzap_amd import _lib as L
     from nnzap_amd import configs as cf
     from nnzap_amd import ops
 
-    n_iter = 64 if quick else 256
-    res = {}
+    f32, f16 = torch.float32, torch.float16
+    H, I, QD, KVD, V = 2048, 6144, 2048, 1024, 151936
 
-    def rec(name, us, nbytes, per_token=None):
+    def act():
+        rng = np.random.default_rng(0)
+        res_d = torch.from_numpy(rng.standard_normal(H).astype(np.float32)).cuda()
+        return res_d, torch.ones(H, dtype=f32, device="cuda")
+
+    def config1(dev, n):
+        w1, x1 = cf.config1()
+        r = Rot(dev, w1, ROTATE_BYTES)
+        xd, y = torch.from_numpy(x1).cuda(), torch.empty(6144, dtype=f32, device="cuda")
+        us = time_launches(dev, lambda i: ops.dispatch_q4mv(dev, r[i], xd, y), n)
+        return us, w1.nbytes + 2048 * 4 + 6144 * 4, None
+
+    def config2(dev, n):
+        w2, x2 = cf.config2()
+        r = Rot(dev, w2, ROTATE_BYTES)
+        xd, y = torch.from_numpy(x2).cuda(), torch.empty(2048, dtype=f32, device="cuda")
+        us = time_launches(dev, lambda i: ops.dispatch_qmv(dev, r[i], xd, y), n)
+        return us, w2.nbytes + 6144 * 4 + 2048 * 4, None
+
+    def config3(dev, n):
+        wg, wu, x3 = cf.config3()
+        rg, ru = Rot(dev, wg, ROTATE_BYTES // 2), Rot(dev, wu, ROTATE_BYTES // 2)
+        xd, y = torch.from_numpy(x3).cuda(), torch.empty(6144, dtype=f32, device="cuda")
+        us = time_launches(dev, lambda i: ops.dispatch_qmv_fused_pair_silu(dev, rg[i], ru[i], xd, y), n)
+        return us, wg.nbytes + wu.nbytes + 2048 * 4 + 6144 * 4, None
+
+    def dec_qkv(dev, n):
+        res_d, nw = act()
+        wq = cf.q1_matrix(QD, H, 128, 500, 501)
+        wk, wv = cf.q1_matrix(KVD, H, 128, 502, 503), cf.q1_matrix(KVD, H, 128, 504, 505)
+        rq = Rot(dev, wq, ROTATE_BYTES // 2)
+        rk, rv = Rot(dev, wk, ROTATE_BYTES // 4), Rot(dev, wv, ROTATE_BYTES // 4)
+        q = torch.empty(QD, dtype=f16, device="cuda")
+        k, v = torch.empty(KVD, dtype=f16, device="cuda"), torch.empty(KVD, dtype=f16, device="cuda")
+        us = time_launches(dev, lambda i: ops.dispatch_fused_norm_qkv_f16io(
+            dev, rq[i], rk[i], rv[i], res_d, q, k, v, nw), n)
+        return us, wq.nbytes + wk.nbytes + wv.nbytes + H * 8 + (QD + 2 * KVD) * 2, 28
+
+    def dec_attention(dev, n):
+        # one decode layer's attention: q/k norm + RoPE, KV append, attention
+        # over 640 tokens (the mean context of the timed steps), merge
+        seq, max_ctx = 640, 1024
+        kc = torch.randn(8, max_ctx, 128, device="cuda").to(f16)
+        vc = torch.randn(8, 128, max_ctx, device="cuda").to(f16)
+        qr = torch.randn(16 * 128, device="cuda").to(f16)
+        kr = torch.randn(8 * 128, device="cuda").to(f16)
+        vr = torch.randn(8 * 128, device="cuda").to(f16)
+        qn = torch.ones(128, dtype=f32, device="cuda")
+        att = torch.empty(16, 128, dtype=f16, device="cuda")
+        fd = L.GQAFusedDims(16, 8, 128, seq, max_ctx, 2, seq - 1, 1e-6, 1e6)
+        scr = torch.zeros(ops.gqa_scratch_bytes(L.GQADims(16, 8, 128, seq, max_ctx, 2)) // 4 + 64,
+                          dtype=f32, device="cuda")
+        us = time_launches(dev, lambda i: ops.dispatch_gqa_attention_fused_1pass(
+            dev, qr, kc, vc, att, kr, vr, qn, qn, scr, fd), n)
+        return us, 2 * 8 * seq * 128 * 2 + 16 * 128 * 4 + 8 * 128 * 8, 28
+
+    def dec_o(dev, n):
+        wo = cf.q1_matrix(H, QD, 128, 506, 507)
+        r = Rot(dev, wo, ROTATE_BYTES)
+        x16 = torch.randn(QD, dtype=f16, device="cuda") * 0.05
+        resid = torch.zeros(H, dtype=f32, device="cuda")
+        us = time_launches(dev, lambda i: ops.dispatch_qmv_f16io_resadd(dev, r[i], x16, resid), n)
+        return us, wo.nbytes + QD * 2 + H * 8, 28
+
+    def dec_gate_up(dev, n):
+        res_d, nw = act()
+        wg5, wu5 = cf.q1_matrix(I, H, 128, 508, 509), cf.q1_matrix(I, H, 128, 510, 511)
+        rg, ru = Rot(dev, wg5, ROTATE_BYTES // 2), Rot(dev, wu5, ROTATE_BYTES // 2)
+        h = torch.empty(I, dtype=f16, device="cuda")
+        us = time_launches(dev, lambda i: ops.dispatch_fused_norm_pair_silu_f16io(
+            dev, rg[i], ru[i], res_d, h, nw), n)
+        return us, wg5.nbytes + wu5.nbytes + H * 8 + I * 2, 28
+
+    def dec_down(dev, n):
+        wd = cf.q1_matrix(H, I, 128, 512, 513)
+        r = Rot(dev, wd, ROTATE_BYTES)
+        x16 = torch.randn(I, dtype=f16, device="cuda") * 0.05
+        resid = torch.zeros(H, dtype=f32, device="cuda")
+        us = time_launches(dev, lambda i: ops.dispatch_qmv_f16io_resadd(dev, r[i], x16, resid), n)
+        return us, wd.nbytes + I * 2 + H * 8, 28
+
+    def dec_lm_head(dev, n):
+        res_d, nw = act()
+        wl = cf.q1_matrix(V, H, 128, 514, 515)
+        r = Rot(dev, wl, ROTATE_BYTES)
+        logits = torch.empty(V, dtype=f32, device="cuda")
+        us = time_launches(dev, lambda i: ops.dispatch_fused_norm_qmv_f16in(
+            dev, r[i], res_d, logits, nw), max(16, n // 8))
+        return us, wl.nbytes + H * 8 + V * 4, 1
+
+    def config4(L_):
+        def run(dev, n):
+            kb = torch.randn(8, L_, 128, device="cuda").to(torch.bfloat16)
+            vb = torch.randn(8, L_, 128, device="cuda").to(torch.bfloat16)
+            qb = torch.randn(16, 128, device="cuda").to(torch.bfloat16)
+            ob = torch.empty(16, 128, dtype=f32, device="cuda")
+            d4 = L.GQADims(16, 8, 128, L_, L_, 2)
+            s4 = torch.empty(ops.gqa_scratch_bytes(d4) // 4 + 64, dtype=f32, device="cuda")
+            us = time_launches(dev, lambda i: ops.dispatch_gqa_attention(
+                dev, qb, kb, vb, ob, s4, d4, v_transposed=False, rope_position=L_,
+                rope_theta=1e6), max(16, n // 4))
+            return us, 4096 * L_ + 12288, None
+        return run
+
+    def copy_calib(dev, n):
+        # a plain device copy of known size: the scale for FETCH/WRITE_SIZE
+        a = torch.ones(64 << 20, dtype=f32, device="cuda")
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(8):
+            b.copy_(a)
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) * 1000.0 / 8, 2 * a.numel() * 4, None
+
+    return {
+        "config1_q4mv": config1, "config2_qmv": config2, "config3_gate_up_silu": config3,
+        "dec_qkv_norm": dec_qkv, "dec_attention_seq640": dec_attention,
+        "dec_o_resadd": dec_o, "dec_gate_up_norm_silu": dec_gate_up,
+        "dec_down_resadd": dec_down, "dec_lm_head_norm": dec_lm_head,
+        "config4_attention_L512": config4(512), "config4_attention_L4096": config4(4096),
+        "config4_attention_L32768": config4(32768), "copy_256MiB": copy_calib,
+    }
+
+
+def bench_kernels(dev, quick=False, only=None):
+    import torch
+
+    n_iter = 64 if quick else 256
+    cases = _kernel_cases()
+    names = [n for n in cases if n != "copy_256MiB"] if not only else only.split(",")
+    res = {}
+    for name in names:
+        us, nbytes, per_token = cases[name](dev, n_iter)
+        torch.cuda.synchronize()
         gbs = nbytes / (us * 1e-6) / 1e9
         res[name] = {"us": round(us, 3), "bytes": int(nbytes), "GBs": round(gbs, 1),
                      "frac": round(gbs / PEAK_HBM_GBS, 4)}
         if per_token is not None:
             res[name]["per_token"] = per_token
         log(f"{name:28s} {us:8.2f} us  {gbs:8.1f} GB/s  ({nbytes} B)")
-
-    f32, f16 = torch.float32, torch.float16
-    # config 1: Q4 W[6144 x 2048] gs64, f32 x/y
-    w1, x1 = cf.config1()
-    r = Rot(dev, w1, ROTATE_BYTES)
-    xd = torch.from_numpy(x1).cuda()
-    y = torch.empty(6144, dtype=f32, device="cuda")
-    torch.cuda.synchronize()
-    us = time_launches(dev, lambda i: ops.dispatch_q4mv(dev, r[i], xd, y), n_iter)
-    rec("config1_q4mv", us, w1.nbytes + 2048 * 4 + 6144 * 4)
-    del r
-    # config 2: Q1 W[2048 x 6144] gs128, f32 x/y
-    w2, x2 = cf.config2()
-    r = Rot(dev, w2, ROTATE_BYTES)
-    xd = torch.from_numpy(x2).cuda()
-    y = torch.empty(2048, dtype=f32, device="cuda")
-    torch.cuda.synchronize()
-    us = time_launches(dev, lambda i: ops.dispatch_qmv(dev, r[i], xd, y), n_iter)
-    rec("config2_qmv", us, w2.nbytes + 6144 * 4 + 2048 * 4)
-    del r
-    # config 3: fused gate/up + SiLU (f32 I/O)
-    wg, wu, x3 = cf.config3()
-    rg, ru = Rot(dev, wg, ROTATE_BYTES // 2), Rot(dev, wu, ROTATE_BYTES // 2)
-    xd = torch.from_numpy(x3).cuda()
-    y = torch.empty(6144, dtype=f32, device="cuda")
-    torch.cuda.synchronize()
-    us = time_launches(dev, lambda i: ops.dispatch_qmv_fused_pair_silu(dev, rg[i], ru[i], xd, y), n_iter)
-    rec("config3_gate_up_silu", us, wg.nbytes + wu.nbytes + 2048 * 4 + 6144 * 4)
-    del rg, ru
-
-    # decode-step kernels at config-5 shapes (counts per token in parentheses)
-    H, I, QD, KVD, V = 2048, 6144, 2048, 1024, 151936
-    res_d = torch.from_numpy(np.random.default_rng(0).standard_normal(H).astype(np.float32)).cuda()
-    nw = torch.ones(H, dtype=f32, device="cuda")
-    x16 = torch.randn(I, dtype=f16, device="cuda") * 0.05
-    o16a = torch.empty(I, dtype=f16, device="cuda")
-    o16b = torch.empty(I, dtype=f16, device="cuda")
-    resid = torch.zeros(H, dtype=f32, device="cuda")
-
-    wq = cf.q1_matrix(QD, H, 128, 500, 501)
-    r = Rot(dev, wq, ROTATE_BYTES)
-    torch.cuda.synchronize()
-    us = time_launches(dev, lambda i: ops.dispatch_fused_norm_qmv_f16io(dev, r[i], res_d, o16a, nw), n_iter)
-    rec("dec_q_norm_qmv", us, wq.nbytes + H * 8 + QD * 2, per_token=28)
-    del r
-    wk, wv = cf.q1_matrix(KVD, H, 128, 502, 503), cf.q1_matrix(KVD, H, 128, 504, 505)
-    rk, rv = Rot(dev, wk, ROTATE_BYTES // 2), Rot(dev, wv, ROTATE_BYTES // 2)
-    torch.cuda.synchronize()
-    us = time_launches(dev, lambda i: ops.dispatch_fused_norm_pair_qmv_f16io(
-        dev, rk[i], rv[i], res_d, o16a, o16b, nw), n_iter)
-    rec("dec_kv_norm_pair", us, wk.nbytes + wv.nbytes + H * 8 + KVD * 4, per_token=28)
-    del rk, rv
-    wo = cf.q1_matrix(H, QD, 128, 506, 507)
-    r = Rot(dev, wo, ROTATE_BYTES)
-    torch.cuda.synchronize()
-    us = time_launches(dev, lambda i: ops.dispatch_qmv_f16io_resadd(dev, r[i], x16[:QD], resid), n_iter)
-    rec("dec_o_resadd", us, wo.nbytes + QD * 2 + H * 8, per_token=28)
-    del r
-    wg5, wu5 = cf.q1_matrix(I, H, 128, 508, 509), cf.q1_matrix(I, H, 128, 510, 511)
-    rg, ru = Rot(dev, wg5, ROTATE_BYTES // 2), Rot(dev, wu5, ROTATE_BYTES // 2)
-    torch.cuda.synchronize()
-    us = time_launches(dev, lambda i: ops.dispatch_fused_norm_pair_silu_f16io(
-        dev, rg[i], ru[i], res_d, o16a, nw), n_iter)
-    rec("dec_gate_up_norm_silu", us, wg5.nbytes + wu5.nbytes + H * 8 + I * 2, per_token=28)
-    del rg, ru
-    wd = cf.q1_matrix(H, I, 128, 512, 513)
-    r = Rot(dev, wd, ROTATE_BYTES)
-    torch.cuda.synchronize()
-    us = time_launches(dev, lambda i: ops.dispatch_qmv_f16io_resadd(dev, r[i], x16, resid), n_iter)
-    rec("dec_down_resadd", us, wd.nbytes + I * 2 + H * 8, per_token=28)
-    del r
-    wl = cf.q1_matrix(V, H, 128, 514, 515)
-    r = Rot(dev, wl, ROTATE_BYTES)
-    logits = torch.empty(V, dtype=f32, device="cuda")
-    torch.cuda.synchronize()
-    us = time_launches(dev, lambda i: ops.dispatch_qmv_f16in(dev, r[i], x16[:H], logits),
-                       max(16, n_iter // 8))
-    rec("dec_lm_head_q1", us, wl.nbytes + H * 2 + V * 4, per_token=1)
-    del r
-    # attention over the average decode context of the timed steps (640)
-    seq, max_ctx = 640, 1024
-    kc = torch.randn(8, max_ctx, 128, device="cuda").to(f16)
-    vc = torch.randn(8, 128, max_ctx, device="cuda").to(f16)
-    qf = torch.randn(16, 128, device="cuda")
-    att = torch.empty(16, 128, dtype=f16, device="cuda")
-    dims = L.GQADims(16, 8, 128, seq, max_ctx, 2)
-    scr = torch.empty(ops.gqa_scratch_bytes(dims) // 4 + 64, dtype=f32, device="cuda")
-    torch.cuda.synchronize()
-    us = time_launches(dev, lambda i: ops.dispatch_gqa_attention(dev, qf, kc, vc, att, scr, dims), n_iter)
-    rec("dec_attention_seq640", us, 2 * 8 * seq * 128 * 2 + 16 * 128 * 6, per_token=28)
-    # config 4 (attention, bf16 KV [8, L, 128], q roped at L)
-    for L_ in (512, 4096, 32768):
-        kb = torch.randn(8, L_, 128, device="cuda").to(torch.bfloat16)
-        vb = torch.randn(8, L_, 128, device="cuda").to(torch.bfloat16)
-        qb = torch.randn(16, 128, device="cuda").to(torch.bfloat16)
-        ob = torch.empty(16, 128, dtype=f32, device="cuda")
-        d4 = L.GQADims(16, 8, 128, L_, L_, 2)
-        s4 = torch.empty(ops.gqa_scratch_bytes(d4) // 4 + 64, dtype=f32, device="cuda")
-        torch.cuda.synchronize()
-        us = time_launches(dev, lambda i: ops.dispatch_gqa_attention(
-            dev, qb, kb, vb, ob, s4, d4, v_transposed=False, rope_position=L_, rope_theta=1e6),
-            max(16, n_iter // 4))
-        rec(f"config4_attention_L{L_}", us, 4096 * L_ + 12288)
-        del kb, vb
     return res
 
 
@@ -264,7 +300,7 @@ def cpu_baseline(sample_layers=2, tokens=3):
 
     cfg = cf.DecoderConfig(**{**cf.BONSAI_1_7B.__dict__, "num_layers": sample_layers,
                               "max_context_length": 1024})
-    w = cf.decoder_weights(cfg, norm_mode="small")
+    w = cf.decoder_weights(cfg, norm_mode="small", host_embed=False)
     od = OracleDecoder(w)
     prompt = cf.prompt_ids(cfg, 64)
     od.forward(list(prompt), 0)
@@ -296,6 +332,10 @@ def main():
     ap.add_argument("--quick", action="store_true", help="fewer kernel timing iterations")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-kernels", action="store_true")
+    ap.add_argument("--skip-decode", action="store_true",
+                    help="kernel timings only (profiling runs); no JSON line")
+    ap.add_argument("--only", default=None,
+                    help="comma-separated kernel cases to time (e.g. for --pmc runs)")
     ap.add_argument("--details", default=None, help="write the full result dict here")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -310,9 +350,12 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = Device(0, own_stream=True)
     log(f"device: {torch.cuda.get_device_name(0)}")
+    if args.skip_decode:
+        bench_kernels(dev, quick=args.quick, only=args.only)
+        return
     dec = bench_decode(args, dev)
     log(f"decode: {dec['tok_s']:.1f} tok/s ({dec['ms_per_step']:.3f} ms/step)")
-    kern = {} if args.skip_kernels else bench_kernels(dev, quick=args.quick)
+    kern = {} if args.skip_kernels else bench_kernels(dev, quick=args.quick, only=args.only)
 
     roofline = None
     dec_k = {k: v for k, v in kern.items() if "per_token" in v}

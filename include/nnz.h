@@ -190,6 +190,21 @@ int nnz_dispatch_fused_norm_pair_qmv_f16io(nnz_ctx *ctx, const nnz_qweight *wa,
                                            void *output_a, void *output_b,
                                            const float *norm_scale, nnz_qmv_dims dims);
 
+/* One launch for the pair transformer.zig:1438 dispatchFusedNormQMVf16io (Q)
+ * + :1501 dispatchFusedNormPairQMVf16io (K, V), which share the normalised
+ * input (encodeAttnProjFusedNorm, :3024-3083).  q_dims = {Q rows, K, gs};
+ * wk and wv have kv_rows rows each. */
+int nnz_dispatch_fused_norm_qkv_f16io(nnz_ctx *ctx, const nnz_qweight *wq, const nnz_qweight *wk,
+                                      const nnz_qweight *wv, const float *residual, void *out_q,
+                                      void *out_k, void *out_v, const float *norm_scale,
+                                      nnz_qmv_dims q_dims, uint32_t kv_rows);
+/* One launch for transformer.zig:669 dispatchRMSNorm (rms_norm_f16out) +
+ * :1653 dispatchQMVf16in, the final norm + LM head (encodeFinalNormAndLMHead,
+ * :2730-2785): the normalised input is rounded to f16 exactly as the
+ * reference stores it, logits are f32. */
+int nnz_dispatch_fused_norm_qmv_f16in(nnz_ctx *ctx, const nnz_qweight *w, const float *residual,
+                                      float *output, const float *norm_scale, nnz_qmv_dims dims);
+
 /* ---- QMV family, Q4 (4-bit affine) ------------------------------------- */
 /* Q4 entry points require bits == 4, K % 32 == 0, group_size % 32 == 0 and
  * K % group_size == 0.  The `*_f16io*` / `_f16in` forms reproduce the
@@ -314,6 +329,20 @@ int nnz_dispatch_gqa_attention_fused(nnz_ctx *ctx, const void *q, void *k_cache,
                                      const float *q_norm_scale, const float *k_norm_scale,
                                      void *scratch, size_t scratch_bytes,
                                      nnz_gqa_fused_dims dims);
+
+/* transformer.zig:962 dispatchGQAAttentionFusedTG again, for graph replay:
+ * the same math as nnz_dispatch_gqa_attention_fused with the norm, RoPE,
+ * cache append and attention in ONE kernel (plus a merge kernel when the
+ * sequence spans several chunks).  Calls sharing one scratch must not
+ * overlap.  If `d_seq_len` is non-NULL it points to a device uint32 holding
+ * position + 1, read at run time (dims.seq_len is then the largest value it
+ * may hold and sizes the launch); otherwise seq_len must be position + 1. */
+int nnz_dispatch_gqa_attention_fused_1pass(nnz_ctx *ctx, const void *q, void *k_cache,
+                                           void *v_cache, void *output, const void *k_raw,
+                                           const void *v_raw, const float *q_norm_scale,
+                                           const float *k_norm_scale, void *scratch,
+                                           size_t scratch_bytes, const uint32_t *d_seq_len,
+                                           nnz_gqa_fused_dims dims);
 
 /* transformer.zig:1072 dispatchEmbeddingLookup (Q1 table, f32 out). */
 int nnz_dispatch_embedding_lookup(nnz_ctx *ctx, const uint32_t *token_ids, const void *packed_bits,

@@ -117,6 +117,9 @@ PROTOS = {
     "nnz_dispatch_fused_norm_pair_silu_f16io": (C.c_int, [vp, QW, QW, vp, vp, vp, QMVDims]),
     "nnz_dispatch_fused_norm_qmv_f16io": (C.c_int, [vp, QW, vp, vp, vp, QMVDims]),
     "nnz_dispatch_fused_norm_pair_qmv_f16io": (C.c_int, [vp, QW, QW, vp, vp, vp, vp, QMVDims]),
+    "nnz_dispatch_fused_norm_qkv_f16io": (C.c_int, [vp, QW, QW, QW, vp, vp, vp, vp, vp, QMVDims,
+                                                    u32]),
+    "nnz_dispatch_fused_norm_qmv_f16in": (C.c_int, [vp, QW, vp, vp, vp, QMVDims]),
     # Q4
     "nnz_dispatch_q4mv": (C.c_int, [vp, QW, vp, vp, QMVDims]),
     "nnz_dispatch_q4mv_f16io": (C.c_int, [vp, QW, vp, vp, QMVDims]),
@@ -145,6 +148,8 @@ PROTOS = {
                                              C.c_int, vp, sz, i32, f32, GQADims]),
     "nnz_dispatch_gqa_attention_fused": (C.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz,
                                                    GQAFusedDims]),
+    "nnz_dispatch_gqa_attention_fused_1pass": (C.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
+                                                         sz, vp, GQAFusedDims]),
     "nnz_dispatch_embedding_lookup": (C.c_int, [vp, vp, vp, vp, vp, EmbedDims]),
     "nnz_dispatch_embedding_lookup_q4": (C.c_int, [vp, vp, vp, vp, vp, vp, EmbedDims]),
     "nnz_dispatch_embedding_lookup_bf16": (C.c_int, [vp, vp, vp, vp, EmbedDims]),

@@ -143,10 +143,15 @@ def norm_weights(seed: int, n: int, mode: str) -> np.ndarray:
     return S.bf16_bits_to_f32(S.f64_to_bf16_bits(z)).astype(np.float32)
 
 
-def decoder_weights(cfg: DecoderConfig, norm_mode: str = "small") -> DecoderWeights:
+def decoder_weights(cfg: DecoderConfig, norm_mode: str = "small",
+                    host_embed: bool = True) -> DecoderWeights:
+    """All weights of the synthetic decoder.  With ``host_embed=False`` the
+    bf16 embedding table is left out (the GPU generates it from the same
+    stream, nnz_synth_normal_bf16; the oracle regenerates single rows)."""
     dw = DecoderWeights(cfg)
     V, H = cfg.vocab_size, cfg.hidden_size
-    dw.embed_bf16 = S.f64_to_bf16_bits(0.02 * S.normal(S.SEED_MODEL_BASE + 0, V * H)).reshape(V, H)
+    if host_embed or cfg.lm_head_kind == 1:
+        dw.embed_bf16 = S.f64_to_bf16_bits(0.02 * S.normal(S.SEED_MODEL_BASE + 0, V * H)).reshape(V, H)
     if cfg.lm_head_kind == 0:
         dw.lm_head = q1_matrix(V, H, cfg.group_size, S.SEED_MODEL_BASE + 1, S.SEED_MODEL_BASE + 2)
     dw.final_norm = norm_weights(S.SEED_MODEL_BASE + 3, H, norm_mode)

@@ -25,6 +25,7 @@ struct NnzAttnCall {
 };
 
 uint32_t nnz_attn_chunk(uint32_t seq_len, uint32_t hkv);
+uint32_t nnz_attn_fused_chunk(uint32_t max_seq, uint32_t hkv);
 int nnz_attn_launch_ex(nnz_ctx *ctx, const NnzAttnCall &c);
 int nnz_attn_prep_launch(nnz_ctx *ctx, const void *q, const void *kr, const void *vr,
                          const float *qn, const float *kn, float *qout, void *kc, void *vc,
@@ -32,5 +33,15 @@ int nnz_attn_prep_launch(nnz_ctx *ctx, const void *q, const void *kr, const void
                          const uint32_t *d_pos, uint32_t nq, uint32_t max_ctx, float eps,
                          float theta);
 int nnz_argmax_launch(nnz_ctx *ctx, const float *x, uint32_t n, uint32_t *oi, float *ov);
+int nnz_attn_fused1_launch(nnz_ctx *ctx, const void *q, const void *kr, const void *vr,
+                           const float *qn, const float *kn, void *kc, void *vc, void *out,
+                           float *part_o, float *part_ml, const uint32_t *d_seq, uint32_t max_seq, uint32_t hq, uint32_t hkv,
+                           uint32_t head_dim, uint32_t max_ctx, float eps, float theta);
+int nnz_qmv_norm_qkv_launch(nnz_ctx *ctx, const nnz_qweight *wq, const nnz_qweight *wk,
+                            const nnz_qweight *wv, const float *residual, const float *norm_w,
+                            void *q, void *k, void *v, uint32_t qrows, uint32_t kvrows, uint32_t K,
+                            uint32_t gs);
+int nnz_qmv_norm_f32out_launch(nnz_ctx *ctx, const nnz_qweight *w, const float *residual,
+                               const float *norm_w, float *out, nnz_qmv_dims d);
 int nnz_gemm_launch(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, const void *a,
                     uint32_t P, void *out, int mode, const nnz_qmv_dims &d);

@@ -135,40 +135,61 @@ __global__ __launch_bounds__(256) void dense_bf16_gemv_kernel(const uint16_t *E,
     }
 }
 
-// Greedy step: argmax (first maximum wins, transformer.zig:3694-3707), record
-// the token and its top-2 margin, then advance token/position/step.
-__global__ __launch_bounds__(1024) void argmax_advance_kernel(const float *x, uint32_t n,
-                                                              uint32_t *state, uint32_t *tokens,
-                                                              float *margins, uint32_t cap) {
-    __shared__ float sv[1024], sv2[1024];
-    __shared__ uint32_t si[1024];
-    float best = -INFINITY, second = -INFINITY;
-    uint32_t bi = 0xFFFFFFFFu;
-    for (uint32_t i = threadIdx.x; i < n; i += 1024) {
-        const float v = x[i];
-        if (v > best) { second = best; best = v; bi = i; }
-        else if (v > second) second = v;
-    }
-    sv[threadIdx.x] = best; sv2[threadIdx.x] = second; si[threadIdx.x] = bi;
+// Greedy sampling, two passes (argmax: first maximum wins, NaN never wins,
+// transformer.zig:3694-3707).  Pass 1: ARGMAX_BLOCKS blocks reduce strided
+// slices to (best, runner-up, index) partials.  Pass 2: one block merges
+// them, records the token and its top-2 margin, and advances the state.
+constexpr int ARGMAX_BLOCKS = 256;
+
+struct Top2 {
+    float best, second;
+    uint32_t idx;
+};
+
+__device__ __forceinline__ Top2 top2_merge(Top2 a, Top2 b) {
+    const bool take_b = (b.best > a.best) || (b.best == a.best && b.idx < a.idx);
+    Top2 r;
+    r.best = take_b ? b.best : a.best;
+    r.idx = take_b ? b.idx : a.idx;
+    r.second = fmaxf(fmaxf(a.second, b.second), take_b ? a.best : b.best);
+    return r;
+}
+
+__device__ __forceinline__ Top2 block_top2_256(Top2 t, Top2 *sh) {
+    sh[threadIdx.x] = t;
     __syncthreads();
-    for (uint32_t s = 512; s > 0; s >>= 1) {
-        if (threadIdx.x < s) {
-            const float a = sv[threadIdx.x], b = sv[threadIdx.x + s];
-            const uint32_t ia = si[threadIdx.x], ib = si[threadIdx.x + s];
-            const bool take_b = (b > a) || (b == a && ib < ia);
-            const float lo = take_b ? a : b;
-            sv2[threadIdx.x] = fmaxf(fmaxf(sv2[threadIdx.x], sv2[threadIdx.x + s]), lo);
-            sv[threadIdx.x] = take_b ? b : a;
-            si[threadIdx.x] = take_b ? ib : ia;
-        }
+    for (uint32_t s = 128; s > 0; s >>= 1) {
+        if (threadIdx.x < s) sh[threadIdx.x] = top2_merge(sh[threadIdx.x], sh[threadIdx.x + s]);
         __syncthreads();
     }
+    return sh[0];
+}
+
+__global__ __launch_bounds__(256) void argmax_partial_kernel(const float *x, uint32_t n, Top2 *part) {
+    __shared__ Top2 sh[256];
+    Top2 t{-INFINITY, -INFINITY, 0xFFFFFFFFu};
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += ARGMAX_BLOCKS * 256) {
+        const float v = x[i];
+        if (v > t.best) { t.second = t.best; t.best = v; t.idx = i; }
+        else if (v > t.second) t.second = v;
+    }
+    const Top2 r = block_top2_256(t, sh);
+    if (threadIdx.x == 0) part[blockIdx.x] = r;
+}
+
+__global__ __launch_bounds__(256) void argmax_final_advance_kernel(const Top2 *part, uint32_t *state,
+                                                                   uint32_t *tokens, float *margins,
+                                                                   uint32_t cap) {
+    __shared__ Top2 sh[256];
+    Top2 t{-INFINITY, -INFINITY, 0xFFFFFFFFu};
+    for (uint32_t i = threadIdx.x; i < (uint32_t)ARGMAX_BLOCKS; i += 256) t = top2_merge(t, part[i]);
+    const Top2 r = block_top2_256(t, sh);
     if (threadIdx.x == 0) {
-        const uint32_t tok = si[0] == 0xFFFFFFFFu ? 0u : si[0];
+        const uint32_t tok = r.idx == 0xFFFFFFFFu ? 0u : r.idx;
         const uint32_t step = state[ST_STEP];
         if (step < cap) {
             tokens[step] = tok;
-            margins[step] = sv[0] - sv2[0];
+            margins[step] = r.best - r.second;
         }
         state[ST_TOKEN] = tok;
         state[ST_POS] += 1;
@@ -204,6 +225,7 @@ struct nnz_model {
     f16_t *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *h = nullptr;
     float *part_o = nullptr, *part_ml = nullptr;
     uint32_t part_chunks = 0;  // capacity in chunks per query head
+    Top2 *top2 = nullptr;          // [ARGMAX_BLOCKS] argmax partials
     uint32_t *state = nullptr;
     uint32_t *tokens_out = nullptr;
     float *margins_out = nullptr;
@@ -294,10 +316,11 @@ int lm_head(nnz_model *m, const f16_t *x, float *logits) {
         if (rc_) return rc_;   \
     } while (0)
 
-// One decode step for the token/position held in the device state block.
-// `chunk`/`nchunks` fix the attention grid for every position this step may
-// be replayed at (sequence length up to chunk * nchunks).
-int enqueue_decode_step(nnz_model *m, uint32_t chunk, uint32_t nchunks) {
+// One decode step for the token/position held in the device state block:
+// per layer 5 launches (norm+QKV, fused attention, O +=, norm+gate/up+SiLU,
+// down +=), then norm+LM head.  `max_seq` sizes the attention grid for every
+// position this step may be replayed at.
+int enqueue_decode_step(nnz_model *m, uint32_t max_seq) {
     nnz_ctx *ctx = m->ctx;
     const nnz_model_config &c = m->c;
     const uint32_t H = c.hidden_size;
@@ -312,48 +335,45 @@ int enqueue_decode_step(nnz_model *m, uint32_t chunk, uint32_t nchunks) {
 
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         Layer &Ly = m->L[l];
-        // transformer.zig:3024-3083 encodeAttnProjFusedNorm
-        RC(nnz_dispatch_fused_norm_qmv_f16io(ctx, &Ly.q.w, m->residual, m->q, Ly.attn_norm,
-                                             dims_of(m, Ly.q)));
-        RC(nnz_dispatch_fused_norm_pair_qmv_f16io(ctx, &Ly.k.w, &Ly.v.w, m->residual, m->k, m->v,
-                                                  Ly.attn_norm, dims_of(m, Ly.k)));
-        // transformer.zig:3244-3370 encodeAttentionGather (fused Q/K norm, RoPE,
-        // KV append, attention), then O-proj with residual +=.
-        RC(nnz_attn_prep_launch(ctx, m->q, m->k, m->v, Ly.q_norm, Ly.k_norm, m->qf, Ly.kc, Ly.vc,
-                                c.num_query_heads, c.num_kv_heads, c.head_dim, 0,
-                                m->state + ST_POS, 1, c.max_context_length, c.rms_eps,
-                                c.rope_theta));
-        NnzAttnCall ac{};
-        ac.q = m->qf;
-        ac.qdt = NNZ_F32;
-        ac.kc = Ly.kc;
-        ac.vc = Ly.vc;
-        ac.kvdt = NNZ_F16;
-        ac.vt = true;
-        ac.out = m->att;
-        ac.odt = NNZ_F16;
-        ac.part_o = m->part_o;
-        ac.part_ml = m->part_ml;
-        ac.d_seq = m->state + ST_SEQ;
-        ac.chunk = chunk;
-        ac.nchunks = nchunks;
-        ac.nq = 1;
-        ac.dims = gqa_dims(m, 0);
-        RC(nnz_attn_launch_ex(ctx, ac));
+        // transformer.zig:3024-3083 encodeAttnProjFusedNorm: the Q and the K/V
+        // dispatches share one normalised input -> one launch here.
+        RC(nnz_qmv_norm_qkv_launch(ctx, &Ly.q.w, &Ly.k.w, &Ly.v.w, m->residual, Ly.attn_norm, m->q,
+                                   m->k, m->v, m->qdim, m->kvdim, H, c.group_size));
+        // transformer.zig:3244-3370 encodeAttentionGather: Q/K norm, RoPE, KV
+        // append and attention in one launch, then O-proj with residual +=.
+        RC(nnz_attn_fused1_launch(ctx, m->q, m->k, m->v, Ly.q_norm, Ly.k_norm, Ly.kc, Ly.vc, m->att,
+                                  m->part_o, m->part_ml, m->state + ST_SEQ, max_seq,
+                                  c.num_query_heads, c.num_kv_heads, c.head_dim,
+                                  c.max_context_length, c.rms_eps, c.rope_theta));
         RC(nnz_dispatch_qmv_f16io_resadd(ctx, &Ly.o.w, m->att, m->residual, dims_of(m, Ly.o)));
         // transformer.zig:3372-3646 encodeMLPHalf (fused norm + gate/up + SiLU, down += )
         RC(nnz_dispatch_fused_norm_pair_silu_f16io(ctx, &Ly.gate.w, &Ly.up.w, m->residual, m->h,
                                                    Ly.ffn_norm, dims_of(m, Ly.gate)));
         RC(nnz_dispatch_qmv_f16io_resadd(ctx, &Ly.down.w, m->h, m->residual, dims_of(m, Ly.down)));
     }
-    // transformer.zig:2730-2785 encodeFinalNormAndLMHead
+    // transformer.zig:2730-2785 encodeFinalNormAndLMHead (norm fused into the
+    // 1-bit LM head; the tied bf16 head keeps a separate norm)
+    if (c.lm_head_kind == NNZ_LMHEAD_Q1)
+        return nnz_qmv_norm_f32out_launch(ctx, &m->lm.w, m->residual, m->final_norm, m->logits,
+                                          dims_of(m, m->lm));
     RC(nnz_dispatch_rms_norm(ctx, m->residual, m->final_norm, m->xn, NNZ_F16, 0,
                              {H, 1, c.rms_eps}));
     return lm_head(m, m->xn, m->logits);
 }
 
+// Greedy sampling of the logits into the state block (two passes).
+int enqueue_argmax_advance(nnz_model *m) {
+    argmax_partial_kernel<<<ARGMAX_BLOCKS, 256, 0, m->ctx->stream>>>(m->logits, m->c.vocab_size,
+                                                                     m->top2);
+    NNZ_LAUNCHED(m->ctx);
+    argmax_final_advance_kernel<<<1, 256, 0, m->ctx->stream>>>(m->top2, m->state, m->tokens_out,
+                                                               m->margins_out, m->out_cap);
+    NNZ_LAUNCHED(m->ctx);
+    return NNZ_OK;
+}
+
 void decode_plan(const nnz_model *m, uint32_t max_seq, uint32_t *chunk, uint32_t *nch) {
-    *chunk = nnz_attn_chunk(max_seq, m->c.num_kv_heads);
+    *chunk = nnz_attn_fused_chunk(max_seq, m->c.num_kv_heads);
     *nch = ceil_div(max_seq, *chunk);
 }
 
@@ -467,6 +487,7 @@ int nnz_model_create(nnz_ctx *ctx, const nnz_model_config *cfg, nnz_model **out)
         MALLOC(parts, (size_t)c.num_query_heads * m->part_chunks * (c.head_dim + 2) * 4);
         m->part_o = parts;
         m->part_ml = parts + (size_t)c.num_query_heads * m->part_chunks * c.head_dim;
+        MALLOC(m->top2, (size_t)ARGMAX_BLOCKS * sizeof(Top2));
         MALLOC(m->state, 64);
         m->out_cap = c.max_context_length + 1;
         MALLOC(m->tokens_out, (size_t)m->out_cap * 4);
@@ -553,9 +574,7 @@ int nnz_model_forward_decode(nnz_model *m, uint32_t token_id, uint32_t position)
     const uint32_t st[4] = {token_id, position, position + 1, 0};
     NNZ_HIP(ctx, hipMemcpyAsync(m->state, st, sizeof(st), hipMemcpyHostToDevice, ctx->stream));
     NNZ_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    uint32_t chunk, nch;
-    decode_plan(m, position + 1, &chunk, &nch);
-    return enqueue_decode_step(m, chunk, nch);
+    return enqueue_decode_step(m, position + 1);
 }
 
 int nnz_model_prefill(nnz_model *m, const uint32_t *tokens_host, uint32_t n, uint32_t start) {
@@ -625,9 +644,9 @@ int nnz_model_prefill(nnz_model *m, const uint32_t *tokens_host, uint32_t n, uin
 namespace {
 
 // Prefill the prompt (in max_prefill_length batches), take the greedy first
-// token into the state block and pick the attention plan for max_new steps.
+// token into the state block; *max_seq = longest sequence of the plan.
 int begin_decode(nnz_model *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t max_new,
-                 uint32_t *chunk, uint32_t *nch) {
+                 uint32_t *max_seq) {
     nnz_ctx *ctx = m->ctx;
     const nnz_model_config &c = m->c;
     NNZ_REQUIRE(ctx, prompt && n_prompt > 0 && max_new > 0, NNZ_EINVAL, "decode: bad arguments");
@@ -642,27 +661,24 @@ int begin_decode(nnz_model *m, const uint32_t *prompt, uint32_t n_prompt, uint32
     // moves to (t0, n_prompt, n_prompt + 1, 1).
     const uint32_t st[4] = {0, n_prompt - 1, n_prompt, 0};
     NNZ_HIP(ctx, hipMemcpyAsync(m->state, st, sizeof(st), hipMemcpyHostToDevice, ctx->stream));
-    argmax_advance_kernel<<<1, 1024, 0, ctx->stream>>>(m->logits, c.vocab_size, m->state,
-                                                       m->tokens_out, m->margins_out, m->out_cap);
-    NNZ_LAUNCHED(ctx);
-    decode_plan(m, n_prompt + max_new, chunk, nch);
-    NNZ_REQUIRE(ctx, *nch <= m->part_chunks, NNZ_EINVAL, "decode: attention plan exceeds scratch");
+    RC(enqueue_argmax_advance(m));
+    *max_seq = n_prompt + max_new;
+    uint32_t chunk, nch;
+    decode_plan(m, *max_seq, &chunk, &nch);
+    NNZ_REQUIRE(ctx, nch <= m->part_chunks, NNZ_EINVAL, "decode: attention plan exceeds scratch");
     return NNZ_OK;
 }
 
 // One greedy decode step: forwardDecode of the state's token, then argmax
 // and state advance.  Graph-capturable (no host data, no allocation).
-int greedy_step(nnz_model *m, uint32_t chunk, uint32_t nch) {
-    RC(enqueue_decode_step(m, chunk, nch));
-    argmax_advance_kernel<<<1, 1024, 0, m->ctx->stream>>>(m->logits, m->c.vocab_size, m->state,
-                                                          m->tokens_out, m->margins_out, m->out_cap);
-    NNZ_LAUNCHED(m->ctx);
-    return NNZ_OK;
+int greedy_step(nnz_model *m, uint32_t max_seq) {
+    RC(enqueue_decode_step(m, max_seq));
+    return enqueue_argmax_advance(m);
 }
 
-int capture_step(nnz_model *m, uint32_t chunk, uint32_t nch, nnz_graph **g) {
+int capture_step(nnz_model *m, uint32_t max_seq, nnz_graph **g) {
     RC(nnz_graph_begin(m->ctx));
-    const int brc = greedy_step(m, chunk, nch);
+    const int brc = greedy_step(m, max_seq);
     const int erc = nnz_graph_end(m->ctx, g);
     return brc ? brc : erc;
 }
@@ -676,8 +692,8 @@ int nnz_model_generate(nnz_model *m, const uint32_t *prompt, uint32_t n_prompt, 
     if (!m) return NNZ_EINVAL;
     nnz_ctx *ctx = m->ctx;
     NNZ_REQUIRE(ctx, out_tokens, NNZ_EINVAL, "generate: null output");
-    uint32_t chunk, nch;
-    RC(begin_decode(m, prompt, n_prompt, n_new, &chunk, &nch));
+    uint32_t max_seq;
+    RC(begin_decode(m, prompt, n_prompt, n_new, &max_seq));
     std::vector<hipEvent_t> ev;
     int rc = NNZ_OK;
     if (out_step_ms) {
@@ -688,10 +704,10 @@ int nnz_model_generate(nnz_model *m, const uint32_t *prompt, uint32_t n_prompt, 
     // The reference decodes every emitted token (transformer.zig:3982-4016):
     // n_new forward passes for n_new output tokens.
     nnz_graph *g = nullptr;
-    if (!rc && use_graph) rc = capture_step(m, chunk, nch, &g);
+    if (!rc && use_graph) rc = capture_step(m, max_seq, &g);
     if (!rc && out_step_ms && hipEventRecord(ev[0], ctx->stream) != hipSuccess) rc = NNZ_EHIP;
     for (uint32_t i = 0; i < n_new && !rc; ++i) {
-        rc = use_graph ? nnz_graph_replay(ctx, g) : greedy_step(m, chunk, nch);
+        rc = use_graph ? nnz_graph_replay(ctx, g) : greedy_step(m, max_seq);
         if (!rc && out_step_ms && hipEventRecord(ev[i + 1], ctx->stream) != hipSuccess) rc = NNZ_EHIP;
     }
     if (!rc) rc = nnz_stream_sync(ctx, 600000);
@@ -708,9 +724,9 @@ int nnz_model_decode_begin(nnz_model *m, const uint32_t *prompt, uint32_t n_prom
                            uint32_t max_new) {
     if (!m) return NNZ_EINVAL;
     NNZ_REQUIRE(m->ctx, !m->step_graph, NNZ_ESTATE, "decode_begin: a decode stream is active");
-    uint32_t chunk, nch;
-    RC(begin_decode(m, prompt, n_prompt, max_new, &chunk, &nch));
-    RC(capture_step(m, chunk, nch, &m->step_graph));
+    uint32_t max_seq;
+    RC(begin_decode(m, prompt, n_prompt, max_new, &max_seq));
+    RC(capture_step(m, max_seq, &m->step_graph));
     m->stream_steps_left = max_new;
     return NNZ_OK;
 }

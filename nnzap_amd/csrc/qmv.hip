@@ -17,10 +17,15 @@
 //     floats) is loaded once into VGPRs, together with the per-unit sums of x,
 //     and reused for every row the wave processes.  No LDS is used: the
 //     RMSNorm prologue is a lane-group reduction in registers.
-//   * Each lane keeps R row-steps of weight loads in flight.  Lanes of a row
-//     read adjacent words, so every load instruction is a contiguous,
-//     coalesced segment of the row.
-//   * Row sums are reduced across the LPR lanes with cross-lane shuffles.
+//   * Latency: the weight loads of the first row-step are issued before the
+//     x / RMSNorm prologue (they do not depend on it), and the row loop is
+//     software-pipelined -- the next step's loads are in flight while the
+//     current step computes -- so a small matrix costs about one memory round
+//     trip instead of two per step.  Lanes of a row read adjacent words, so
+//     every load instruction is one contiguous, coalesced segment of a row.
+//   * Rows may be split into up to three segments with their own matrix and
+//     output (same K): the Q, K and V projections of a layer run as one
+//     launch sharing the normalised input.
 //
 // Q1 arithmetic: sum_c (bit ? +x_c : -x_c) = 2 * sum_{bit=1} x_c - sum_c x_c,
 // computed per 32-column unit with a sign-extended bit mask ANDed into x
@@ -28,24 +33,154 @@
 // Q4 arithmetic: acc += s * sum(n_i x_i) + b * sum(x_i) per unit
 // (q4mv_bf16_specialized.metal:14-16), nibbles widened with the byte
 // converts after splitting even/odd nibbles.
-#include "common.h"
+#include "internal.h"
 
 namespace {
 
 enum { EPI_STORE = 0, EPI_RESADD = 1, EPI_SILU = 2 };
 
+constexpr int MAX_SEG = 3;
+
 struct QmvArgs {
-    const uint32_t *codes[2];
-    const uint16_t *scales[2];
-    const uint16_t *biases[2];
+    // NMAT == 2: matrices 0 and 1 share rows [0, M).  NMAT == 1: rows are
+    // the concatenation of `nseg` segments, segment s = rows
+    // [seg_end[s-1], seg_end[s]) of matrix s, written to out[s].
+    const uint32_t *codes[MAX_SEG];
+    const uint16_t *scales[MAX_SEG];
+    const uint16_t *biases[MAX_SEG];
+    void *out[MAX_SEG];
+    uint32_t seg_end[MAX_SEG];
+    uint32_t nseg;
     const void *x;         // input vector (XDT) or f32 residual (NORM)
     const float *norm_w;   // f32 [K], NORM only
-    void *out[2];
     uint32_t M, K, gs;
     uint32_t lpr_log2;     // lanes per row = 1 << lpr_log2
     uint32_t sdt;          // scale/bias dtype (NNZ_F16 / NNZ_BF16)
     float eps;
 };
+
+// Weight registers of one row-step.
+template <int NMAT, int R, int NV, int VEC>
+struct StepRegs {
+    uint32_t cw[NMAT][R][NV][VEC];
+    uint16_t sc[NMAT][R][NV];
+    uint16_t bi[NMAT][R][NV];
+};
+
+// Segment of a wave-uniform step base (steps never straddle segments: the
+// host only splits rows at multiples of the rows per step).
+__device__ __forceinline__ int step_segment(const QmvArgs &a, uint32_t base, uint32_t &seg_start) {
+    int seg = 0;
+    seg_start = 0;
+    if (a.nseg > 1 && base >= a.seg_end[0]) { seg = 1; seg_start = a.seg_end[0]; }
+    if (a.nseg > 2 && base >= a.seg_end[1]) { seg = 2; seg_start = a.seg_end[1]; }
+    seg_start = __builtin_amdgcn_readfirstlane(seg_start);
+    return __builtin_amdgcn_readfirstlane(seg);
+}
+
+template <int BITS, int NMAT, int R, int NV>
+__device__ __forceinline__ void load_step(const QmvArgs &a, StepRegs<NMAT, R, NV, (BITS == 1 ? 1 : 4)> &s,
+                                          uint32_t base, int RPW, int rr, int ll, int LPR,
+                                          const bool (&uvalid)[NV], uint32_t units, uint32_t G) {
+    constexpr int VEC = (BITS == 1) ? 1 : 4;
+    const uint32_t words_per_row = units * VEC;
+    // Matrix pointers of this step, chosen with a wave-uniform segment index
+    // (a per-lane index would turn into a per-lane load of the pointer).
+    const uint32_t *cp[NMAT];
+    const uint16_t *sp[NMAT];
+    const uint16_t *bp[NMAT];
+    uint32_t seg_start = 0;
+    if constexpr (NMAT == 1) {
+        const int seg = step_segment(a, base, seg_start);
+        if (seg == 0) { cp[0] = a.codes[0]; sp[0] = a.scales[0]; bp[0] = a.biases[0]; }
+        else if (seg == 1) { cp[0] = a.codes[1]; sp[0] = a.scales[1]; bp[0] = a.biases[1]; }
+        else { cp[0] = a.codes[2]; sp[0] = a.scales[2]; bp[0] = a.biases[2]; }
+    } else {
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) { cp[m] = a.codes[m]; sp[m] = a.scales[m]; bp[m] = a.biases[m]; }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t row = base + (uint32_t)(r * RPW + rr);
+        const bool rv = row < a.M;
+        const uint32_t lrow = row - seg_start;
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) {
+            const uint32_t *codes = cp[m];
+            const uint16_t *scales = sp[m];
+            const uint16_t *biases = bp[m];
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const uint32_t u = (uint32_t)ll + (uint32_t)(LPR * j);
+                const bool ok = rv && uvalid[j];
+                const size_t wofs = (size_t)lrow * words_per_row + (size_t)u * VEC;
+                if constexpr (VEC == 1) {
+                    s.cw[m][r][j][0] = ok ? codes[wofs] : 0u;
+                } else {
+                    uint4 q = ok ? *(const uint4 *)(codes + wofs) : make_uint4(0, 0, 0, 0);
+                    s.cw[m][r][j][0] = q.x; s.cw[m][r][j][1] = q.y;
+                    s.cw[m][r][j][2] = q.z; s.cw[m][r][j][3] = q.w;
+                }
+                const size_t gidx = (size_t)lrow * G + (u * 32u) / a.gs;
+                s.sc[m][r][j] = ok ? scales[gidx] : (uint16_t)0;
+                if constexpr (BITS == 4) s.bi[m][r][j] = ok ? biases[gidx] : (uint16_t)0;
+            }
+        }
+    }
+}
+
+// Sum N per-lane values over the 64 lanes of a wave; returns, in lane l, the
+// total of value index (l >> (6 - log2 N)) & (N - 1).  Each halving step
+// keeps half of the values and trades the other half with the partner lane.
+template <int N>
+__device__ __forceinline__ float butterfly_sum(const float (&v)[N], int lane) {
+    float cur[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j) cur[j] = v[j];
+    int off = 32;
+#pragma unroll
+    for (int n = N; n > 1; n >>= 1, off >>= 1) {
+        const bool upper = (lane & off) != 0;
+#pragma unroll
+        for (int j = 0; j < n / 2; ++j) {
+            const float keep = upper ? cur[j + n / 2] : cur[j];
+            const float send = upper ? cur[j] : cur[j + n / 2];
+            cur[j] = keep + __shfl_xor(send, off, 64);
+        }
+    }
+    for (; off > 0; off >>= 1) cur[0] += __shfl_xor(cur[0], off, 64);
+    return cur[0];
+}
+
+// Store / residual-add / SiLU epilogue of one row.  `row` indexes the pair
+// outputs and the residual, `lrow` the row within the step's segment.
+template <int EPI, int ODT, bool FAITH, int NMAT>
+__device__ __forceinline__ void qmv_epilogue(const QmvArgs &a, void *out0, uint32_t row,
+                                             uint32_t lrow, const float (&tot)[NMAT]) {
+    if constexpr (EPI == EPI_STORE) {
+        if constexpr (NMAT == 1) {
+            float v = tot[0];
+            if constexpr (FAITH) v = bf16_trunc(v);
+            store_from_f32<ODT>(out0, lrow, v);
+        } else {
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m) {
+                float v = tot[m];
+                if constexpr (FAITH) v = bf16_trunc(v);
+                store_from_f32<ODT>(a.out[m], row, v);
+            }
+        }
+    } else if constexpr (EPI == EPI_RESADD) {
+        float v = tot[0];
+        if constexpr (FAITH) v = bf16_trunc(v);
+        ((float *)out0)[row] += v;
+    } else {
+        const float g = tot[0];
+        float v = g / (1.f + expf(-g)) * tot[NMAT - 1];
+        if constexpr (FAITH) v = bf16_trunc(v);
+        store_from_f32<ODT>(out0, row, v);
+    }
+}
 
 template <int BITS, int XDT, int NMAT, bool NORM, int EPI, int ODT, bool FAITH, int NV, int R>
 __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
@@ -59,17 +194,23 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
     const uint32_t K = a.K;
     const uint32_t units = K >> 5;          // 32-column units per row
     const uint32_t G = K / a.gs;            // groups per row
-    const uint32_t words_per_row = units * VEC;
+
+    bool uvalid[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) uvalid[j] = (uint32_t)ll + (uint32_t)(LPR * j) < units;
+
+    const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
+    const uint32_t rows_per_iter = (uint32_t)(R * RPW);
+    uint32_t base = wave * rows_per_iter;
+
+    // ---- first weight loads, before the x prologue ------------------------
+    StepRegs<NMAT, R, NV, VEC> cur;
+    if (base < a.M) load_step<BITS, NMAT, R, NV>(a, cur, base, RPW, rr, ll, LPR, uvalid, units, G);
 
     // ---- x slice for the owned units, kept in registers -------------------
     float xr[NV][32];
     float xsum[NV];
-    bool uvalid[NV];
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        const uint32_t u = (uint32_t)ll + (uint32_t)(LPR * j);
-        uvalid[j] = u < units;
-    }
     if constexpr (NORM) {
         const float *res = (const float *)a.x;
         float ss = 0.f;
@@ -83,23 +224,26 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                 ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
             }
         }
-        ss = group_sum(ss, LPR);
-        const float rms = rsqrtf(ss / (float)K + a.eps);
+        float wn[NV][32];
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const uint32_t u = (uint32_t)ll + (uint32_t)(LPR * j);
 #pragma unroll
             for (int i = 0; i < 32; i += 4) {
                 float4 w = uvalid[j] ? *(const float4 *)(a.norm_w + u * 32 + i) : make_float4(0, 0, 0, 0);
-                float wv[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    float v = xr[j][i + t] * rms * wv[t];
-                    if constexpr (FAITH) v = bf16_trunc(v);
-                    xr[j][i + t] = f16_round(v);
-                }
+                wn[j][i] = w.x; wn[j][i + 1] = w.y; wn[j][i + 2] = w.z; wn[j][i + 3] = w.w;
             }
         }
+        ss = group_sum(ss, LPR);
+        const float rms = rsqrtf(ss / (float)K + a.eps);
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                float v = xr[j][i] * rms * wn[j][i];
+                if constexpr (FAITH) v = bf16_trunc(v);
+                xr[j][i] = f16_round(v);
+            }
     } else {
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
@@ -141,44 +285,11 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
         xsum[j] = s;
     }
 
-    // ---- row loop ----------------------------------------------------------
-    const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
-    const uint32_t rows_per_iter = (uint32_t)(R * RPW);
-
-    for (uint32_t base = wave * rows_per_iter; base < a.M; base += nwaves * rows_per_iter) {
-        uint32_t row[R];
-        bool rvalid[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            row[r] = base + (uint32_t)(r * RPW + rr);
-            rvalid[r] = row[r] < a.M;
-        }
-
-        // Issue every weight load of this step before any arithmetic.
-        uint32_t cw[NMAT][R][NV][VEC];
-        uint16_t sc[NMAT][R][NV];
-        uint16_t bi[NMAT][R][NV];
-#pragma unroll
-        for (int m = 0; m < NMAT; ++m)
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-#pragma unroll
-                for (int j = 0; j < NV; ++j) {
-                    const uint32_t u = (uint32_t)ll + (uint32_t)(LPR * j);
-                    const bool ok = rvalid[r] && uvalid[j];
-                    const size_t wofs = (size_t)row[r] * words_per_row + (size_t)u * VEC;
-                    if constexpr (VEC == 1) {
-                        cw[m][r][j][0] = ok ? a.codes[m][wofs] : 0u;
-                    } else {
-                        uint4 q = ok ? *(const uint4 *)(a.codes[m] + wofs) : make_uint4(0, 0, 0, 0);
-                        cw[m][r][j][0] = q.x; cw[m][r][j][1] = q.y;
-                        cw[m][r][j][2] = q.z; cw[m][r][j][3] = q.w;
-                    }
-                    const size_t gidx = (size_t)row[r] * G + (u * 32u) / a.gs;
-                    sc[m][r][j] = ok ? a.scales[m][gidx] : (uint16_t)0;
-                    if constexpr (BITS == 4) bi[m][r][j] = ok ? a.biases[m][gidx] : (uint16_t)0;
-                }
+    // ---- software-pipelined row loop ---------------------------------------
+    for (; base < a.M; base += nwaves * rows_per_iter) {
+        const uint32_t next = base + nwaves * rows_per_iter;
+        StepRegs<NMAT, R, NV, VEC> nxt;
+        if (next < a.M) load_step<BITS, NMAT, R, NV>(a, nxt, next, RPW, rr, ll, LPR, uvalid, units, G);
 
         float acc[NMAT][R];
 #pragma unroll
@@ -188,9 +299,9 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                 float accv = 0.f;
 #pragma unroll
                 for (int j = 0; j < NV; ++j) {
-                    const float s = scale_to_f32(sc[m][r][j], (int)a.sdt);
+                    const float s = scale_to_f32(cur.sc[m][r][j], (int)a.sdt);
                     if constexpr (BITS == 1) {
-                        const uint32_t w = cw[m][r][j][0];
+                        const uint32_t w = cur.cw[m][r][j][0];
                         float sb = 0.f;
 #pragma unroll
                         for (int i = 0; i < 32; ++i) {
@@ -202,7 +313,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                         float nd = 0.f;
 #pragma unroll
                         for (int k = 0; k < 4; ++k) {
-                            const uint32_t w = cw[m][r][j][k];
+                            const uint32_t w = cur.cw[m][r][j][k];
                             const uint32_t lo = w & 0x0F0F0F0Fu;
                             const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
                             nd = fmaf((float)(lo & 0xFFu), xr[j][8 * k + 0], nd);
@@ -214,46 +325,56 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                             nd = fmaf((float)(lo >> 24), xr[j][8 * k + 6], nd);
                             nd = fmaf((float)(hi >> 24), xr[j][8 * k + 7], nd);
                         }
-                        const float b = scale_to_f32(bi[m][r][j], (int)a.sdt);
+                        const float b = scale_to_f32(cur.bi[m][r][j], (int)a.sdt);
                         accv = fmaf(s, nd, fmaf(b, xsum[j], accv));
                     }
                 }
-                acc[m][r] = group_sum(accv, LPR);
+                acc[m][r] = accv;
             }
 
-        if (ll == 0) {
+        // Row sums.  Full-wave rows (LPR == 64): a butterfly folds the R
+        // partial sums of each matrix together, leaving row r's total in
+        // lanes [r*64/R, (r+1)*64/R) -- log2(R) + 6 - log2(R) shuffles per
+        // matrix instead of 6 per row.  Narrow rows: plain group sums.
+        uint32_t seg_start = 0;
+        int seg = 0;
+        if constexpr (NMAT == 1) seg = step_segment(a, base, seg_start);
+        void *out0 = a.out[0];
+        if constexpr (NMAT == 1) {
+            if (seg == 1) out0 = a.out[1];
+            else if (seg == 2) out0 = a.out[2];
+        }
+        if (LPR == 64) {
+            float tot[NMAT];
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m) tot[m] = butterfly_sum<R>(acc[m], lane);
+            constexpr int LOG_R = R == 4 ? 2 : (R == 2 ? 1 : 0);
+            const int r = (lane >> (6 - LOG_R)) & (R - 1);
+            const uint32_t row = base + (uint32_t)r;  // RPW == 1
+            if ((lane & ((64 / R) - 1)) == 0 && row < a.M)
+                qmv_epilogue<EPI, ODT, FAITH, NMAT>(a, out0, row, row - seg_start, tot);
+        } else {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                if (!rvalid[r]) continue;
-                if constexpr (EPI == EPI_STORE) {
+                float tot[NMAT];
 #pragma unroll
-                    for (int m = 0; m < NMAT; ++m) {
-                        float v = acc[m][r];
-                        if constexpr (FAITH) v = bf16_trunc(v);
-                        store_from_f32<ODT>(a.out[m], row[r], v);
-                    }
-                } else if constexpr (EPI == EPI_RESADD) {
-                    float v = acc[0][r];
-                    if constexpr (FAITH) v = bf16_trunc(v);
-                    ((float *)a.out[0])[row[r]] += v;
-                } else {
-                    const float g = acc[0][r];
-                    float v = g / (1.f + expf(-g)) * acc[NMAT - 1][r];
-                    if constexpr (FAITH) v = bf16_trunc(v);
-                    store_from_f32<ODT>(a.out[0], row[r], v);
-                }
+                for (int m = 0; m < NMAT; ++m) tot[m] = group_sum(acc[m][r], LPR);
+                const uint32_t row = base + (uint32_t)(r * RPW + rr);
+                if (ll == 0 && row < a.M)
+                    qmv_epilogue<EPI, ODT, FAITH, NMAT>(a, out0, row, row - seg_start, tot);
             }
         }
+        cur = nxt;
     }
 }
 
-int check_weight(nnz_ctx *ctx, const nnz_qweight *w, int bits, const nnz_qmv_dims &d,
+int check_weight(nnz_ctx *ctx, const nnz_qweight *w, int bits, uint32_t M, const nnz_qmv_dims &d,
                  const char *name) {
     NNZ_REQUIRE(ctx, w != nullptr, NNZ_EINVAL, "%s: null weight descriptor", name);
     NNZ_REQUIRE(ctx, w->codes && w->scales, NNZ_EINVAL, "%s: null codes/scales", name);
     NNZ_REQUIRE(ctx, (int)w->bits == bits, NNZ_EINVAL, "%s: weight has %u bits, kernel needs %d",
                 name, w->bits, bits);
-    NNZ_REQUIRE(ctx, (uint64_t)w->packed_count == (uint64_t)d.M * d.K, NNZ_EINVAL,
+    NNZ_REQUIRE(ctx, (uint64_t)w->packed_count == (uint64_t)M * d.K, NNZ_EINVAL,
                 "%s: packed_count %u != M*K", name, w->packed_count);
     NNZ_REQUIRE(ctx, w->group_size == d.group_size, NNZ_EINVAL,
                 "%s: weight group_size %u != dims.group_size %u", name, w->group_size,
@@ -295,27 +416,33 @@ int launch_nv(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks) {
     return NNZ_OK;
 }
 
+// `w[0..nw)` are either a pair sharing rows (NMAT == 2) or row segments of
+// one concatenated matrix (NMAT == 1, seg_rows[s] rows each).
 template <int BITS, int XDT, int NMAT, bool NORM, int EPI, int ODT, bool FAITH>
-int launch_qmv(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, const void *x,
-               const float *norm_w, void *out0, void *out1, nnz_qmv_dims d, const char *name) {
+int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg_rows, int nw,
+                  const void *x, const float *norm_w, void *const *out, nnz_qmv_dims d,
+                  const char *name) {
     NNZ_CHECK_CTX(ctx);
     int rc = check_dims(ctx, d, name);
     if (rc) return rc;
-    rc = check_weight(ctx, wa, BITS, d, name);
-    if (rc) return rc;
-    if (NMAT == 2) {
-        rc = check_weight(ctx, wb, BITS, d, name);
+    uint32_t total = 0;
+    for (int i = 0; i < nw; ++i) {
+        const uint32_t rows = NMAT == 1 ? seg_rows[i] : d.M;
+        rc = check_weight(ctx, w[i], BITS, rows, d, name);
         if (rc) return rc;
-        NNZ_REQUIRE(ctx, wb->scale_dtype == wa->scale_dtype, NNZ_EINVAL,
-                    "%s: paired weights differ in scale dtype", name);
+        NNZ_REQUIRE(ctx, w[i]->scale_dtype == w[0]->scale_dtype, NNZ_EINVAL,
+                    "%s: weights differ in scale dtype", name);
+        NNZ_REQUIRE(ctx, out[i] != nullptr || (EPI != EPI_STORE && i > 0), NNZ_EINVAL,
+                    "%s: null output", name);
+        total += rows;
     }
-    NNZ_REQUIRE(ctx, x && out0, NNZ_EINVAL, "%s: null input/output", name);
+    if (NMAT == 1) NNZ_REQUIRE(ctx, total == d.M, NNZ_EINVAL, "%s: segments do not add up to M", name);
+    NNZ_REQUIRE(ctx, x != nullptr, NNZ_EINVAL, "%s: null input", name);
     NNZ_REQUIRE(ctx, ((uintptr_t)x & 15) == 0, NNZ_EINVAL, "%s: input must be 16-byte aligned", name);
-    NNZ_REQUIRE(ctx, !(NMAT == 2 && EPI == EPI_STORE) || out1, NNZ_EINVAL, "%s: null output_b", name);
     if (NORM) {
         NNZ_REQUIRE(ctx, norm_w != nullptr, NNZ_EINVAL, "%s: null norm_scale", name);
-        NNZ_REQUIRE(ctx, (((uintptr_t)x | (uintptr_t)norm_w) & 15) == 0, NNZ_EINVAL,
-                    "%s: residual/norm_scale must be 16-byte aligned", name);
+        NNZ_REQUIRE(ctx, ((uintptr_t)norm_w & 15) == 0, NNZ_EINVAL,
+                    "%s: norm_scale must be 16-byte aligned", name);
     }
 
     const uint32_t units = d.K / 32;
@@ -329,29 +456,41 @@ int launch_qmv(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, const
     const int vec = BITS == 1 ? 1 : 4;
     int R = 4;
     // Keep >= 2 waves of work per CU where the matrix allows, and bound the
-    // number of weight words a lane holds in flight.
+    // number of weight words a lane holds in flight (two steps are live).
     while (R > 1 && (ceil_div(d.M, 4u * R * rpw) < 512 || NMAT * R * (int)nv * vec > 32)) R >>= 1;
+    if (NMAT == 1 && nw > 1) {  // a step must not straddle two segments
+        auto aligned = [&](uint32_t step) {
+            for (int i = 0; i < nw; ++i)
+                if (seg_rows[i] % step) return false;
+            return true;
+        };
+        while (R > 1 && !aligned((uint32_t)R * rpw)) R >>= 1;
+        NNZ_REQUIRE(ctx, aligned(rpw), NNZ_EUNSUPPORTED,
+                    "%s: segment rows must be multiples of %u", name, rpw);
+    }
     uint32_t blocks = ceil_div(d.M, 4u * R * rpw);
     if (blocks > 8192) blocks = 8192;
 
     QmvArgs a{};
-    a.codes[0] = (const uint32_t *)wa->codes;
-    a.scales[0] = (const uint16_t *)wa->scales;
-    a.biases[0] = (const uint16_t *)wa->biases;
-    if (NMAT == 2) {
-        a.codes[1] = (const uint32_t *)wb->codes;
-        a.scales[1] = (const uint16_t *)wb->scales;
-        a.biases[1] = (const uint16_t *)wb->biases;
+    for (int i = 0; i < nw; ++i) {
+        a.codes[i] = (const uint32_t *)w[i]->codes;
+        a.scales[i] = (const uint16_t *)w[i]->scales;
+        a.biases[i] = (const uint16_t *)w[i]->biases;
+        a.out[i] = out[i];
+    }
+    a.nseg = NMAT == 1 ? (uint32_t)nw : 1;
+    uint32_t acc = 0;
+    for (int i = 0; i < MAX_SEG; ++i) {
+        if (NMAT == 1 && i < nw) acc += seg_rows[i];
+        a.seg_end[i] = NMAT == 1 ? acc : d.M;
     }
     a.x = x;
     a.norm_w = norm_w;
-    a.out[0] = out0;
-    a.out[1] = out1;
     a.M = d.M;
     a.K = d.K;
     a.gs = d.group_size;
     a.lpr_log2 = (uint32_t)lpr_log2;
-    a.sdt = wa->scale_dtype;
+    a.sdt = w[0]->scale_dtype;
     a.eps = 1e-6f;
     switch (nv) {
     case 1: return launch_nv<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, 1>(ctx, a, R, blocks);
@@ -361,7 +500,44 @@ int launch_qmv(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, const
     }
 }
 
+template <int BITS, int XDT, int NMAT, bool NORM, int EPI, int ODT, bool FAITH>
+int launch_qmv(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, const void *x,
+               const float *norm_w, void *out0, void *out1, nnz_qmv_dims d, const char *name) {
+    const nnz_qweight *w[2] = {wa, wb};
+    void *out[2] = {out0, out1};
+    const uint32_t rows[1] = {d.M};
+    if (NMAT == 2) NNZ_REQUIRE(ctx, wb != nullptr, NNZ_EINVAL, "%s: null second weight", name);
+    return launch_qmv_ex<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH>(ctx, w, rows, NMAT, x, norm_w, out, d,
+                                                                  name);
+}
+
 }  // namespace
+
+// ---------------------------------------------------------------------------
+// Internal fused launches used by the decoder (csrc/model.hip).
+// ---------------------------------------------------------------------------
+
+// RMSNorm prologue + Q, K and V projections in one launch (f16 outputs).
+int nnz_qmv_norm_qkv_launch(nnz_ctx *ctx, const nnz_qweight *wq, const nnz_qweight *wk,
+                            const nnz_qweight *wv, const float *residual, const float *norm_w,
+                            void *q, void *k, void *v, uint32_t qrows, uint32_t kvrows, uint32_t K,
+                            uint32_t gs) {
+    const nnz_qweight *w[3] = {wq, wk, wv};
+    void *out[3] = {q, k, v};
+    const uint32_t rows[3] = {qrows, kvrows, kvrows};
+    return launch_qmv_ex<1, NNZ_F32, 1, true, EPI_STORE, NNZ_F16, false>(
+        ctx, w, rows, 3, residual, norm_w, out, {qrows + 2 * kvrows, K, gs}, "norm_qkv");
+}
+
+// RMSNorm prologue (x rounded to f16 like rms_norm_f16out) + 1-bit LM head,
+// f32 logits: the reference's final rms_norm_f16out + qmv_spec_f16in pair
+// (transformer.zig:2730-2785) in one launch.
+int nnz_qmv_norm_f32out_launch(nnz_ctx *ctx, const nnz_qweight *w, const float *residual,
+                               const float *norm_w, float *out, nnz_qmv_dims d) {
+    return launch_qmv<1, NNZ_F32, 1, true, EPI_STORE, NNZ_F32, false>(ctx, w, nullptr, residual,
+                                                                       norm_w, out, nullptr, d,
+                                                                       "norm_lm_head");
+}
 
 extern "C" {
 
@@ -435,6 +611,20 @@ int nnz_dispatch_fused_norm_pair_qmv_f16io(nnz_ctx *ctx, const nnz_qweight *wa,
     return launch_qmv<1, NNZ_F32, 2, true, EPI_STORE, NNZ_F16, false>(
         ctx, wa, wb, residual, norm_scale, output_a, output_b, dims,
         "dispatch_fused_norm_pair_qmv_f16io");
+}
+
+int nnz_dispatch_fused_norm_qkv_f16io(nnz_ctx *ctx, const nnz_qweight *wq, const nnz_qweight *wk,
+                                      const nnz_qweight *wv, const float *residual, void *out_q,
+                                      void *out_k, void *out_v, const float *norm_scale,
+                                      nnz_qmv_dims q_dims, uint32_t kv_rows) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, kv_rows > 0, NNZ_EINVAL, "fused_norm_qkv: kv_rows == 0");
+    return nnz_qmv_norm_qkv_launch(ctx, wq, wk, wv, residual, norm_scale, out_q, out_k, out_v,
+                                   q_dims.M, kv_rows, q_dims.K, q_dims.group_size);
+}
+int nnz_dispatch_fused_norm_qmv_f16in(nnz_ctx *ctx, const nnz_qweight *w, const float *residual,
+                                      float *output, const float *norm_scale, nnz_qmv_dims dims) {
+    return nnz_qmv_norm_f32out_launch(ctx, w, residual, norm_scale, output, dims);
 }
 
 // ---------------------------- Q4 ------------------------------------------

@@ -446,6 +446,219 @@ __global__ __launch_bounds__(128) void attn_combine_kernel(AttnArgs a, uint32_t 
     store_dt(a.out, (size_t)z * a.o_stride + (size_t)qh * D + d, num / den, a.odt);
 }
 
+// ------------------------------------------- fused decode attention (1 launch)
+// The whole attention half of a decode step for one layer in one launch:
+//   prologue: per-head RMSNorm + RoPE of the G query heads (kept f32); the
+//     block whose chunk holds `pos` also normalises+rotates the new key,
+//     rounds it to f16 and appends K/V to the caches (transformer.metal:
+//     1506-1592), and uses the new row from LDS for its own scores;
+//   body: the split-sequence scores / softmax / P.V of attn_split_kernel,
+//     with TPT lanes per token in the score pass so short chunks keep every
+//     lane busy;
+//   tail: one chunk -> f16 output; several -> partials (m, l, o) merged by
+//     attn_combine_kernel in a second launch.
+// Caches: f16, K [Hkv][max_ctx][D], V [Hkv][D][max_ctx]; seq_len and
+// position come from device memory (graph replay) when d_seq is set.
+constexpr int FUSED_MAX_CHUNK = 1024;
+
+struct FusedAttnArgs {
+    const f16_t *q, *kr, *vr;       // raw projections [Hq*D], [Hkv*D], [Hkv*D]
+    const float *qn, *kn;           // per-head norm scales [D]
+    f16_t *kc, *vc;                 // caches
+    f16_t *out;                     // [Hq*D]
+    float *part_o, *part_ml;        // [Hq][nchunks][D], [Hq][nchunks][2]
+    const uint32_t *d_seq;          // device seq_len (= position + 1) or null
+    uint32_t seq_len, max_ctx, chunk, nchunks;
+    float eps, theta, scale;
+};
+
+template <int D, int G, int TPT>
+__global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
+    static_assert(G * D <= 1024, "group too large");
+    static_assert(TPT >= 1 && TPT <= 8 && (D / 8) % TPT == 0, "lanes per token");
+    constexpr int NQ = (G * D + 255) / 256;
+    __shared__ float qs[G][D];
+    __shared__ float ps[G][FUSED_MAX_CHUNK];
+    __shared__ float knew[D], vnew[D];
+    __shared__ float red[4];
+    __shared__ float ored[4][G][D];
+    __shared__ float hsum[G][4];
+
+    const int tid = threadIdx.x;
+    const uint32_t c = blockIdx.x, h = blockIdx.y;
+    const uint32_t seq = a.d_seq ? *a.d_seq : a.seq_len;
+    const uint32_t pos = seq - 1;
+    const uint32_t t0 = c * a.chunk;
+    if (t0 >= seq) return;
+    const uint32_t len = min(a.chunk, seq - t0);
+    const bool owns_new = pos < t0 + len;   // this chunk holds the new token
+
+    // ---- q: per-head RMSNorm * q_norm, RoPE; one head = D consecutive slots
+    float qv[NQ];
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+        const int i = tid + 256 * k;
+        qv[k] = i < G * D ? (float)a.q[(size_t)h * G * D + i] : 0.f;
+    }
+    // sum of squares per head: wave partials -> LDS
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+        const int i = tid + 256 * k;
+        float s = qv[k] * qv[k];
+        // lanes of one wave belong to one head when D >= 64
+        s = wave_sum(s);
+        if ((tid & 63) == 0 && i < G * D) hsum[i / D][(i % D) / 64] = s;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+        const int i = tid + 256 * k;
+        const bool ok = i < G * D;
+        const int g = ok ? i / D : 0, d = i % D;
+        float ss = 0.f;
+#pragma unroll
+        for (int w = 0; w < D / 64; ++w) ss += hsum[g][w];
+        const float v = ok ? qv[k] * rsqrtf(ss / (float)D + a.eps) * a.qn[d] : 0.f;
+        const float partner = __shfl_xor(v, 1, 64);  // all lanes take part
+        if (ok) qs[g][d] = rope_rotate(v, partner, d, pos, D, a.theta);
+    }
+    // ---- new key/value (only the block that holds position pos)
+    if (owns_new) {
+        const float kv = tid < D ? (float)a.kr[(size_t)h * D + tid] : 0.f;
+        const float ss = block_sum_256(kv * kv, red);
+        const float kn = kv * rsqrtf(ss / (float)D + a.eps) * (tid < D ? a.kn[tid] : 0.f);
+        const float partner = __shfl_xor(kn, 1, 64);
+        const float kr = f16_round(rope_rotate(kn, partner, tid, pos, D, a.theta));
+        if (tid < D) {
+            knew[tid] = kr;
+            const f16_t vv = a.vr[(size_t)h * D + tid];
+            vnew[tid] = (float)vv;
+            a.kc[(size_t)h * a.max_ctx * D + (size_t)pos * D + tid] = (f16_t)kr;
+            a.vc[(size_t)h * D * a.max_ctx + (size_t)tid * a.max_ctx + pos] = vv;
+        }
+    }
+    __syncthreads();
+
+    // ---- scores: TPT consecutive lanes per token, each dotting D/TPT
+    // dimensions with 16-byte K loads (the new row comes from LDS)
+    const size_t kv_stride = (size_t)a.max_ctx * D;
+    const f16_t *kb = a.kc + h * kv_stride;
+    constexpr int VPL = D / 8 / TPT;   // 16-byte vectors per lane
+    const int sub = tid % TPT;
+    for (uint32_t t = tid / TPT; t < ceil_div(len, 256 / TPT) * (256 / TPT); t += 256 / TPT) {
+        float dot[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) dot[g] = 0.f;
+        if (t < len) {
+            if (t0 + t == pos) {
+                for (int d = sub * VPL * 8; d < (sub + 1) * VPL * 8; ++d)
+#pragma unroll
+                    for (int g = 0; g < G; ++g) dot[g] = fmaf(qs[g][d], knew[d], dot[g]);
+            } else {
+                const uint4 *kr = (const uint4 *)(kb + (size_t)(t0 + t) * D) + sub * VPL;
+#pragma unroll 4
+                for (int v = 0; v < VPL; ++v) {
+                    const uint4 w = kr[v];
+                    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float k0, k1;
+                        unpack2<NNZ_F16>(wv[e], k0, k1);
+                        const int d = (sub * VPL + v) * 8 + 2 * e;
+#pragma unroll
+                        for (int g = 0; g < G; ++g)
+                            dot[g] = fmaf(qs[g][d + 1], k1, fmaf(qs[g][d], k0, dot[g]));
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+#pragma unroll
+            for (int o = TPT / 2; o >= 1; o >>= 1) dot[g] += __shfl_xor(dot[g], o, 64);
+        }
+        if (sub == 0 && t < len) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) ps[g][t] = dot[g] * a.scale;
+        }
+    }
+    __syncthreads();
+
+    float mval[G], lval[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float m = -INFINITY;
+        for (uint32_t t = tid; t < len; t += 256) m = fmaxf(m, ps[g][t]);
+        m = block_max_256(m, red);
+        float l = 0.f;
+        for (uint32_t t = tid; t < len; t += 256) {
+            const float e = expf(ps[g][t] - m);
+            ps[g][t] = e;
+            l += e;
+        }
+        l = block_sum_256(l, red);
+        mval[g] = m;
+        lval[g] = l;
+    }
+    __syncthreads();
+
+    // ---- P.V: a thread owns one d and streams 8 tokens per 16-byte load
+    constexpr int PARTS = 256 / D;
+    {
+        const int d = tid % D, part = tid / D;
+        float o[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) o[g] = 0.f;
+        const uint32_t ngroups = len / 8;
+        const uint32_t per = ceil_div(ngroups, PARTS);
+        const uint32_t k0 = part * per, k1 = min(ngroups, k0 + per);
+        const f16_t *row = a.vc + h * kv_stride + (size_t)d * a.max_ctx + t0;
+        for (uint32_t k = k0; k < k1; ++k) {
+            const uint4 w = *(const uint4 *)(row + 8 * k);
+            const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+            float vv[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) unpack2<NNZ_F16>(wv[e], vv[2 * e], vv[2 * e + 1]);
+            if (owns_new && pos >= t0 + 8 * k && pos < t0 + 8 * k + 8) vv[pos - t0 - 8 * k] = vnew[d];
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+#pragma unroll
+                for (int g = 0; g < G; ++g) o[g] = fmaf(ps[g][8 * k + e], vv[e], o[g]);
+        }
+        if (part == PARTS - 1) {
+            for (uint32_t t = ngroups * 8; t < len; ++t) {
+                const float v = (t0 + t == pos) ? vnew[d] : (float)row[t];
+#pragma unroll
+                for (int g = 0; g < G; ++g) o[g] = fmaf(ps[g][t], v, o[g]);
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) ored[part][g][d] = o[g];
+    }
+    __syncthreads();
+
+    // One chunk: final output.  Several: partials for attn_combine_kernel
+    // (merging inside this kernel would need an agent-scope fence between
+    // workgroups, which on a multi-XCD part writes back and invalidates the
+    // XCD's L2 -- a kernel boundary is the cheaper synchronisation).
+    for (int i = tid; i < G * D; i += 256) {
+        const int g = i / D, d = i % D;
+        float s = 0.f;
+#pragma unroll
+        for (int p = 0; p < PARTS; ++p) s += ored[p][g][d];
+        if (a.nchunks == 1) {
+            a.out[(size_t)(h * G + g) * D + d] = (f16_t)(s / lval[g]);
+        } else {
+            const size_t slot = (size_t)(h * G + g) * a.nchunks + c;
+            a.part_o[slot * D + d] = s;
+            if (d == 0) {
+                a.part_ml[slot * 2] = mval[g];
+                a.part_ml[slot * 2 + 1] = lval[g];
+            }
+        }
+    }
+}
+
 // -------------------------------------------------------------- embedding --
 // transformer.metal:428-481: flat bit index row*hidden + d, group flat/gs.
 __global__ void embed_q1_kernel(const uint32_t *ids, const uint8_t *bits, const uint16_t *scales,
@@ -690,6 +903,100 @@ int nnz_attn_launch(nnz_ctx *ctx, const void *q, int qdt, const void *kc, const 
     return nnz_attn_launch_ex(ctx, c);
 }
 
+// Chunk length of the fused decode attention for sequences up to max_seq.
+// Never shorter than nnz_attn_chunk's, so the partials fit the same scratch.
+// The NNZ_ATTN_FUSED_CHUNK environment variable (a power of two, 64..1024)
+// raises it, for tuning.
+uint32_t nnz_attn_fused_chunk(uint32_t max_seq, uint32_t hkv) {
+    static const uint32_t forced = [] {
+        const char *e = getenv("NNZ_ATTN_FUSED_CHUNK");
+        const uint32_t v = e ? (uint32_t)strtoul(e, nullptr, 10) : 0u;
+        return (v >= 64 && v <= (uint32_t)FUSED_MAX_CHUNK && (v & (v - 1)) == 0) ? v : 0u;
+    }();
+    const uint32_t base = nnz_attn_chunk(max_seq, hkv);
+    const uint32_t want = forced ? forced : base;
+    return want > base ? want : base;
+}
+
+template <int D, int G>
+static void launch_fused_t(nnz_ctx *ctx, const FusedAttnArgs &a, dim3 grid) {
+    // lanes per token: all 256 lanes busy in the score pass when possible
+    if (a.chunk >= 256) attn_fused_kernel<D, G, 1><<<grid, 256, 0, ctx->stream>>>(a);
+    else if (a.chunk >= 128) attn_fused_kernel<D, G, 2><<<grid, 256, 0, ctx->stream>>>(a);
+    else attn_fused_kernel<D, G, 4><<<grid, 256, 0, ctx->stream>>>(a);
+}
+
+// Fused decode attention (see attn_fused_kernel).  `max_seq` sizes the grid;
+// the live seq_len is d_seq ? *d_seq : max_seq.  part_o / part_ml hold
+// Hq * nchunks partials for the chunk from nnz_attn_fused_chunk.
+int nnz_attn_fused1_launch(nnz_ctx *ctx, const void *q, const void *kr, const void *vr,
+                           const float *qn, const float *kn, void *kc, void *vc, void *out,
+                           float *part_o, float *part_ml, const uint32_t *d_seq, uint32_t max_seq,
+                           uint32_t hq, uint32_t hkv, uint32_t head_dim, uint32_t max_ctx, float eps,
+                           float theta) {
+    NNZ_REQUIRE(ctx, q && kr && vr && qn && kn && kc && vc && out && part_o && part_ml,
+                NNZ_EINVAL, "gqa_fused_1pass: null buffer");
+    NNZ_REQUIRE(ctx, hkv > 0 && hq % hkv == 0 && max_seq > 0 && max_seq <= max_ctx, NNZ_EINVAL,
+                "gqa_fused_1pass: bad dims");
+    NNZ_REQUIRE(ctx, head_dim == 64 || head_dim == 128, NNZ_EUNSUPPORTED,
+                "gqa_fused_1pass: head_dim %u (supported: 64, 128)", head_dim);
+    NNZ_REQUIRE(ctx, max_ctx % 8 == 0 && ((uintptr_t)kc & 15) == 0 && ((uintptr_t)vc & 15) == 0,
+                NNZ_EUNSUPPORTED, "gqa_fused_1pass: caches must be 16-byte aligned, max_ctx %% 8 == 0");
+    const uint32_t G = hq / hkv;
+    FusedAttnArgs a{};
+    a.q = (const f16_t *)q;
+    a.kr = (const f16_t *)kr;
+    a.vr = (const f16_t *)vr;
+    a.qn = qn;
+    a.kn = kn;
+    a.kc = (f16_t *)kc;
+    a.vc = (f16_t *)vc;
+    a.out = (f16_t *)out;
+    a.part_o = part_o;
+    a.part_ml = part_ml;
+    a.d_seq = d_seq;
+    a.seq_len = max_seq;
+    a.max_ctx = max_ctx;
+    a.chunk = nnz_attn_fused_chunk(max_seq, hkv);
+    a.nchunks = ceil_div(max_seq, a.chunk);
+    a.eps = eps;
+    a.theta = theta;
+    a.scale = 1.0f / sqrtf((float)head_dim);
+    dim3 grid(a.nchunks, hkv);
+#define FUSED(DD, GG) launch_fused_t<DD, GG>(ctx, a, grid)
+    if (head_dim == 128) {
+        if (G == 1) FUSED(128, 1);
+        else if (G == 2) FUSED(128, 2);
+        else if (G == 4) FUSED(128, 4);
+        else if (G == 8) FUSED(128, 8);
+        else return nnz_fail(ctx, NNZ_EUNSUPPORTED, "gqa_fused_1pass: group %u", G);
+    } else {
+        if (G == 1) FUSED(64, 1);
+        else if (G == 2) FUSED(64, 2);
+        else if (G == 4) FUSED(64, 4);
+        else if (G == 8) FUSED(64, 8);
+        else return nnz_fail(ctx, NNZ_EUNSUPPORTED, "gqa_fused_1pass: group %u", G);
+    }
+#undef FUSED
+    NNZ_LAUNCHED(ctx);
+    if (a.nchunks > 1) {
+        AttnArgs m{};
+        m.out = out;
+        m.odt = NNZ_F16;
+        m.part_o = part_o;
+        m.part_ml = part_ml;
+        m.d_seq = d_seq;
+        m.seq_len = max_seq;
+        m.chunk = a.chunk;
+        m.nchunks = a.nchunks;
+        m.hq = hq;
+        m.o_stride = hq * head_dim;
+        attn_combine_kernel<<<dim3(hq, 1), 128, 0, ctx->stream>>>(m, head_dim);
+        NNZ_LAUNCHED(ctx);
+    }
+    return NNZ_OK;
+}
+
 // q buffer (f32) inside the attention scratch, used by the fused path.
 float *nnz_attn_scratch_q(void *scratch, const nnz_gqa_dims &d) {
     const uint32_t chunk = nnz_attn_chunk(d.seq_len, d.num_kv_heads);
@@ -875,6 +1182,35 @@ int nnz_dispatch_gqa_attention_fused(nnz_ctx *ctx, const void *q, void *k_cache,
     if (rc) return rc;
     return nnz_attn_launch(ctx, qf, NNZ_F32, k_cache, v_cache, NNZ_F16, true, output, NNZ_F16, scratch,
                            scratch_bytes, -1, fd.rope_theta, d);
+}
+
+int nnz_dispatch_gqa_attention_fused_1pass(nnz_ctx *ctx, const void *q, void *k_cache,
+                                           void *v_cache, void *output, const void *k_raw,
+                                           const void *v_raw, const float *q_norm_scale,
+                                           const float *k_norm_scale, void *scratch,
+                                           size_t scratch_bytes, const uint32_t *d_seq_len,
+                                           nnz_gqa_fused_dims fd) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, fd.num_kv_heads > 0 && fd.seq_len > 0 && fd.seq_len <= fd.max_context_length,
+                NNZ_EINVAL, "gqa_fused_1pass: bad seq_len");
+    NNZ_REQUIRE(ctx, d_seq_len || fd.seq_len == fd.position + 1, NNZ_EINVAL,
+                "gqa_fused_1pass: seq_len must be position + 1");
+    NNZ_REQUIRE(ctx, fd.heads_per_kv_group * fd.num_kv_heads == fd.num_query_heads, NNZ_EINVAL,
+                "gqa_fused_1pass: heads_per_kv_group mismatch");
+    nnz_gqa_dims d{fd.num_query_heads, fd.num_kv_heads, fd.head_dim, fd.seq_len,
+                   fd.max_context_length, fd.heads_per_kv_group};
+    const size_t need = nnz_gqa_scratch_bytes(d);
+    NNZ_REQUIRE(ctx, scratch && scratch_bytes >= need, NNZ_EINVAL,
+                "gqa_fused_1pass: scratch of %zu bytes needed", need);
+    const uint32_t chunk = nnz_attn_fused_chunk(fd.seq_len, fd.num_kv_heads);
+    const uint32_t nch = ceil_div(fd.seq_len, chunk);
+    float *base = (float *)(((uintptr_t)scratch + 255) & ~(uintptr_t)255);
+    float *part_o = base;
+    float *part_ml = base + (size_t)fd.num_query_heads * nch * fd.head_dim;
+    return nnz_attn_fused1_launch(ctx, q, k_raw, v_raw, q_norm_scale, k_norm_scale, k_cache, v_cache,
+                                  output, part_o, part_ml, d_seq_len, fd.seq_len,
+                                  fd.num_query_heads, fd.num_kv_heads, fd.head_dim,
+                                  fd.max_context_length, fd.eps, fd.rope_theta);
 }
 
 int nnz_dispatch_embedding_lookup(nnz_ctx *ctx, const uint32_t *ids, const void *bits,

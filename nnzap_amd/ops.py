@@ -183,6 +183,18 @@ def dispatch_fused_norm_pair_qmv_f16io(dev, wa, wb, residual, ya, yb, norm_scale
              _v(yb), _v(norm_scale), dims or wa.dims())
 
 
+def dispatch_fused_norm_qkv_f16io(dev, wq, wk, wv, residual, q, k, v, norm_scale):
+    """transformer.zig:1438 + :1501 as one launch (shared normalised input)."""
+    dev.call("nnz_dispatch_fused_norm_qkv_f16io", wq.ref, wk.ref, wv.ref, _v(residual), _v(q), _v(k),
+             _v(v), _v(norm_scale), wq.dims(), wk.M)
+
+
+def dispatch_fused_norm_qmv_f16in(dev, w, residual, y, norm_scale, dims=None):
+    """transformer.zig:669 (rms_norm_f16out) + :1653 dispatchQMVf16in as one launch."""
+    dev.call("nnz_dispatch_fused_norm_qmv_f16in", w.ref, _v(residual), _v(y), _v(norm_scale),
+             dims or w.dims())
+
+
 # ----------------------------------------------------------------- QMV, Q4
 def dispatch_q4mv(dev, w, x, y, dims=None):
     """f32 x -> f32 y, plain fp32 result."""
@@ -312,6 +324,15 @@ def dispatch_gqa_attention_fused(dev, q, k_cache, v_cache, out, k_raw, v_raw, q_
     dev.call("nnz_dispatch_gqa_attention_fused", _v(q), _v(k_cache), _v(v_cache), _v(out),
              _v(k_raw), _v(v_raw), _v(q_norm), _v(k_norm), _v(scratch),
              scratch.numel() * scratch.element_size(), dims)
+
+
+def dispatch_gqa_attention_fused_1pass(dev, q, k_cache, v_cache, out, k_raw, v_raw, q_norm,
+                                       k_norm, scratch, dims: L.GQAFusedDims, d_seq_len=None):
+    """transformer.zig:962 dispatchGQAAttentionFusedTG as one launch (graph
+    replay form; ``scratch`` must start zeroed, see include/nnz.h)."""
+    dev.call("nnz_dispatch_gqa_attention_fused_1pass", _v(q), _v(k_cache), _v(v_cache), _v(out),
+             _v(k_raw), _v(v_raw), _v(q_norm), _v(k_norm), _v(scratch),
+             scratch.numel() * scratch.element_size(), _v(d_seq_len), dims)
 
 
 def dispatch_embedding_lookup(dev, ids, bits, scales, out, dims: L.EmbedDims):

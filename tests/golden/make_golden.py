@@ -75,8 +75,7 @@ def small():
 def config5(n_prompt=512, n_new=256, norm_mode="small"):
     t0 = time.time()
     cfg = cf.BONSAI_1_7B
-    w = cf.decoder_weights(cfg, norm_mode=norm_mode)
-    w.embed_bf16 = None  # rows are generated on demand (synth.normal_at)
+    w = cf.decoder_weights(cfg, norm_mode=norm_mode, host_embed=False)  # rows on demand
     print(f"weights {time.time() - t0:.0f}s", flush=True)
     od = OracleDecoder(w, max_ctx=n_prompt + n_new + 8)
     print(f"dequant {time.time() - t0:.0f}s", flush=True)

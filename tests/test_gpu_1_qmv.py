@@ -167,6 +167,30 @@ def test_q1_fused_norm_variants(dev, K):
     assert_close(host(y), _f16(O.qmv_pair_silu(wa, wb, xn)), what="norm pair silu")
 
 
+@pytest.mark.parametrize("qrows,kvrows,K", [(2048, 1024, 2048), (256, 128, 256)])
+def test_fused_norm_qkv_and_norm_lm_head(dev, qrows, kvrows, K):
+    """One-launch norm + Q/K/V (equals the reference's norm-Q plus norm-KV-pair
+    dispatches) and norm + f32-output QMV (rms_norm_f16out + qmv_f16in)."""
+    wq = cf.q1_matrix(qrows, K, 128, 380, 381)
+    wk = cf.q1_matrix(kvrows, K, 128, 382, 383)
+    wv = cf.q1_matrix(kvrows, K, 128, 384, 385)
+    res = S.normal(386, K).astype(np.float32)
+    nw = (1.0 + 0.1 * S.normal(387, K)).astype(np.float32)
+    xn = O.norm_to_half(res, nw)
+    q = torch.empty(qrows, dtype=torch.float16, device="cuda")
+    k = torch.empty(kvrows, dtype=torch.float16, device="cuda")
+    v = torch.empty(kvrows, dtype=torch.float16, device="cuda")
+    rd, nd = tdev(res), tdev(nw)
+    ops.dispatch_fused_norm_qkv_f16io(dev, _dw(dev, wq), _dw(dev, wk), _dw(dev, wv), rd, q, k, v, nd)
+    y = torch.empty(qrows, dtype=torch.float32, device="cuda")
+    ops.dispatch_fused_norm_qmv_f16in(dev, _dw(dev, wq), rd, y, nd)
+    dev.sync()
+    assert_close(host(q), _f16(O.qmv(wq, xn)), what="qkv q")
+    assert_close(host(k), _f16(O.qmv(wk, xn)), what="qkv k")
+    assert_close(host(v), _f16(O.qmv(wv, xn)), what="qkv v")
+    assert_close(host(y), O.qmv(wq, xn), what="norm lm head")
+
+
 # ------------------------------------------------------------ Q4 family ---
 def test_config1_q4_qmv_f32(dev):
     """W[6144 x 2048] gs64, f16 scale/bias, f32 x/y."""

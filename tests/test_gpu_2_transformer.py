@@ -88,6 +88,42 @@ def test_gqa_fused_norm_rope_kv(dev, pos):
     assert_close(host(out), O.f16(ref), what=f"fused pos={pos}")
 
 
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (4, 2, 64), (8, 8, 128)])
+def test_gqa_fused_1pass_successive_positions(dev, hq, hkv, d):
+    """Single-launch fused attention at consecutive positions sharing one
+    scratch (exercises the merge counters being left at zero), with the
+    sequence length read from device memory as in graph replay."""
+    max_ctx, theta = 2048, 1e6
+    qn = (1 + 0.1 * S.normal(417, d)).astype(np.float32)
+    kn = (1 + 0.1 * S.normal(418, d)).astype(np.float32)
+    kc = np.zeros((hkv, max_ctx, d), np.float16)
+    vc = np.zeros((hkv, d, max_ctx), np.float16)
+    start = 1400
+    kc[:, :start] = (0.5 * S.normal(419, hkv * start * d)).astype(np.float16).reshape(hkv, start, d)
+    vc[:, :, :start] = S.normal(420, hkv * start * d).astype(np.float16).reshape(hkv, d, start)
+    kcd, vcd = tdev(kc), tdev(vc)
+    kc_ref, vc_ref = kc.astype(np.float64), vc.astype(np.float64)
+    max_seq = start + 8
+    dims = L.GQAFusedDims(hq, hkv, d, max_seq, max_ctx, hq // hkv, 0, 1e-6, theta)
+    gd = L.GQADims(hq, hkv, d, max_seq, max_ctx, hq // hkv)
+    scr = torch.zeros(ops.gqa_scratch_bytes(gd) // 4 + 64, dtype=torch.float32, device="cuda")
+    dseq = torch.zeros(1, dtype=torch.int32, device="cuda")
+    out = torch.empty(hq, d, dtype=torch.float16, device="cuda")
+    for i, pos in enumerate(range(start, start + 8)):
+        q = S.normal(430 + i, hq * d).astype(np.float16).reshape(hq, d)
+        kr = S.normal(440 + i, hkv * d).astype(np.float16).reshape(hkv, d)
+        vr = S.normal(450 + i, hkv * d).astype(np.float16).reshape(hkv, d)
+        dseq.fill_(pos + 1)
+        ops.dispatch_gqa_attention_fused_1pass(dev, tdev(q), kcd, vcd, out, tdev(kr), tdev(vr),
+                                               tdev(qn), tdev(kn), scr, dims, d_seq_len=dseq)
+        dev.sync()
+        ref = O.gqa_fused_step(q.astype(np.float64), kr.astype(np.float64), vr.astype(np.float64),
+                               kc_ref, vc_ref, qn, kn, pos, theta, v_transposed=True)
+        assert_close(host(out), O.f16(ref), what=f"1pass pos={pos}")
+    assert_close(host(kcd)[:, start:start + 8], kc_ref[:, start:start + 8], what="k rows")
+    assert np.array_equal(host(vcd)[:, :, start:start + 8], vc_ref[:, :, start:start + 8])
+
+
 # ------------------------------------------------------------------ norms ---
 @pytest.mark.parametrize("variant", ["f32", "f16", "bf16_f16"])
 def test_rms_norm_variants(dev, variant):

@@ -128,7 +128,7 @@ def test_config5_golden_tokens(mdev):
     gold = json.load(open(path))
     cfg = cf.BONSAI_1_7B
     print("config5: building weights", flush=True)
-    w = cf.decoder_weights(cfg, norm_mode=gold["norm_mode"])
+    w = cf.decoder_weights(cfg, norm_mode=gold["norm_mode"], host_embed=False)
     m = DecoderModel(mdev, cfg)
     try:
         m.load(w, embed_on_device=True)

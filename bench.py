@@ -233,6 +233,23 @@ def _kernel_cases():
             dev, r[i], res_d, logits, nw), max(16, n // 8))
         return us, wl.nbytes + H * 8 + V * 4, 1
 
+    def dec_lm_head_f16in(dev, n):
+        # the unfused alternative: f16 normalised input, f32 logits
+        wl = cf.q1_matrix(V, H, 128, 514, 515)
+        r = Rot(dev, wl, ROTATE_BYTES)
+        x16 = torch.randn(H, dtype=f16, device="cuda") * 0.05
+        logits = torch.empty(V, dtype=f32, device="cuda")
+        us = time_launches(dev, lambda i: ops.dispatch_qmv_f16in(dev, r[i], x16, logits),
+                           max(16, n // 8))
+        return us, wl.nbytes + H * 2 + V * 4, None
+
+    def floor_small(dev, n):
+        # launch floor: one tiny kernel (residual += addition over 2048 f32)
+        a = torch.zeros(H, dtype=f32, device="cuda")
+        b = torch.ones(H, dtype=f32, device="cuda")
+        us = time_launches(dev, lambda i: ops.dispatch_residual_add(dev, a, b), n)
+        return us, 3 * H * 4, None
+
     def config4(L_):
         def run(dev, n):
             kb = torch.randn(8, L_, 128, device="cuda").to(torch.bfloat16)
@@ -266,6 +283,7 @@ def _kernel_cases():
         "dec_qkv_norm": dec_qkv, "dec_attention_seq640": dec_attention,
         "dec_o_resadd": dec_o, "dec_gate_up_norm_silu": dec_gate_up,
         "dec_down_resadd": dec_down, "dec_lm_head_norm": dec_lm_head,
+        "dec_lm_head_f16in": dec_lm_head_f16in, "floor_residual_add": floor_small,
         "config4_attention_L512": config4(512), "config4_attention_L4096": config4(4096),
         "config4_attention_L32768": config4(32768), "copy_256MiB": copy_calib,
     }

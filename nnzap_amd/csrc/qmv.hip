@@ -41,15 +41,22 @@ enum { EPI_STORE = 0, EPI_RESADD = 1, EPI_SILU = 2 };
 
 constexpr int MAX_SEG = 3;
 
+// One matrix (or row segment) and its output.
+struct QmvMat {
+    const uint32_t *codes;
+    const uint16_t *scales;
+    const uint16_t *biases;
+    void *out;
+    uint32_t seg_end;      // NMAT == 1: one past the segment's last row
+};
+
 struct QmvArgs {
-    // NMAT == 2: matrices 0 and 1 share rows [0, M).  NMAT == 1: rows are
+    // NMAT == 2: matrices m0 and m1 share rows [0, M).  NMAT == 1: rows are
     // the concatenation of `nseg` segments, segment s = rows
-    // [seg_end[s-1], seg_end[s]) of matrix s, written to out[s].
-    const uint32_t *codes[MAX_SEG];
-    const uint16_t *scales[MAX_SEG];
-    const uint16_t *biases[MAX_SEG];
-    void *out[MAX_SEG];
-    uint32_t seg_end[MAX_SEG];
+    // [m(s-1).seg_end, m(s).seg_end) of matrix s, written to its out.
+    // Separate fields, not an array: a runtime index into a kernel-argument
+    // array makes the compiler copy the arguments to scratch memory.
+    QmvMat m0, m1, m2;
     uint32_t nseg;
     const void *x;         // input vector (XDT) or f32 residual (NORM)
     const float *norm_w;   // f32 [K], NORM only
@@ -65,6 +72,8 @@ struct StepRegs {
     uint32_t cw[NMAT][R][NV][VEC];
     uint16_t sc[NMAT][R][NV];
     uint16_t bi[NMAT][R][NV];
+    bool ok[NMAT][R][NV];      // lane holds a real (row, unit)
+    float res[R];              // residual-add epilogue: current residual rows
 };
 
 // Segment of a wave-uniform step base (steps never straddle segments: the
@@ -72,13 +81,67 @@ struct StepRegs {
 __device__ __forceinline__ int step_segment(const QmvArgs &a, uint32_t base, uint32_t &seg_start) {
     int seg = 0;
     seg_start = 0;
-    if (a.nseg > 1 && base >= a.seg_end[0]) { seg = 1; seg_start = a.seg_end[0]; }
-    if (a.nseg > 2 && base >= a.seg_end[1]) { seg = 2; seg_start = a.seg_end[1]; }
+    if (a.nseg > 1 && base >= a.m0.seg_end) { seg = 1; seg_start = a.m0.seg_end; }
+    if (a.nseg > 2 && base >= a.m1.seg_end) { seg = 2; seg_start = a.m1.seg_end; }
     seg_start = __builtin_amdgcn_readfirstlane(seg_start);
     return __builtin_amdgcn_readfirstlane(seg);
 }
 
-template <int BITS, int NMAT, int R, int NV>
+// Matrix `m` of a pair (compile-time index).
+template <int m>
+__device__ __forceinline__ const QmvMat &mat_of(const QmvArgs &a) {
+    static_assert(m >= 0 && m < MAX_SEG, "matrix index");
+    if constexpr (m == 0) return a.m0;
+    else if constexpr (m == 1) return a.m1;
+    else return a.m2;
+}
+
+// A wave-uniform pointer as an opaque scalar value.  Selecting between
+// argument fields through this keeps the compiler from turning the select
+// into a load through a selected field address, which would force a copy of
+// the whole argument block to scratch memory.
+// The result is typed as a global-memory pointer so loads through it are
+// global (not flat) loads.
+#if defined(__HIP_DEVICE_COMPILE__)
+template <class T>
+using gptr = T __attribute__((address_space(1))) *;
+#else
+template <class T>
+using gptr = T *;   // host pass: device bodies are parsed, not generated
+#endif
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <class T>
+__device__ __forceinline__ gptr<T> uniform_ptr(T *p) {
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (gptr<T>)(((uint64_t)hi << 32) | lo);
+}
+
+template <class T>
+__device__ __forceinline__ gptr<T> pick3(int seg, T *p0, T *p1, T *p2) {
+    gptr<T> a = uniform_ptr(p0), b = uniform_ptr(p1), c = uniform_ptr(p2);
+    return seg == 0 ? a : (seg == 1 ? b : c);
+}
+
+// Pointers of segment `seg` (wave-uniform runtime index).
+struct SegPtrs {
+    gptr<const uint32_t> codes;
+    gptr<const uint16_t> scales, biases;
+    gptr<void> out;
+};
+
+__device__ __forceinline__ SegPtrs seg_mat(const QmvArgs &a, int seg) {
+    SegPtrs r;
+    r.codes = pick3(seg, a.m0.codes, a.m1.codes, a.m2.codes);
+    r.scales = pick3(seg, a.m0.scales, a.m1.scales, a.m2.scales);
+    r.biases = pick3(seg, a.m0.biases, a.m1.biases, a.m2.biases);
+    r.out = pick3(seg, a.m0.out, a.m1.out, a.m2.out);
+    return r;
+}
+
+template <int BITS, int NMAT, int R, int NV, bool RES>
 __device__ __forceinline__ void load_step(const QmvArgs &a, StepRegs<NMAT, R, NV, (BITS == 1 ? 1 : 4)> &s,
                                           uint32_t base, int RPW, int rr, int ll, int LPR,
                                           const bool (&uvalid)[NV], uint32_t units, uint32_t G) {
@@ -86,44 +149,56 @@ __device__ __forceinline__ void load_step(const QmvArgs &a, StepRegs<NMAT, R, NV
     const uint32_t words_per_row = units * VEC;
     // Matrix pointers of this step, chosen with a wave-uniform segment index
     // (a per-lane index would turn into a per-lane load of the pointer).
-    const uint32_t *cp[NMAT];
-    const uint16_t *sp[NMAT];
-    const uint16_t *bp[NMAT];
+    gptr<const uint32_t> cp[NMAT];
+    gptr<const uint16_t> sp[NMAT];
+    gptr<const uint16_t> bp[NMAT];
     uint32_t seg_start = 0;
+    gptr<void> outp = nullptr;
     if constexpr (NMAT == 1) {
-        const int seg = step_segment(a, base, seg_start);
-        if (seg == 0) { cp[0] = a.codes[0]; sp[0] = a.scales[0]; bp[0] = a.biases[0]; }
-        else if (seg == 1) { cp[0] = a.codes[1]; sp[0] = a.scales[1]; bp[0] = a.biases[1]; }
-        else { cp[0] = a.codes[2]; sp[0] = a.scales[2]; bp[0] = a.biases[2]; }
+        const SegPtrs sm = seg_mat(a, step_segment(a, base, seg_start));
+        cp[0] = sm.codes; sp[0] = sm.scales; bp[0] = sm.biases;
+        outp = sm.out;
     } else {
-#pragma unroll
-        for (int m = 0; m < NMAT; ++m) { cp[m] = a.codes[m]; sp[m] = a.scales[m]; bp[m] = a.biases[m]; }
+        cp[0] = uniform_ptr(a.m0.codes); sp[0] = uniform_ptr(a.m0.scales);
+        bp[0] = uniform_ptr(a.m0.biases);
+        cp[NMAT - 1] = uniform_ptr(mat_of<NMAT - 1>(a).codes);
+        sp[NMAT - 1] = uniform_ptr(mat_of<NMAT - 1>(a).scales);
+        bp[NMAT - 1] = uniform_ptr(mat_of<NMAT - 1>(a).biases);
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t row = base + (uint32_t)(r * RPW + rr);
         const bool rv = row < a.M;
         const uint32_t lrow = row - seg_start;
+        if constexpr (RES) {  // residual rows this step will add to, read early
+            static_assert(NMAT == 1, "residual add has one matrix");
+            s.res[r] = ((gptr<const float>)outp)[rv ? lrow : 0u];
+        }
 #pragma unroll
         for (int m = 0; m < NMAT; ++m) {
-            const uint32_t *codes = cp[m];
-            const uint16_t *scales = sp[m];
-            const uint16_t *biases = bp[m];
+            const gptr<const uint32_t> codes = cp[m];
+            const gptr<const uint16_t> scales = sp[m];
+            const gptr<const uint16_t> biases = bp[m];
 #pragma unroll
             for (int j = 0; j < NV; ++j) {
-                const uint32_t u = (uint32_t)ll + (uint32_t)(LPR * j);
+                // Unconditional loads from a clamped address (word 0 of the
+                // matrix stands in for a lane past the end); the dead lane's
+                // scale and bias are zeroed so its weights contribute 0.
                 const bool ok = rv && uvalid[j];
-                const size_t wofs = (size_t)lrow * words_per_row + (size_t)u * VEC;
+                const uint32_t u = ok ? (uint32_t)ll + (uint32_t)(LPR * j) : 0u;
+                const uint32_t lr = ok ? lrow : 0u;
+                const size_t wofs = (size_t)lr * words_per_row + (size_t)u * VEC;
                 if constexpr (VEC == 1) {
-                    s.cw[m][r][j][0] = ok ? codes[wofs] : 0u;
+                    s.cw[m][r][j][0] = codes[wofs];
                 } else {
-                    uint4 q = ok ? *(const uint4 *)(codes + wofs) : make_uint4(0, 0, 0, 0);
+                    const u32x4 q = *(gptr<const u32x4>)(codes + wofs);
                     s.cw[m][r][j][0] = q.x; s.cw[m][r][j][1] = q.y;
                     s.cw[m][r][j][2] = q.z; s.cw[m][r][j][3] = q.w;
                 }
-                const size_t gidx = (size_t)lrow * G + (u * 32u) / a.gs;
-                s.sc[m][r][j] = ok ? scales[gidx] : (uint16_t)0;
-                if constexpr (BITS == 4) s.bi[m][r][j] = ok ? biases[gidx] : (uint16_t)0;
+                const size_t gidx = (size_t)lr * G + (u * 32u) / a.gs;
+                s.sc[m][r][j] = scales[gidx];
+                if constexpr (BITS == 4) s.bi[m][r][j] = biases[gidx];
+                s.ok[m][r][j] = ok;
             }
         }
     }
@@ -156,7 +231,7 @@ __device__ __forceinline__ float butterfly_sum(const float (&v)[N], int lane) {
 // outputs and the residual, `lrow` the row within the step's segment.
 template <int EPI, int ODT, bool FAITH, int NMAT>
 __device__ __forceinline__ void qmv_epilogue(const QmvArgs &a, void *out0, uint32_t row,
-                                             uint32_t lrow, const float (&tot)[NMAT]) {
+                                             uint32_t lrow, const float (&tot)[NMAT], float prev) {
     if constexpr (EPI == EPI_STORE) {
         if constexpr (NMAT == 1) {
             float v = tot[0];
@@ -167,13 +242,13 @@ __device__ __forceinline__ void qmv_epilogue(const QmvArgs &a, void *out0, uint3
             for (int m = 0; m < NMAT; ++m) {
                 float v = tot[m];
                 if constexpr (FAITH) v = bf16_trunc(v);
-                store_from_f32<ODT>(a.out[m], row, v);
+                store_from_f32<ODT>(m == 0 ? a.m0.out : a.m1.out, row, v);
             }
         }
     } else if constexpr (EPI == EPI_RESADD) {
         float v = tot[0];
         if constexpr (FAITH) v = bf16_trunc(v);
-        ((float *)out0)[row] += v;
+        ((float *)out0)[row] = prev + v;   // prev: residual[row] read with the weights
     } else {
         const float g = tot[0];
         float v = g / (1.f + expf(-g)) * tot[NMAT - 1];
@@ -206,53 +281,87 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
 
     // ---- first weight loads, before the x prologue ------------------------
     StepRegs<NMAT, R, NV, VEC> cur;
-    if (base < a.M) load_step<BITS, NMAT, R, NV>(a, cur, base, RPW, rr, ll, LPR, uvalid, units, G);
+    if (base < a.M)
+        load_step<BITS, NMAT, R, NV, EPI == EPI_RESADD>(a, cur, base, RPW, rr, ll, LPR, uvalid, units, G);
 
     // ---- x slice for the owned units, kept in registers -------------------
+    // A unit past the row end holds unit 0's (finite) values; its scale is
+    // zero, so it adds nothing and needs no masking here.
     float xr[NV][32];
     float xsum[NV];
     if constexpr (NORM) {
-        const float *res = (const float *)a.x;
+        // The block normalises x once: each thread loads K/256 residual and
+        // norm-weight values (K <= 2048*NV, so at most 2*NV float4 each),
+        // the sum of squares is reduced through LDS, and the f16-rounded
+        // normalised vector is staged in LDS for every wave to read its
+        // slice -- one copy of the prologue's loads per block, not per wave.
+        constexpr int P4 = 2 * NV;
+        __shared__ __align__(16) f16_t xs[2048 * NV];
+        __shared__ float red[4];
+        const float4 *res4 = (const float4 *)a.x;
+        const float4 *nw4 = (const float4 *)a.norm_w;
+        const uint32_t n4 = K / 4;
+        float4 rv[P4], wv[P4];
+#pragma unroll
+        for (int k = 0; k < P4; ++k) {
+            const uint32_t i4 = threadIdx.x + 256u * k;
+            const uint32_t ic = i4 < n4 ? i4 : 0u;
+            rv[k] = res4[ic];
+            wv[k] = nw4[ic];
+        }
         float ss = 0.f;
 #pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            const uint32_t u = (uint32_t)ll + (uint32_t)(LPR * j);
-#pragma unroll
-            for (int i = 0; i < 32; i += 4) {
-                float4 v = uvalid[j] ? *(const float4 *)(res + u * 32 + i) : make_float4(0, 0, 0, 0);
-                xr[j][i] = v.x; xr[j][i + 1] = v.y; xr[j][i + 2] = v.z; xr[j][i + 3] = v.w;
-                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-            }
+        for (int k = 0; k < P4; ++k) {
+            if (threadIdx.x + 256u * k >= n4) rv[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+            ss = fmaf(rv[k].x, rv[k].x, ss);
+            ss = fmaf(rv[k].y, rv[k].y, ss);
+            ss = fmaf(rv[k].z, rv[k].z, ss);
+            ss = fmaf(rv[k].w, rv[k].w, ss);
         }
-        float wn[NV][32];
-#pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            const uint32_t u = (uint32_t)ll + (uint32_t)(LPR * j);
-#pragma unroll
-            for (int i = 0; i < 32; i += 4) {
-                float4 w = uvalid[j] ? *(const float4 *)(a.norm_w + u * 32 + i) : make_float4(0, 0, 0, 0);
-                wn[j][i] = w.x; wn[j][i + 1] = w.y; wn[j][i + 2] = w.z; wn[j][i + 3] = w.w;
-            }
-        }
-        ss = group_sum(ss, LPR);
+        ss = wave_sum(ss);
+        if (lane == 0) red[threadIdx.x >> 6] = ss;
+        __syncthreads();
+        ss = (red[0] + red[1]) + (red[2] + red[3]);
         const float rms = rsqrtf(ss / (float)K + a.eps);
 #pragma unroll
-        for (int j = 0; j < NV; ++j)
+        for (int k = 0; k < P4; ++k) {
+            const uint32_t i4 = threadIdx.x + 256u * k;
+            if (i4 < n4) {
+                float v[4] = {rv[k].x * rms * wv[k].x, rv[k].y * rms * wv[k].y,
+                              rv[k].z * rms * wv[k].z, rv[k].w * rms * wv[k].w};
 #pragma unroll
-            for (int i = 0; i < 32; ++i) {
-                float v = xr[j][i] * rms * wn[j][i];
-                if constexpr (FAITH) v = bf16_trunc(v);
-                xr[j][i] = f16_round(v);
+                for (int e = 0; e < 4; ++e) {
+                    if constexpr (FAITH) v[e] = bf16_trunc(v[e]);
+                    xs[4 * i4 + e] = (f16_t)v[e];
+                }
             }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const uint32_t u = uvalid[j] ? (uint32_t)ll + (uint32_t)(LPR * j) : 0u;
+            const uint4 *p = (const uint4 *)(xs + u * 32);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint4 q = p[i];
+                const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    xr[j][8 * i + 2 * t] = (float)__builtin_bit_cast(f16_t, (uint16_t)(w4[t] & 0xFFFFu));
+                    xr[j][8 * i + 2 * t + 1] = (float)__builtin_bit_cast(f16_t, (uint16_t)(w4[t] >> 16));
+                }
+            }
+        }
     } else {
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
-            const uint32_t u = (uint32_t)ll + (uint32_t)(LPR * j);
+            // unconditional loads (unit 0 stands in past the row end)
+            const uint32_t u = uvalid[j] ? (uint32_t)ll + (uint32_t)(LPR * j) : 0u;
             if constexpr (XDT == NNZ_F32) {
                 const float4 *p = (const float4 *)((const float *)a.x + (size_t)u * 32);
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
-                    float4 v = uvalid[j] ? p[i] : make_float4(0, 0, 0, 0);
+                    const float4 v = p[i];
                     xr[j][4 * i] = v.x; xr[j][4 * i + 1] = v.y;
                     xr[j][4 * i + 2] = v.z; xr[j][4 * i + 3] = v.w;
                 }
@@ -260,7 +369,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                 const uint4 *p = (const uint4 *)((const uint16_t *)a.x + (size_t)u * 32);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    uint4 v = uvalid[j] ? p[i] : make_uint4(0, 0, 0, 0);
+                    const uint4 v = p[i];
                     uint32_t wv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
@@ -289,7 +398,8 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
     for (; base < a.M; base += nwaves * rows_per_iter) {
         const uint32_t next = base + nwaves * rows_per_iter;
         StepRegs<NMAT, R, NV, VEC> nxt;
-        if (next < a.M) load_step<BITS, NMAT, R, NV>(a, nxt, next, RPW, rr, ll, LPR, uvalid, units, G);
+        if (next < a.M)
+            load_step<BITS, NMAT, R, NV, EPI == EPI_RESADD>(a, nxt, next, RPW, rr, ll, LPR, uvalid, units, G);
 
         float acc[NMAT][R];
 #pragma unroll
@@ -299,7 +409,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                 float accv = 0.f;
 #pragma unroll
                 for (int j = 0; j < NV; ++j) {
-                    const float s = scale_to_f32(cur.sc[m][r][j], (int)a.sdt);
+                    const float s = cur.ok[m][r][j] ? scale_to_f32(cur.sc[m][r][j], (int)a.sdt) : 0.f;
                     if constexpr (BITS == 1) {
                         const uint32_t w = cur.cw[m][r][j][0];
                         float sb = 0.f;
@@ -325,7 +435,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                             nd = fmaf((float)(lo >> 24), xr[j][8 * k + 6], nd);
                             nd = fmaf((float)(hi >> 24), xr[j][8 * k + 7], nd);
                         }
-                        const float b = scale_to_f32(cur.bi[m][r][j], (int)a.sdt);
+                        const float b = cur.ok[m][r][j] ? scale_to_f32(cur.bi[m][r][j], (int)a.sdt) : 0.f;
                         accv = fmaf(s, nd, fmaf(b, xsum[j], accv));
                     }
                 }
@@ -339,11 +449,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
         uint32_t seg_start = 0;
         int seg = 0;
         if constexpr (NMAT == 1) seg = step_segment(a, base, seg_start);
-        void *out0 = a.out[0];
-        if constexpr (NMAT == 1) {
-            if (seg == 1) out0 = a.out[1];
-            else if (seg == 2) out0 = a.out[2];
-        }
+        void *out0 = NMAT == 1 ? (void *)seg_mat(a, seg).out : a.m0.out;
         if (LPR == 64) {
             float tot[NMAT];
 #pragma unroll
@@ -351,8 +457,11 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
             constexpr int LOG_R = R == 4 ? 2 : (R == 2 ? 1 : 0);
             const int r = (lane >> (6 - LOG_R)) & (R - 1);
             const uint32_t row = base + (uint32_t)r;  // RPW == 1
+            float prev = cur.res[0];
+#pragma unroll
+            for (int k = 1; k < R; ++k) prev = r == k ? cur.res[k] : prev;
             if ((lane & ((64 / R) - 1)) == 0 && row < a.M)
-                qmv_epilogue<EPI, ODT, FAITH, NMAT>(a, out0, row, row - seg_start, tot);
+                qmv_epilogue<EPI, ODT, FAITH, NMAT>(a, out0, row, row - seg_start, tot, prev);
         } else {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
@@ -361,7 +470,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                 for (int m = 0; m < NMAT; ++m) tot[m] = group_sum(acc[m][r], LPR);
                 const uint32_t row = base + (uint32_t)(r * RPW + rr);
                 if (ll == 0 && row < a.M)
-                    qmv_epilogue<EPI, ODT, FAITH, NMAT>(a, out0, row, row - seg_start, tot);
+                    qmv_epilogue<EPI, ODT, FAITH, NMAT>(a, out0, row, row - seg_start, tot, cur.res[r]);
             }
         }
         cur = nxt;
@@ -404,14 +513,22 @@ int check_dims(nnz_ctx *ctx, const nnz_qmv_dims &d, const char *name) {
     return NNZ_OK;
 }
 
+// Weight words a lane holds for one row-step; the host keeps it <= 32.
+constexpr int step_words(int BITS, int NMAT, int NV, int R) { return NMAT * R * NV * (BITS == 1 ? 1 : 4); }
+
 template <int BITS, int XDT, int NMAT, bool NORM, int EPI, int ODT, bool FAITH, int NV>
 int launch_nv(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks) {
     dim3 grid(blocks), block(256);
-    switch (R) {
-    case 4: qmv_kernel<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, 4><<<grid, block, 0, ctx->stream>>>(a); break;
-    case 2: qmv_kernel<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, 2><<<grid, block, 0, ctx->stream>>>(a); break;
-    default: qmv_kernel<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, 1><<<grid, block, 0, ctx->stream>>>(a); break;
+    if (R == 4) {
+        if constexpr (step_words(BITS, NMAT, NV, 4) <= 32)
+            qmv_kernel<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, 4><<<grid, block, 0, ctx->stream>>>(a);
+        else R = 1;
+    } else if (R == 2) {
+        if constexpr (step_words(BITS, NMAT, NV, 2) <= 32)
+            qmv_kernel<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, 2><<<grid, block, 0, ctx->stream>>>(a);
+        else R = 1;
     }
+    if (R == 1) qmv_kernel<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, 1><<<grid, block, 0, ctx->stream>>>(a);
     NNZ_LAUNCHED(ctx);
     return NNZ_OK;
 }
@@ -469,20 +586,25 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
                     "%s: segment rows must be multiples of %u", name, rpw);
     }
     uint32_t blocks = ceil_div(d.M, 4u * R * rpw);
-    if (blocks > 8192) blocks = 8192;
+    // Every wave re-reads its x slice (and, with the norm prologue, the
+    // residual and norm weights): cap the grid so large matrices amortise
+    // that over several row-steps per wave.
+    const uint32_t max_blocks = NORM ? 1024u : 2048u;
+    if (blocks > max_blocks) blocks = max_blocks;
 
     QmvArgs a{};
     for (int i = 0; i < nw; ++i) {
-        a.codes[i] = (const uint32_t *)w[i]->codes;
-        a.scales[i] = (const uint16_t *)w[i]->scales;
-        a.biases[i] = (const uint16_t *)w[i]->biases;
-        a.out[i] = out[i];
+        QmvMat &mm = i == 0 ? a.m0 : (i == 1 ? a.m1 : a.m2);
+        mm.codes = (const uint32_t *)w[i]->codes;
+        mm.scales = (const uint16_t *)w[i]->scales;
+        mm.biases = (const uint16_t *)w[i]->biases;
+        mm.out = out[i];
     }
     a.nseg = NMAT == 1 ? (uint32_t)nw : 1;
     uint32_t acc = 0;
     for (int i = 0; i < MAX_SEG; ++i) {
         if (NMAT == 1 && i < nw) acc += seg_rows[i];
-        a.seg_end[i] = NMAT == 1 ? acc : d.M;
+        (i == 0 ? a.m0 : (i == 1 ? a.m1 : a.m2)).seg_end = NMAT == 1 ? acc : d.M;
     }
     a.x = x;
     a.norm_w = norm_w;

@@ -446,20 +446,23 @@ __global__ __launch_bounds__(128) void attn_combine_kernel(AttnArgs a, uint32_t 
     store_dt(a.out, (size_t)z * a.o_stride + (size_t)qh * D + d, num / den, a.odt);
 }
 
-// ------------------------------------------- fused decode attention (1 launch)
-// The whole attention half of a decode step for one layer in one launch:
-//   prologue: per-head RMSNorm + RoPE of the G query heads (kept f32); the
-//     block whose chunk holds `pos` also normalises+rotates the new key,
-//     rounds it to f16 and appends K/V to the caches (transformer.metal:
-//     1506-1592), and uses the new row from LDS for its own scores;
-//   body: the split-sequence scores / softmax / P.V of attn_split_kernel,
-//     with TPT lanes per token in the score pass so short chunks keep every
-//     lane busy;
-//   tail: one chunk -> f16 output; several -> partials (m, l, o) merged by
-//     attn_combine_kernel in a second launch.
+// ------------------------------------------------- fused decode attention --
+// The attention half of a decode step for one layer:
+//   attn_fused_kernel, grid (chunks of FCHUNK tokens, Hkv), 256 threads:
+//     * first, every thread issues its K and V loads for the chunk (they do
+//       not depend on q), so the q prologue, the scores and P.V wait on one
+//       memory round trip instead of three;
+//     * per-head RMSNorm + RoPE of the G query heads (kept f32); the block
+//       whose chunk holds `pos` also normalises+rotates the new key, rounds
+//       it to f16, appends K/V to the caches (transformer.metal:1506-1592)
+//       and uses the new row from LDS in place of the prefetched one;
+//     * scores with 256/FCHUNK lanes per token, one softmax pass for all G
+//       heads, P.V with a thread per (d, token part);
+//     * one chunk: f16 output; several: partials (m, l, o) for
+//       attn_merge_kernel, which folds them with one round of loads.
 // Caches: f16, K [Hkv][max_ctx][D], V [Hkv][D][max_ctx]; seq_len and
 // position come from device memory (graph replay) when d_seq is set.
-constexpr int FUSED_MAX_CHUNK = 1024;
+constexpr int FCHUNK = 64;
 
 struct FusedAttnArgs {
     const f16_t *q, *kr, *vr;       // raw projections [Hq*D], [Hkv*D], [Hkv*D]
@@ -468,46 +471,102 @@ struct FusedAttnArgs {
     f16_t *out;                     // [Hq*D]
     float *part_o, *part_ml;        // [Hq][nchunks][D], [Hq][nchunks][2]
     const uint32_t *d_seq;          // device seq_len (= position + 1) or null
-    uint32_t seq_len, max_ctx, chunk, nchunks;
+    uint32_t seq_len, max_ctx, nchunks;
     float eps, theta, scale;
 };
 
-template <int D, int G, int TPT>
+template <int D, int G>
 __global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
     static_assert(G * D <= 1024, "group too large");
-    static_assert(TPT >= 1 && TPT <= 8 && (D / 8) % TPT == 0, "lanes per token");
     constexpr int NQ = (G * D + 255) / 256;
+    constexpr int TPT = 256 / FCHUNK;          // lanes per token in the score pass
+    constexpr int KV4 = D / 8 / TPT;           // K: 16-byte vectors per lane
+    constexpr int PARTS = 256 / D;             // P.V: token parts per d
+    constexpr int VT = FCHUNK / PARTS;         // P.V: tokens per thread
+    constexpr int VV4 = VT / 8;                // V: 16-byte vectors per thread
+    static_assert(KV4 >= 1 && VV4 >= 1, "chunk/head_dim");
     __shared__ float qs[G][D];
-    __shared__ float ps[G][FUSED_MAX_CHUNK];
+    __shared__ float ps[G][FCHUNK];   // scores
+    __shared__ float pe[G][FCHUNK];   // exp(score - max)
     __shared__ float knew[D], vnew[D];
-    __shared__ float red[4];
-    __shared__ float ored[4][G][D];
+    __shared__ float red[4][G];
+    __shared__ float ored[PARTS][G][D];
     __shared__ float hsum[G][4];
 
     const int tid = threadIdx.x;
     const uint32_t c = blockIdx.x, h = blockIdx.y;
     const uint32_t seq = a.d_seq ? *a.d_seq : a.seq_len;
     const uint32_t pos = seq - 1;
-    const uint32_t t0 = c * a.chunk;
+    const uint32_t t0 = c * FCHUNK;
     if (t0 >= seq) return;
-    const uint32_t len = min(a.chunk, seq - t0);
+    const uint32_t len = min((uint32_t)FCHUNK, seq - t0);
     const bool owns_new = pos < t0 + len;   // this chunk holds the new token
 
-    // ---- q: per-head RMSNorm * q_norm, RoPE; one head = D consecutive slots
-    float qv[NQ];
+    // ---- loads, in the order they are needed: the small q/k/v vectors and
+    // norm weights first, then the chunk's K and V (vmcnt counts in order,
+    // so the prologue can start while K and V are still in flight)
+    float qv[NQ], qnv[NQ];
 #pragma unroll
     for (int k = 0; k < NQ; ++k) {
         const int i = tid + 256 * k;
-        qv[k] = i < G * D ? (float)a.q[(size_t)h * G * D + i] : 0.f;
+        const int ic = i < G * D ? i : 0;
+        qv[k] = (float)a.q[(size_t)h * G * D + ic];
+        qnv[k] = a.qn[ic % D];
     }
-    // sum of squares per head: wave partials -> LDS
+    const int kd = tid < D ? tid : 0;
+    const float kraw = (float)a.kr[(size_t)h * D + kd];
+    const float knw = a.kn[kd];
+    const f16_t vraw = a.vr[(size_t)h * D + kd];
+
+    const size_t kv_stride = (size_t)a.max_ctx * D;
+    const int kt = tid / TPT, ksub = tid % TPT;
+    const uint32_t ktok = t0 + min((uint32_t)kt, len - 1);
+    uint4 kreg[KV4];
+    {
+        const uint4 *kp = (const uint4 *)(a.kc + h * kv_stride + (size_t)ktok * D) + ksub * KV4;
+#pragma unroll
+        for (int v = 0; v < KV4; ++v) kreg[v] = kp[v];
+    }
+    // V: 8-token groups; a group that starts past the chunk's end reads
+    // group 0 instead (it stays inside the row) and is masked below.
+    const int vd = tid % D, vpart = tid / D;
+    uint4 vreg[VV4];
+    {
+        const f16_t *vrow = a.vc + h * kv_stride + (size_t)vd * a.max_ctx + t0;
+#pragma unroll
+        for (int v = 0; v < VV4; ++v) {
+            const uint32_t g0 = (uint32_t)(vpart * VT + v * 8);
+            vreg[v] = *(const uint4 *)(vrow + (g0 < len ? g0 : 0u));
+        }
+    }
+
+    // ---- q: per-head RMSNorm * q_norm, RoPE; one head = D consecutive slots
 #pragma unroll
     for (int k = 0; k < NQ; ++k) {
         const int i = tid + 256 * k;
-        float s = qv[k] * qv[k];
-        // lanes of one wave belong to one head when D >= 64
-        s = wave_sum(s);
+        if (i >= G * D) qv[k] = 0.f;
+        // lanes of one wave belong to one head (D >= 64)
+        const float s = wave_sum(qv[k] * qv[k]);
         if ((tid & 63) == 0 && i < G * D) hsum[i / D][(i % D) / 64] = s;
+    }
+    // new key: RMSNorm * k_norm, RoPE, f16; appended to the caches
+    if (owns_new) {
+        const float kv = tid < D ? kraw : 0.f;
+        float ss = wave_sum(kv * kv);
+        if (D > 64) {
+            if ((tid & 63) == 0) red[tid >> 6][0] = ss;
+        }
+        __syncthreads();
+        if (D > 64) ss = red[0][0] + red[1][0];
+        const float kn = kv * rsqrtf(ss / (float)D + a.eps) * knw;
+        const float partner = __shfl_xor(kn, 1, 64);
+        const float kr = f16_round(rope_rotate(kn, partner, tid, pos, D, a.theta));
+        if (tid < D) {
+            knew[tid] = kr;
+            vnew[tid] = (float)vraw;
+            a.kc[(size_t)h * kv_stride + (size_t)pos * D + tid] = (f16_t)kr;
+            a.vc[(size_t)h * kv_stride + (size_t)tid * a.max_ctx + pos] = vraw;
+        }
     }
     __syncthreads();
 #pragma unroll
@@ -518,58 +577,29 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
         float ss = 0.f;
 #pragma unroll
         for (int w = 0; w < D / 64; ++w) ss += hsum[g][w];
-        const float v = ok ? qv[k] * rsqrtf(ss / (float)D + a.eps) * a.qn[d] : 0.f;
+        const float v = ok ? qv[k] * rsqrtf(ss / (float)D + a.eps) * qnv[k] : 0.f;
         const float partner = __shfl_xor(v, 1, 64);  // all lanes take part
         if (ok) qs[g][d] = rope_rotate(v, partner, d, pos, D, a.theta);
     }
-    // ---- new key/value (only the block that holds position pos)
-    if (owns_new) {
-        const float kv = tid < D ? (float)a.kr[(size_t)h * D + tid] : 0.f;
-        const float ss = block_sum_256(kv * kv, red);
-        const float kn = kv * rsqrtf(ss / (float)D + a.eps) * (tid < D ? a.kn[tid] : 0.f);
-        const float partner = __shfl_xor(kn, 1, 64);
-        const float kr = f16_round(rope_rotate(kn, partner, tid, pos, D, a.theta));
-        if (tid < D) {
-            knew[tid] = kr;
-            const f16_t vv = a.vr[(size_t)h * D + tid];
-            vnew[tid] = (float)vv;
-            a.kc[(size_t)h * a.max_ctx * D + (size_t)pos * D + tid] = (f16_t)kr;
-            a.vc[(size_t)h * D * a.max_ctx + (size_t)tid * a.max_ctx + pos] = vv;
-        }
-    }
     __syncthreads();
 
-    // ---- scores: TPT consecutive lanes per token, each dotting D/TPT
-    // dimensions with 16-byte K loads (the new row comes from LDS)
-    const size_t kv_stride = (size_t)a.max_ctx * D;
-    const f16_t *kb = a.kc + h * kv_stride;
-    constexpr int VPL = D / 8 / TPT;   // 16-byte vectors per lane
-    const int sub = tid % TPT;
-    for (uint32_t t = tid / TPT; t < ceil_div(len, 256 / TPT) * (256 / TPT); t += 256 / TPT) {
+    // ---- scores: TPT consecutive lanes per token
+    {
         float dot[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) dot[g] = 0.f;
-        if (t < len) {
-            if (t0 + t == pos) {
-                for (int d = sub * VPL * 8; d < (sub + 1) * VPL * 8; ++d)
+        const bool is_new = owns_new && t0 + (uint32_t)kt == pos;
 #pragma unroll
-                    for (int g = 0; g < G; ++g) dot[g] = fmaf(qs[g][d], knew[d], dot[g]);
-            } else {
-                const uint4 *kr = (const uint4 *)(kb + (size_t)(t0 + t) * D) + sub * VPL;
-#pragma unroll 4
-                for (int v = 0; v < VPL; ++v) {
-                    const uint4 w = kr[v];
-                    const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+        for (int v = 0; v < KV4; ++v) {
+            const uint32_t wv[4] = {kreg[v].x, kreg[v].y, kreg[v].z, kreg[v].w};
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        float k0, k1;
-                        unpack2<NNZ_F16>(wv[e], k0, k1);
-                        const int d = (sub * VPL + v) * 8 + 2 * e;
+            for (int e = 0; e < 4; ++e) {
+                const int d = (ksub * KV4 + v) * 8 + 2 * e;
+                float k0, k1;
+                unpack2<NNZ_F16>(wv[e], k0, k1);
+                if (is_new) { k0 = knew[d]; k1 = knew[d + 1]; }
 #pragma unroll
-                        for (int g = 0; g < G; ++g)
-                            dot[g] = fmaf(qs[g][d + 1], k1, fmaf(qs[g][d], k0, dot[g]));
-                    }
-                }
+                for (int g = 0; g < G; ++g) dot[g] = fmaf(qs[g][d + 1], k1, fmaf(qs[g][d], k0, dot[g]));
             }
         }
 #pragma unroll
@@ -577,70 +607,61 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
 #pragma unroll
             for (int o = TPT / 2; o >= 1; o >>= 1) dot[g] += __shfl_xor(dot[g], o, 64);
         }
-        if (sub == 0 && t < len) {
+        if (ksub == 0) {
 #pragma unroll
-            for (int g = 0; g < G; ++g) ps[g][t] = dot[g] * a.scale;
+            for (int g = 0; g < G; ++g) ps[g][kt] = (uint32_t)kt < len ? dot[g] * a.scale : -INFINITY;
         }
     }
     __syncthreads();
 
+    // ---- softmax over the chunk, all G heads at once.  FCHUNK <= 64, so
+    // every wave sees the whole chunk and computes the same max and sum.
+    static_assert(FCHUNK <= 64, "softmax assumes one wave covers the chunk");
     float mval[G], lval[G];
+    {
+        const int lane = tid & 63;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-        float m = -INFINITY;
-        for (uint32_t t = tid; t < len; t += 256) m = fmaxf(m, ps[g][t]);
-        m = block_max_256(m, red);
-        float l = 0.f;
-        for (uint32_t t = tid; t < len; t += 256) {
-            const float e = expf(ps[g][t] - m);
-            ps[g][t] = e;
-            l += e;
+        for (int g = 0; g < G; ++g) {
+            const float sc = lane < FCHUNK ? ps[g][lane] : -INFINITY;
+            mval[g] = wave_max(sc);
+            const float e = lane < FCHUNK ? expf(sc - mval[g]) : 0.f;
+            lval[g] = wave_sum(e);
+            if (tid < FCHUNK) pe[g][lane] = e;
         }
-        l = block_sum_256(l, red);
-        mval[g] = m;
-        lval[g] = l;
     }
     __syncthreads();
 
-    // ---- P.V: a thread owns one d and streams 8 tokens per 16-byte load
-    constexpr int PARTS = 256 / D;
+    // ---- P.V from the prefetched V (new token from LDS)
     {
-        const int d = tid % D, part = tid / D;
         float o[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) o[g] = 0.f;
-        const uint32_t ngroups = len / 8;
-        const uint32_t per = ceil_div(ngroups, PARTS);
-        const uint32_t k0 = part * per, k1 = min(ngroups, k0 + per);
-        const f16_t *row = a.vc + h * kv_stride + (size_t)d * a.max_ctx + t0;
-        for (uint32_t k = k0; k < k1; ++k) {
-            const uint4 w = *(const uint4 *)(row + 8 * k);
-            const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
-            float vv[8];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) unpack2<NNZ_F16>(wv[e], vv[2 * e], vv[2 * e + 1]);
-            if (owns_new && pos >= t0 + 8 * k && pos < t0 + 8 * k + 8) vv[pos - t0 - 8 * k] = vnew[d];
+        for (int v = 0; v < VV4; ++v) {
+            const uint32_t wv[4] = {vreg[v].x, vreg[v].y, vreg[v].z, vreg[v].w};
 #pragma unroll
-            for (int e = 0; e < 8; ++e)
+            for (int e = 0; e < 4; ++e) {
+                const int t = vpart * VT + v * 8 + 2 * e;
+                float v0, v1;
+                unpack2<NNZ_F16>(wv[e], v0, v1);
+                // past the end: weight 0, value 0 (never NaN * 0)
+                v0 = (uint32_t)t < len ? v0 : 0.f;
+                v1 = (uint32_t)t + 1 < len ? v1 : 0.f;
+                if (owns_new && t0 + t == pos) v0 = vnew[vd];
+                if (owns_new && t0 + t + 1 == pos) v1 = vnew[vd];
 #pragma unroll
-                for (int g = 0; g < G; ++g) o[g] = fmaf(ps[g][8 * k + e], vv[e], o[g]);
-        }
-        if (part == PARTS - 1) {
-            for (uint32_t t = ngroups * 8; t < len; ++t) {
-                const float v = (t0 + t == pos) ? vnew[d] : (float)row[t];
-#pragma unroll
-                for (int g = 0; g < G; ++g) o[g] = fmaf(ps[g][t], v, o[g]);
+                for (int g = 0; g < G; ++g) o[g] = fmaf(pe[g][t + 1], v1, fmaf(pe[g][t], v0, o[g]));
             }
         }
 #pragma unroll
-        for (int g = 0; g < G; ++g) ored[part][g][d] = o[g];
+        for (int g = 0; g < G; ++g) ored[vpart][g][vd] = o[g];
     }
     __syncthreads();
 
-    // One chunk: final output.  Several: partials for attn_combine_kernel
-    // (merging inside this kernel would need an agent-scope fence between
-    // workgroups, which on a multi-XCD part writes back and invalidates the
-    // XCD's L2 -- a kernel boundary is the cheaper synchronisation).
+    // One chunk: final output.  Several: partials for attn_merge_kernel
+    // (merging here would need an agent-scope fence between workgroups,
+    // which on a multi-XCD part writes back and invalidates the XCD's L2;
+    // a kernel boundary is the cheaper synchronisation).
     for (int i = tid; i < G * D; i += 256) {
         const int g = i / D, d = i % D;
         float s = 0.f;
@@ -657,6 +678,54 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
             }
         }
     }
+}
+
+// Fold the per-chunk partials of attn_fused_kernel: grid Hq, block 128.
+// The first MERGE_PRE chunks' (m, l) pairs and outputs are loaded in one
+// round together with seq_len -- (m, l) by one lane per chunk and shared
+// through LDS, so the loads stay vector loads; longer sequences loop over
+// the rest.
+constexpr int MERGE_PRE = 16;
+
+__global__ __launch_bounds__(128) void attn_merge_kernel(const float *part_o, const float *part_ml,
+                                                         f16_t *out, const uint32_t *d_seq,
+                                                         uint32_t seq_len, uint32_t nchunks,
+                                                         uint32_t D) {
+    __shared__ float2 ml_s[MERGE_PRE];
+    const uint32_t seq = d_seq ? *d_seq : seq_len;
+    const uint32_t qh = blockIdx.x, d = threadIdx.x;
+    const size_t base = (size_t)qh * nchunks;
+    const uint32_t dd = d < D ? d : 0u;
+    const float2 mlv = *(const float2 *)(part_ml + (base + min(d % MERGE_PRE, nchunks - 1)) * 2);
+    float o[MERGE_PRE];
+#pragma unroll
+    for (int c = 0; c < MERGE_PRE; ++c) {
+        const uint32_t cc = min((uint32_t)c, nchunks - 1);
+        o[c] = part_o[(base + cc) * D + dd];
+    }
+    if (d < MERGE_PRE) ml_s[d] = mlv;
+    __syncthreads();
+    if (d >= D) return;
+    const uint32_t nch = min(nchunks, ceil_div(seq, (uint32_t)FCHUNK));
+    float M = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < MERGE_PRE; ++c) M = (uint32_t)c < nch ? fmaxf(M, ml_s[c].x) : M;
+    for (uint32_t c = MERGE_PRE; c < nch; ++c) M = fmaxf(M, part_ml[(base + c) * 2]);
+    float num = 0.f, den = 0.f;
+#pragma unroll
+    for (int c = 0; c < MERGE_PRE; ++c) {
+        if ((uint32_t)c < nch) {
+            const float w = expf(ml_s[c].x - M);
+            den = fmaf(w, ml_s[c].y, den);
+            num = fmaf(w, o[c], num);
+        }
+    }
+    for (uint32_t c = MERGE_PRE; c < nch; ++c) {
+        const float w = expf(part_ml[(base + c) * 2] - M);
+        den = fmaf(w, part_ml[(base + c) * 2 + 1], den);
+        num = fmaf(w, part_o[(base + c) * D + d], num);
+    }
+    out[(size_t)qh * D + d] = (f16_t)(num / den);
 }
 
 // -------------------------------------------------------------- embedding --
@@ -779,8 +848,10 @@ uint32_t nnz_attn_chunk(uint32_t seq_len, uint32_t hkv) {
 
 size_t nnz_attn_scratch_bytes_impl(uint32_t hq, uint32_t head_dim, uint32_t seq_len,
                                    uint32_t hkv) {
-    const uint32_t chunk = nnz_attn_chunk(seq_len, hkv);
-    const uint32_t nch = ceil_div(seq_len, chunk);
+    // the fused decode path splits into FCHUNK-token chunks, the split
+    // kernel into nnz_attn_chunk ones (never shorter): size for the former
+    const uint32_t nch = ceil_div(seq_len, (uint32_t)FCHUNK);
+    (void)hkv;
     // partial outputs + (m, l) pairs + one f32 q buffer for the fused path
     return ((size_t)hq * nch * head_dim + (size_t)hq * nch * 2 + (size_t)hq * head_dim) * 4 + 256;
 }
@@ -903,28 +974,9 @@ int nnz_attn_launch(nnz_ctx *ctx, const void *q, int qdt, const void *kc, const 
     return nnz_attn_launch_ex(ctx, c);
 }
 
-// Chunk length of the fused decode attention for sequences up to max_seq.
-// Never shorter than nnz_attn_chunk's, so the partials fit the same scratch.
-// The NNZ_ATTN_FUSED_CHUNK environment variable (a power of two, 64..1024)
-// raises it, for tuning.
-uint32_t nnz_attn_fused_chunk(uint32_t max_seq, uint32_t hkv) {
-    static const uint32_t forced = [] {
-        const char *e = getenv("NNZ_ATTN_FUSED_CHUNK");
-        const uint32_t v = e ? (uint32_t)strtoul(e, nullptr, 10) : 0u;
-        return (v >= 64 && v <= (uint32_t)FUSED_MAX_CHUNK && (v & (v - 1)) == 0) ? v : 0u;
-    }();
-    const uint32_t base = nnz_attn_chunk(max_seq, hkv);
-    const uint32_t want = forced ? forced : base;
-    return want > base ? want : base;
-}
-
-template <int D, int G>
-static void launch_fused_t(nnz_ctx *ctx, const FusedAttnArgs &a, dim3 grid) {
-    // lanes per token: all 256 lanes busy in the score pass when possible
-    if (a.chunk >= 256) attn_fused_kernel<D, G, 1><<<grid, 256, 0, ctx->stream>>>(a);
-    else if (a.chunk >= 128) attn_fused_kernel<D, G, 2><<<grid, 256, 0, ctx->stream>>>(a);
-    else attn_fused_kernel<D, G, 4><<<grid, 256, 0, ctx->stream>>>(a);
-}
+// Chunk length of the fused decode attention (fixed: the kernel prefetches
+// a whole chunk into registers).
+uint32_t nnz_attn_fused_chunk(uint32_t, uint32_t) { return (uint32_t)FCHUNK; }
 
 // Fused decode attention (see attn_fused_kernel).  `max_seq` sizes the grid;
 // the live seq_len is d_seq ? *d_seq : max_seq.  part_o / part_ml hold
@@ -957,13 +1009,12 @@ int nnz_attn_fused1_launch(nnz_ctx *ctx, const void *q, const void *kr, const vo
     a.d_seq = d_seq;
     a.seq_len = max_seq;
     a.max_ctx = max_ctx;
-    a.chunk = nnz_attn_fused_chunk(max_seq, hkv);
-    a.nchunks = ceil_div(max_seq, a.chunk);
+    a.nchunks = ceil_div(max_seq, (uint32_t)FCHUNK);
     a.eps = eps;
     a.theta = theta;
     a.scale = 1.0f / sqrtf((float)head_dim);
     dim3 grid(a.nchunks, hkv);
-#define FUSED(DD, GG) launch_fused_t<DD, GG>(ctx, a, grid)
+#define FUSED(DD, GG) attn_fused_kernel<DD, GG><<<grid, 256, 0, ctx->stream>>>(a)
     if (head_dim == 128) {
         if (G == 1) FUSED(128, 1);
         else if (G == 2) FUSED(128, 2);
@@ -980,18 +1031,8 @@ int nnz_attn_fused1_launch(nnz_ctx *ctx, const void *q, const void *kr, const vo
 #undef FUSED
     NNZ_LAUNCHED(ctx);
     if (a.nchunks > 1) {
-        AttnArgs m{};
-        m.out = out;
-        m.odt = NNZ_F16;
-        m.part_o = part_o;
-        m.part_ml = part_ml;
-        m.d_seq = d_seq;
-        m.seq_len = max_seq;
-        m.chunk = a.chunk;
-        m.nchunks = a.nchunks;
-        m.hq = hq;
-        m.o_stride = hq * head_dim;
-        attn_combine_kernel<<<dim3(hq, 1), 128, 0, ctx->stream>>>(m, head_dim);
+        attn_merge_kernel<<<hq, 128, 0, ctx->stream>>>(part_o, part_ml, (f16_t *)out, d_seq, max_seq,
+                                                       a.nchunks, head_dim);
         NNZ_LAUNCHED(ctx);
     }
     return NNZ_OK;

@@ -116,18 +116,33 @@ class Rot:
 
 
 def time_launches(dev, fn, n_iter, reps=3):
-    """Average duration of one launch: events around n_iter back-to-back
-    launches on the library stream, best of ``reps`` blocks."""
+    """Average duration of one launch as the decoder runs it: ``n_iter``
+    launches captured into one hipGraph on the library stream and replayed,
+    HIP events around each replay, best of ``reps`` replays."""
+    import ctypes as C
+    from nnzap_amd import _lib as L
+
     fn(0)
     dev.sync()
-    best = None
-    for r in range(reps):
-        dev.mark(0)
+    g = C.c_void_p()
+    dev.call("nnz_graph_begin")
+    try:
         for i in range(n_iter):
-            fn(i + 1 + r * n_iter)
-        dev.mark(1)
-        ms = dev.elapsed_ms(0, 1) / n_iter
-        best = ms if best is None else min(best, ms)
+            fn(i + 1)
+    finally:
+        dev.call("nnz_graph_end", C.byref(g))
+    try:
+        dev.call("nnz_graph_replay", g)
+        dev.sync()
+        best = None
+        for _ in range(reps):
+            dev.mark(0)
+            dev.call("nnz_graph_replay", g)
+            dev.mark(1)
+            ms = dev.elapsed_ms(0, 1) / n_iter
+            best = ms if best is None else min(best, ms)
+    finally:
+        L.lib().nnz_graph_destroy(g)
     return best * 1000.0  # us
 
 

@@ -2,6 +2,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <math.h>
 #include <stdint.h>
 #include <stdarg.h>
 #include <stdio.h>
@@ -106,14 +107,53 @@ __device__ __forceinline__ float group_sum(float v, int width) {
     return v;
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+// Whole-wave reductions with DPP lane moves (VALU instructions, no LDS
+// round trip per step): swap lanes within quads (xor 1, xor 2), mirror
+// within 8 and 16 lanes, then broadcast lane 15 of each 16-lane row into
+// rows 1 and 3 and lane 31 into rows 2 and 3.  Lanes 48..63 end with the
+// total; rows a step leaves unwritten read `neutral`.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_move(float v, float neutral) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(neutral), __float_as_int(v), CTRL,
+                                                      ROW_MASK, 0xF, false));
+}
+
+enum : int {
+    DPP_XOR1 = 0xB1,         // quad_perm [1,0,3,2]
+    DPP_XOR2 = 0x4E,         // quad_perm [2,3,0,1]
+    DPP_ROW_MIRROR = 0x140,
+    DPP_ROW_HALF_MIRROR = 0x141,
+    DPP_ROW_BCAST15 = 0x142,
+    DPP_ROW_BCAST31 = 0x143,
+};
+
+// Sum over the wave; the total is valid in lane 63.
+__device__ __forceinline__ float wave_sum_to_last(float v) {
+    v += dpp_move<DPP_XOR1>(v, 0.f);
+    v += dpp_move<DPP_XOR2>(v, 0.f);
+    v += dpp_move<DPP_ROW_HALF_MIRROR>(v, 0.f);
+    v += dpp_move<DPP_ROW_MIRROR>(v, 0.f);
+    v += dpp_move<DPP_ROW_BCAST15, 0xA>(v, 0.f);
+    v += dpp_move<DPP_ROW_BCAST31, 0xC>(v, 0.f);
     return v;
 }
 
+__device__ __forceinline__ float lane63(float v) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Sum / max over the wave, returned in every lane.
+__device__ __forceinline__ float wave_sum(float v) { return lane63(wave_sum_to_last(v)); }
+
 __device__ __forceinline__ float wave_max(float v) {
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
+    const float n = -INFINITY;
+    v = fmaxf(v, dpp_move<DPP_XOR1>(v, n));
+    v = fmaxf(v, dpp_move<DPP_XOR2>(v, n));
+    v = fmaxf(v, dpp_move<DPP_ROW_HALF_MIRROR>(v, n));
+    v = fmaxf(v, dpp_move<DPP_ROW_MIRROR>(v, n));
+    v = fmaxf(v, dpp_move<DPP_ROW_BCAST15, 0xA>(v, n));
+    v = fmaxf(v, dpp_move<DPP_ROW_BCAST31, 0xC>(v, n));
+    return lane63(v);
 }
 
 // Dtype size in bytes for the public element types.

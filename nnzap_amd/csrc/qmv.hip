@@ -204,29 +204,6 @@ __device__ __forceinline__ void load_step(const QmvArgs &a, StepRegs<NMAT, R, NV
     }
 }
 
-// Sum N per-lane values over the 64 lanes of a wave; returns, in lane l, the
-// total of value index (l >> (6 - log2 N)) & (N - 1).  Each halving step
-// keeps half of the values and trades the other half with the partner lane.
-template <int N>
-__device__ __forceinline__ float butterfly_sum(const float (&v)[N], int lane) {
-    float cur[N];
-#pragma unroll
-    for (int j = 0; j < N; ++j) cur[j] = v[j];
-    int off = 32;
-#pragma unroll
-    for (int n = N; n > 1; n >>= 1, off >>= 1) {
-        const bool upper = (lane & off) != 0;
-#pragma unroll
-        for (int j = 0; j < n / 2; ++j) {
-            const float keep = upper ? cur[j + n / 2] : cur[j];
-            const float send = upper ? cur[j] : cur[j + n / 2];
-            cur[j] = keep + __shfl_xor(send, off, 64);
-        }
-    }
-    for (; off > 0; off >>= 1) cur[0] += __shfl_xor(cur[0], off, 64);
-    return cur[0];
-}
-
 // Store / residual-add / SiLU epilogue of one row.  `row` indexes the pair
 // outputs and the residual, `lrow` the row within the step's segment.
 template <int EPI, int ODT, bool FAITH, int NMAT>
@@ -257,8 +234,9 @@ __device__ __forceinline__ void qmv_epilogue(const QmvArgs &a, void *out0, uint3
     }
 }
 
-template <int BITS, int XDT, int NMAT, bool NORM, int EPI, int ODT, bool FAITH, int NV, int R>
+template <int BITS, int XDT, int NMAT, bool NORM, int EPI, int ODT, bool FAITH, int NV, int R, bool LUT>
 __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
+    static_assert(!LUT || BITS == 1, "nibble tables are for 1-bit weights");
     constexpr int VEC = (BITS == 1) ? 1 : 4;  // u32 words per 32-column unit
     const int lane = threadIdx.x & 63;
     const int lpr_log2 = (int)a.lpr_log2;
@@ -394,6 +372,36 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
         xsum[j] = s;
     }
 
+    // ---- 1-bit nibble tables (LUT, full-wave rows only) --------------------
+    // For each owned unit j and nibble n (columns 4n..4n+3 of the unit), the
+    // 16 subset sums T[e] = sum_{k in e} x[4n+k], so a row's sum over its set
+    // bits is 8 table reads per 32 weights instead of 32 mask-and-adds.  All
+    // waves of a block own the same columns: wave w builds nibbles 2w, 2w+1
+    // of every unit and the block shares the tables through LDS, laid out
+    // [unit][nibble][entry][lane] so a wave's 64 reads hit 64 distinct banks.
+    __shared__ float lut[LUT ? NV * 8 * 16 * 64 : 1];
+    if constexpr (LUT) {
+        const int wid = threadIdx.x >> 6;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+#pragma unroll
+            for (int n = 0; n < 8; ++n) {
+                if ((n >> 1) != wid) continue;   // wave-uniform
+                const float x0 = xr[j][4 * n], x1 = xr[j][4 * n + 1];
+                const float x2 = xr[j][4 * n + 2], x3 = xr[j][4 * n + 3];
+                float t[16];
+                t[0] = 0.f; t[1] = x0; t[2] = x1; t[3] = x0 + x1;
+                t[4] = x2; t[5] = x2 + x0; t[6] = x2 + x1; t[7] = x2 + t[3];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) t[8 + e] = e == 0 ? x3 : x3 + t[e];
+                float *dst = lut + ((j * 8 + n) * 16) * 64 + lane;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) dst[e * 64] = t[e];
+            }
+        }
+        __syncthreads();
+    }
+
     // ---- software-pipelined row loop ---------------------------------------
     for (; base < a.M; base += nwaves * rows_per_iter) {
         const uint32_t next = base + nwaves * rows_per_iter;
@@ -410,7 +418,14 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
 #pragma unroll
                 for (int j = 0; j < NV; ++j) {
                     const float s = cur.ok[m][r][j] ? scale_to_f32(cur.sc[m][r][j], (int)a.sdt) : 0.f;
-                    if constexpr (BITS == 1) {
+                    if constexpr (BITS == 1 && LUT) {
+                        const uint32_t w = cur.cw[m][r][j][0];
+                        const float *tb = lut + (j * 8 * 16) * 64 + lane;
+                        float sb = 0.f;
+#pragma unroll
+                        for (int n = 0; n < 8; ++n) sb += tb[(n * 16 + ((w >> (4 * n)) & 15u)) * 64];
+                        accv = fmaf(s, 2.f * sb - xsum[j], accv);
+                    } else if constexpr (BITS == 1) {
                         const uint32_t w = cur.cw[m][r][j][0];
                         float sb = 0.f;
 #pragma unroll
@@ -442,25 +457,33 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                 acc[m][r] = accv;
             }
 
-        // Row sums.  Full-wave rows (LPR == 64): a butterfly folds the R
-        // partial sums of each matrix together, leaving row r's total in
-        // lanes [r*64/R, (r+1)*64/R) -- log2(R) + 6 - log2(R) shuffles per
-        // matrix instead of 6 per row.  Narrow rows: plain group sums.
+        // Row sums: DPP reductions for full-wave rows, lane-group
+        // shuffles for narrow ones.
         uint32_t seg_start = 0;
         int seg = 0;
         if constexpr (NMAT == 1) seg = step_segment(a, base, seg_start);
         void *out0 = NMAT == 1 ? (void *)seg_mat(a, seg).out : a.m0.out;
         if (LPR == 64) {
+            // Each row's total by a DPP reduction (lands in lane 63, read
+            // back as a wave-uniform value); lane r then stores row base+r.
+            float rt[NMAT][R];
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+                for (int r = 0; r < R; ++r) rt[m][r] = lane63(wave_sum_to_last(acc[m][r]));
             float tot[NMAT];
 #pragma unroll
-            for (int m = 0; m < NMAT; ++m) tot[m] = butterfly_sum<R>(acc[m], lane);
-            constexpr int LOG_R = R == 4 ? 2 : (R == 2 ? 1 : 0);
-            const int r = (lane >> (6 - LOG_R)) & (R - 1);
-            const uint32_t row = base + (uint32_t)r;  // RPW == 1
+            for (int m = 0; m < NMAT; ++m) {
+                float t = rt[m][0];
+#pragma unroll
+                for (int k = 1; k < R; ++k) t = lane == k ? rt[m][k] : t;
+                tot[m] = t;
+            }
             float prev = cur.res[0];
 #pragma unroll
-            for (int k = 1; k < R; ++k) prev = r == k ? cur.res[k] : prev;
-            if ((lane & ((64 / R) - 1)) == 0 && row < a.M)
+            for (int k = 1; k < R; ++k) prev = lane == k ? cur.res[k] : prev;
+            const uint32_t row = base + (uint32_t)lane;  // RPW == 1
+            if (lane < R && row < a.M)
                 qmv_epilogue<EPI, ODT, FAITH, NMAT>(a, out0, row, row - seg_start, tot, prev);
         } else {
 #pragma unroll
@@ -513,22 +536,42 @@ int check_dims(nnz_ctx *ctx, const nnz_qmv_dims &d, const char *name) {
     return NNZ_OK;
 }
 
+// Nibble tables take NV * 32 KB of LDS per block.
+constexpr int LUT_MAX_NV = 3;
+
 // Weight words a lane holds for one row-step; the host keeps it <= 32.
 constexpr int step_words(int BITS, int NMAT, int NV, int R) { return NMAT * R * NV * (BITS == 1 ? 1 : 4); }
 
-template <int BITS, int XDT, int NMAT, bool NORM, int EPI, int ODT, bool FAITH, int NV>
-int launch_nv(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks) {
+template <int BITS, int XDT, int NMAT, bool NORM, int EPI, int ODT, bool FAITH, int NV, bool LUT>
+void launch_r(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks) {
     dim3 grid(blocks), block(256);
+    if (R == 8) {
+        // long matrices only (the 1-bit LM head): more rows in flight per wave
+        if constexpr (LUT && step_words(BITS, NMAT, NV, 8) <= 32)
+            qmv_kernel<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, 8, LUT><<<grid, block, 0, ctx->stream>>>(a);
+        else R = 4;
+    }
     if (R == 4) {
         if constexpr (step_words(BITS, NMAT, NV, 4) <= 32)
-            qmv_kernel<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, 4><<<grid, block, 0, ctx->stream>>>(a);
+            qmv_kernel<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, 4, LUT><<<grid, block, 0, ctx->stream>>>(a);
         else R = 1;
     } else if (R == 2) {
         if constexpr (step_words(BITS, NMAT, NV, 2) <= 32)
-            qmv_kernel<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, 2><<<grid, block, 0, ctx->stream>>>(a);
+            qmv_kernel<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, 2, LUT><<<grid, block, 0, ctx->stream>>>(a);
         else R = 1;
     }
-    if (R == 1) qmv_kernel<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, 1><<<grid, block, 0, ctx->stream>>>(a);
+    if (R == 1)
+        qmv_kernel<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, 1, LUT><<<grid, block, 0, ctx->stream>>>(a);
+}
+
+template <int BITS, int XDT, int NMAT, bool NORM, int EPI, int ODT, bool FAITH, int NV>
+int launch_nv(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks, bool lut) {
+    if constexpr (BITS == 1 && NV <= LUT_MAX_NV) {
+        if (lut) launch_r<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, true>(ctx, a, R, blocks);
+        else launch_r<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, false>(ctx, a, R, blocks);
+    } else {
+        launch_r<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, false>(ctx, a, R, blocks);
+    }
     NNZ_LAUNCHED(ctx);
     return NNZ_OK;
 }
@@ -575,6 +618,13 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
     // Keep >= 2 waves of work per CU where the matrix allows, and bound the
     // number of weight words a lane holds in flight (two steps are live).
     while (R > 1 && (ceil_div(d.M, 4u * R * rpw) < 512 || NMAT * R * (int)nv * vec > 32)) R >>= 1;
+    // 1-bit full-wave rows may use the nibble tables.  Building them is a
+    // fixed cost per block that pays off from about four matrix rows per
+    // wave: pairs take two rows per wave; single matrices only when the
+    // grid cap below leaves each wave many rows.
+    bool lut = BITS == 1 && lpr == 64 && nv <= (uint32_t)LUT_MAX_NV;
+    if (lut && NMAT == 2 && R < 2 && 2 * 2 * (int)nv * vec <= 32) R = 2;
+    if (lut && NMAT == 1 && d.M >= 4u * 2048u * 8u) R = 8;   // e.g. a vocabulary-sized LM head
     if (NMAT == 1 && nw > 1) {  // a step must not straddle two segments
         auto aligned = [&](uint32_t step) {
             for (int i = 0; i < nw; ++i)
@@ -591,6 +641,7 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
     // that over several row-steps per wave.
     const uint32_t max_blocks = NORM ? 1024u : 2048u;
     if (blocks > max_blocks) blocks = max_blocks;
+    if (lut && NMAT * ceil_div(d.M, blocks * 4u) < 4u) lut = false;
 
     QmvArgs a{};
     for (int i = 0; i < nw; ++i) {
@@ -615,10 +666,10 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
     a.sdt = w[0]->scale_dtype;
     a.eps = 1e-6f;
     switch (nv) {
-    case 1: return launch_nv<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, 1>(ctx, a, R, blocks);
-    case 2: return launch_nv<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, 2>(ctx, a, R, blocks);
-    case 3: return launch_nv<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, 3>(ctx, a, R, blocks);
-    default: return launch_nv<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, 4>(ctx, a, R, blocks);
+    case 1: return launch_nv<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, 1>(ctx, a, R, blocks, lut);
+    case 2: return launch_nv<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, 2>(ctx, a, R, blocks, lut);
+    case 3: return launch_nv<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, 3>(ctx, a, R, blocks, lut);
+    default: return launch_nv<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, 4>(ctx, a, R, blocks, lut);
     }
 }
 

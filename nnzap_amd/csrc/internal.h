@@ -26,6 +26,7 @@ struct NnzAttnCall {
 
 uint32_t nnz_attn_chunk(uint32_t seq_len, uint32_t hkv);
 uint32_t nnz_attn_fused_chunk(uint32_t max_seq, uint32_t hkv);
+int nnz_rope_table_launch(nnz_ctx *ctx, float *out, uint32_t head_dim, float theta);
 int nnz_attn_launch_ex(nnz_ctx *ctx, const NnzAttnCall &c);
 int nnz_attn_prep_launch(nnz_ctx *ctx, const void *q, const void *kr, const void *vr,
                          const float *qn, const float *kn, float *qout, void *kc, void *vc,
@@ -35,8 +36,9 @@ int nnz_attn_prep_launch(nnz_ctx *ctx, const void *q, const void *kr, const void
 int nnz_argmax_launch(nnz_ctx *ctx, const float *x, uint32_t n, uint32_t *oi, float *ov);
 int nnz_attn_fused1_launch(nnz_ctx *ctx, const void *q, const void *kr, const void *vr,
                            const float *qn, const float *kn, void *kc, void *vc, void *out,
-                           float *part_o, float *part_ml, const uint32_t *d_seq, uint32_t max_seq, uint32_t hq, uint32_t hkv,
-                           uint32_t head_dim, uint32_t max_ctx, float eps, float theta);
+                           float *part_o, float *part_ml, const uint32_t *d_seq, uint32_t max_seq,
+                           uint32_t hq, uint32_t hkv, uint32_t head_dim, uint32_t max_ctx, float eps, float theta,
+                           const float *inv_freq);
 int nnz_qmv_norm_qkv_launch(nnz_ctx *ctx, const nnz_qweight *wq, const nnz_qweight *wk,
                             const nnz_qweight *wv, const float *residual, const float *norm_w,
                             void *q, void *k, void *v, uint32_t qrows, uint32_t kvrows, uint32_t K,

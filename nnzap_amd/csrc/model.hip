@@ -225,6 +225,7 @@ struct nnz_model {
     f16_t *xn = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *att = nullptr, *h = nullptr;
     float *part_o = nullptr, *part_ml = nullptr;
     uint32_t part_chunks = 0;  // capacity in chunks per query head
+    float *rope_inv = nullptr;     // [head_dim/2] RoPE frequencies
     Top2 *top2 = nullptr;          // [ARGMAX_BLOCKS] argmax partials
     uint32_t *state = nullptr;
     uint32_t *tokens_out = nullptr;
@@ -344,7 +345,7 @@ int enqueue_decode_step(nnz_model *m, uint32_t max_seq) {
         RC(nnz_attn_fused1_launch(ctx, m->q, m->k, m->v, Ly.q_norm, Ly.k_norm, Ly.kc, Ly.vc, m->att,
                                   m->part_o, m->part_ml, m->state + ST_SEQ, max_seq,
                                   c.num_query_heads, c.num_kv_heads, c.head_dim,
-                                  c.max_context_length, c.rms_eps, c.rope_theta));
+                                  c.max_context_length, c.rms_eps, c.rope_theta, m->rope_inv));
         RC(nnz_dispatch_qmv_f16io_resadd(ctx, &Ly.o.w, m->att, m->residual, dims_of(m, Ly.o)));
         // transformer.zig:3372-3646 encodeMLPHalf (fused norm + gate/up + SiLU, down += )
         RC(nnz_dispatch_fused_norm_pair_silu_f16io(ctx, &Ly.gate.w, &Ly.up.w, m->residual, m->h,
@@ -489,6 +490,8 @@ int nnz_model_create(nnz_ctx *ctx, const nnz_model_config *cfg, nnz_model **out)
         m->part_ml = parts + (size_t)c.num_query_heads * m->part_chunks * c.head_dim;
         MALLOC(m->top2, (size_t)ARGMAX_BLOCKS * sizeof(Top2));
         MALLOC(m->state, 64);
+        MALLOC(m->rope_inv, (size_t)c.head_dim / 2 * 4);
+        RC(nnz_rope_table_launch(ctx, m->rope_inv, c.head_dim, c.rope_theta));
         m->out_cap = c.max_context_length + 1;
         MALLOC(m->tokens_out, (size_t)m->out_cap * 4);
         MALLOC(m->margins_out, (size_t)m->out_cap * 4);

@@ -20,12 +20,23 @@ __device__ __forceinline__ float rope_inv_freq(int pair, int head_dim, float the
 
 // Rotate element d of a head given its partner (d^1); consecutive-pair RoPE
 // (transformer.metal:154-202).
-__device__ __forceinline__ float rope_rotate(float self, float partner, int d, uint32_t position,
-                                             int head_dim, float theta) {
-    const float ang = (float)position * rope_inv_freq(d >> 1, head_dim, theta);
+__device__ __forceinline__ float rope_rotate_f(float self, float partner, int d, uint32_t position,
+                                               float inv_freq) {
+    const float ang = (float)position * inv_freq;
     float s, c;
     sincosf(ang, &s, &c);
     return (d & 1) ? fmaf(partner, s, self * c) : fmaf(self, c, -partner * s);
+}
+
+__device__ __forceinline__ float rope_rotate(float self, float partner, int d, uint32_t position,
+                                             int head_dim, float theta) {
+    return rope_rotate_f(self, partner, d, position, rope_inv_freq(d >> 1, head_dim, theta));
+}
+
+// The head_dim/2 frequencies once, for kernels that take them from memory.
+__global__ void rope_table_kernel(float *out, uint32_t head_dim, float theta) {
+    const uint32_t p = threadIdx.x;
+    if (p < head_dim / 2) out[p] = rope_inv_freq((int)p, (int)head_dim, theta);
 }
 
 __device__ __forceinline__ float block_sum_256(float v, float *red) {
@@ -471,6 +482,7 @@ struct FusedAttnArgs {
     f16_t *out;                     // [Hq*D]
     float *part_o, *part_ml;        // [Hq][nchunks][D], [Hq][nchunks][2]
     const uint32_t *d_seq;          // device seq_len (= position + 1) or null
+    const float *inv_freq;          // [D/2] RoPE frequencies, or null (computed here)
     uint32_t seq_len, max_ctx, nchunks;
     float eps, theta, scale;
 };
@@ -517,6 +529,22 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
     const float kraw = (float)a.kr[(size_t)h * D + kd];
     const float knw = a.kn[kd];
     const f16_t vraw = a.vr[(size_t)h * D + kd];
+    float qfreq[NQ], kfreq;
+    if (a.inv_freq) {
+#pragma unroll
+        for (int k = 0; k < NQ; ++k) {
+            const int i = tid + 256 * k;
+            qfreq[k] = a.inv_freq[((i < G * D ? i : 0) % D) >> 1];
+        }
+        kfreq = a.inv_freq[kd >> 1];
+    } else {
+#pragma unroll
+        for (int k = 0; k < NQ; ++k) {
+            const int i = tid + 256 * k;
+            qfreq[k] = rope_inv_freq(((i < G * D ? i : 0) % D) >> 1, D, a.theta);
+        }
+        kfreq = rope_inv_freq(kd >> 1, D, a.theta);
+    }
 
     const size_t kv_stride = (size_t)a.max_ctx * D;
     const int kt = tid / TPT, ksub = tid % TPT;
@@ -560,7 +588,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
         if (D > 64) ss = red[0][0] + red[1][0];
         const float kn = kv * rsqrtf(ss / (float)D + a.eps) * knw;
         const float partner = __shfl_xor(kn, 1, 64);
-        const float kr = f16_round(rope_rotate(kn, partner, tid, pos, D, a.theta));
+        const float kr = f16_round(rope_rotate_f(kn, partner, tid, pos, kfreq));
         if (tid < D) {
             knew[tid] = kr;
             vnew[tid] = (float)vraw;
@@ -579,7 +607,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
         for (int w = 0; w < D / 64; ++w) ss += hsum[g][w];
         const float v = ok ? qv[k] * rsqrtf(ss / (float)D + a.eps) * qnv[k] : 0.f;
         const float partner = __shfl_xor(v, 1, 64);  // all lanes take part
-        if (ok) qs[g][d] = rope_rotate(v, partner, d, pos, D, a.theta);
+        if (ok) qs[g][d] = rope_rotate_f(v, partner, d, pos, qfreq[k]);
     }
     __syncthreads();
 
@@ -985,7 +1013,7 @@ int nnz_attn_fused1_launch(nnz_ctx *ctx, const void *q, const void *kr, const vo
                            const float *qn, const float *kn, void *kc, void *vc, void *out,
                            float *part_o, float *part_ml, const uint32_t *d_seq, uint32_t max_seq,
                            uint32_t hq, uint32_t hkv, uint32_t head_dim, uint32_t max_ctx, float eps,
-                           float theta) {
+                           float theta, const float *inv_freq) {
     NNZ_REQUIRE(ctx, q && kr && vr && qn && kn && kc && vc && out && part_o && part_ml,
                 NNZ_EINVAL, "gqa_fused_1pass: null buffer");
     NNZ_REQUIRE(ctx, hkv > 0 && hq % hkv == 0 && max_seq > 0 && max_seq <= max_ctx, NNZ_EINVAL,
@@ -1007,6 +1035,7 @@ int nnz_attn_fused1_launch(nnz_ctx *ctx, const void *q, const void *kr, const vo
     a.part_o = part_o;
     a.part_ml = part_ml;
     a.d_seq = d_seq;
+    a.inv_freq = inv_freq;
     a.seq_len = max_seq;
     a.max_ctx = max_ctx;
     a.nchunks = ceil_div(max_seq, (uint32_t)FCHUNK);
@@ -1035,6 +1064,15 @@ int nnz_attn_fused1_launch(nnz_ctx *ctx, const void *q, const void *kr, const vo
                                                        a.nchunks, head_dim);
         NNZ_LAUNCHED(ctx);
     }
+    return NNZ_OK;
+}
+
+// RoPE frequency table [head_dim / 2] (same values the kernels compute).
+int nnz_rope_table_launch(nnz_ctx *ctx, float *out, uint32_t head_dim, float theta) {
+    NNZ_REQUIRE(ctx, out && head_dim >= 2 && head_dim <= 256 && head_dim % 2 == 0, NNZ_EINVAL,
+                "rope table: bad head_dim %u", head_dim);
+    rope_table_kernel<<<1, 128, 0, ctx->stream>>>(out, head_dim, theta);
+    NNZ_LAUNCHED(ctx);
     return NNZ_OK;
 }
 
@@ -1251,7 +1289,7 @@ int nnz_dispatch_gqa_attention_fused_1pass(nnz_ctx *ctx, const void *q, void *k_
     return nnz_attn_fused1_launch(ctx, q, k_raw, v_raw, q_norm_scale, k_norm_scale, k_cache, v_cache,
                                   output, part_o, part_ml, d_seq_len, fd.seq_len,
                                   fd.num_query_heads, fd.num_kv_heads, fd.head_dim,
-                                  fd.max_context_length, fd.eps, fd.rope_theta);
+                                  fd.max_context_length, fd.eps, fd.rope_theta, nullptr);
 }
 
 int nnz_dispatch_embedding_lookup(nnz_ctx *ctx, const uint32_t *ids, const void *bits,

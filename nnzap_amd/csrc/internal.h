@@ -37,12 +37,19 @@ int nnz_argmax_launch(nnz_ctx *ctx, const float *x, uint32_t n, uint32_t *oi, fl
 int nnz_attn_fused1_launch(nnz_ctx *ctx, const void *q, const void *kr, const void *vr,
                            const float *qn, const float *kn, void *kc, void *vc, void *out,
                            float *part_o, float *part_ml, const uint32_t *d_seq, uint32_t max_seq,
-                           uint32_t hq, uint32_t hkv, uint32_t head_dim, uint32_t max_ctx, float eps, float theta,
-                           const float *inv_freq);
+                           uint32_t hq, uint32_t hkv, uint32_t head_dim, uint32_t max_ctx,
+                           float eps, float theta, const float *inv_freq,
+                           bool partials_only = false);
 int nnz_qmv_norm_qkv_launch(nnz_ctx *ctx, const nnz_qweight *wq, const nnz_qweight *wk,
                             const nnz_qweight *wv, const float *residual, const float *norm_w,
                             void *q, void *k, void *v, uint32_t qrows, uint32_t kvrows, uint32_t K,
                             uint32_t gs);
+// Largest attention chunk count the merge-in-O-projection path accepts.
+constexpr uint32_t NNZ_O_MERGE_MAX_CHUNKS = 16;
+int nnz_qmv_merge_resadd_launch(nnz_ctx *ctx, const nnz_qweight *w, const float *part_o,
+                                const float *part_ml, const uint32_t *d_seq, uint32_t seq_len,
+                                uint32_t nchunks, uint32_t chunk, uint32_t head_dim,
+                                float *residual, nnz_qmv_dims d);
 int nnz_qmv_norm_f32out_launch(nnz_ctx *ctx, const nnz_qweight *w, const float *residual,
                                const float *norm_w, float *out, nnz_qmv_dims d);
 int nnz_gemm_launch(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, const void *a,

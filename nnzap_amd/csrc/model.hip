@@ -342,11 +342,20 @@ int enqueue_decode_step(nnz_model *m, uint32_t max_seq) {
                                    m->k, m->v, m->qdim, m->kvdim, H, c.group_size));
         // transformer.zig:3244-3370 encodeAttentionGather: Q/K norm, RoPE, KV
         // append and attention in one launch, then O-proj with residual +=.
+        // Up to MERGE chunks of partials, the O-projection merges them itself.
+        const uint32_t nch = ceil_div(max_seq, nnz_attn_fused_chunk(max_seq, c.num_kv_heads));
+        const bool merge_in_o = nch <= NNZ_O_MERGE_MAX_CHUNKS;
         RC(nnz_attn_fused1_launch(ctx, m->q, m->k, m->v, Ly.q_norm, Ly.k_norm, Ly.kc, Ly.vc, m->att,
                                   m->part_o, m->part_ml, m->state + ST_SEQ, max_seq,
                                   c.num_query_heads, c.num_kv_heads, c.head_dim,
-                                  c.max_context_length, c.rms_eps, c.rope_theta, m->rope_inv));
-        RC(nnz_dispatch_qmv_f16io_resadd(ctx, &Ly.o.w, m->att, m->residual, dims_of(m, Ly.o)));
+                                  c.max_context_length, c.rms_eps, c.rope_theta, m->rope_inv,
+                                  merge_in_o));
+        if (merge_in_o)
+            RC(nnz_qmv_merge_resadd_launch(ctx, &Ly.o.w, m->part_o, m->part_ml, m->state + ST_SEQ,
+                                           max_seq, nch, nnz_attn_fused_chunk(max_seq, c.num_kv_heads),
+                                           c.head_dim, m->residual, dims_of(m, Ly.o)));
+        else
+            RC(nnz_dispatch_qmv_f16io_resadd(ctx, &Ly.o.w, m->att, m->residual, dims_of(m, Ly.o)));
         // transformer.zig:3372-3646 encodeMLPHalf (fused norm + gate/up + SiLU, down += )
         RC(nnz_dispatch_fused_norm_pair_silu_f16io(ctx, &Ly.gate.w, &Ly.up.w, m->residual, m->h,
                                                    Ly.ffn_norm, dims_of(m, Ly.gate)));

@@ -39,6 +39,20 @@ namespace {
 
 enum { EPI_STORE = 0, EPI_RESADD = 1, EPI_SILU = 2 };
 
+// Input modes: x as given (XDT); RMSNorm of an f32 residual; the merge of
+// split-sequence attention partials (x = attention output, f16-rounded).
+enum { XIN_X = 0, XIN_NORM = 1, XIN_MERGE = 2 };
+
+// Attention partials read by XIN_MERGE (written by the fused decode
+// attention): part_o [Hq][nchunks][D], part_ml [Hq][nchunks][2]; the live
+// chunk count is ceil(seq / chunk), seq = d_seq ? *d_seq : seq_len.
+constexpr int MERGE_MAX_CHUNKS = 16;
+struct MergeIn {
+    const float *part_o, *part_ml;
+    const uint32_t *d_seq;
+    uint32_t seq_len, nchunks, chunk, head_dim;
+};
+
 constexpr int MAX_SEG = 3;
 
 // One matrix (or row segment) and its output.
@@ -58,8 +72,9 @@ struct QmvArgs {
     // array makes the compiler copy the arguments to scratch memory.
     QmvMat m0, m1, m2;
     uint32_t nseg;
-    const void *x;         // input vector (XDT) or f32 residual (NORM)
-    const float *norm_w;   // f32 [K], NORM only
+    const void *x;         // input vector (XDT) or f32 residual (XIN_NORM)
+    const float *norm_w;   // f32 [K], XIN_NORM only
+    MergeIn mg;            // XIN_MERGE only
     uint32_t M, K, gs;
     uint32_t lpr_log2;     // lanes per row = 1 << lpr_log2
     uint32_t sdt;          // scale/bias dtype (NNZ_F16 / NNZ_BF16)
@@ -234,9 +249,11 @@ __device__ __forceinline__ void qmv_epilogue(const QmvArgs &a, void *out0, uint3
     }
 }
 
-template <int BITS, int XDT, int NMAT, bool NORM, int EPI, int ODT, bool FAITH, int NV, int R, bool LUT>
+template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH, int NV, int R, bool LUT>
 __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
     static_assert(!LUT || BITS == 1, "nibble tables are for 1-bit weights");
+    constexpr bool NORM = XIN == XIN_NORM;
+    constexpr bool MERGE = XIN == XIN_MERGE;
     constexpr int VEC = (BITS == 1) ? 1 : 4;  // u32 words per 32-column unit
     const int lane = threadIdx.x & 63;
     const int lpr_log2 = (int)a.lpr_log2;
@@ -312,6 +329,74 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                     if constexpr (FAITH) v[e] = bf16_trunc(v[e]);
                     xs[4 * i4 + e] = (f16_t)v[e];
                 }
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const uint32_t u = uvalid[j] ? (uint32_t)ll + (uint32_t)(LPR * j) : 0u;
+            const uint4 *p = (const uint4 *)(xs + u * 32);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint4 q = p[i];
+                const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    xr[j][8 * i + 2 * t] = (float)__builtin_bit_cast(f16_t, (uint16_t)(w4[t] & 0xFFFFu));
+                    xr[j][8 * i + 2 * t + 1] = (float)__builtin_bit_cast(f16_t, (uint16_t)(w4[t] >> 16));
+                }
+            }
+        }
+    } else if constexpr (MERGE) {
+        // The block merges the attention partials into x once (8 outputs
+        // per thread per 2048 columns), stages it f16 in LDS, and every wave
+        // reads its slice -- the merge that would otherwise be a launch of
+        // its own.  The first MERGE_MAX_CHUNKS chunks' partials are loaded
+        // in one round, independently of the live length.
+        __shared__ __align__(16) f16_t xs[2048 * NV];
+        const MergeIn &mg = a.mg;
+        const uint32_t D = mg.head_dim;
+#pragma unroll
+        for (int kk = 0; kk < NV; ++kk) {
+            const uint32_t e0 = (threadIdx.x + 256u * kk) * 8u;
+            const bool live = e0 < K;
+            const uint32_t ec = live ? e0 : 0u;
+            const size_t base = (size_t)(ec / D) * mg.nchunks;
+            const uint32_t d0 = ec % D;
+            float4 oa[MERGE_MAX_CHUNKS], ob[MERGE_MAX_CHUNKS];
+            float2 ml[MERGE_MAX_CHUNKS];
+#pragma unroll
+            for (int c = 0; c < MERGE_MAX_CHUNKS; ++c) {
+                if ((uint32_t)c < mg.nchunks) {   // launch bound: uniform
+                    const size_t cc = base + c;
+                    oa[c] = *(const float4 *)(mg.part_o + cc * D + d0);
+                    ob[c] = *(const float4 *)(mg.part_o + cc * D + d0 + 4);
+                    ml[c] = *(const float2 *)(mg.part_ml + cc * 2);
+                } else {
+                    oa[c] = ob[c] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    ml[c] = make_float2(-INFINITY, 0.f);
+                }
+            }
+            const uint32_t seq = mg.d_seq ? *mg.d_seq : mg.seq_len;
+            const uint32_t nch = min(mg.nchunks, ceil_div(seq, mg.chunk));
+            float M = -INFINITY;
+#pragma unroll
+            for (int c = 0; c < MERGE_MAX_CHUNKS; ++c) M = (uint32_t)c < nch ? fmaxf(M, ml[c].x) : M;
+            float num[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, den = 0.f;
+#pragma unroll
+            for (int c = 0; c < MERGE_MAX_CHUNKS; ++c) {
+                if ((uint32_t)c < nch) {
+                    const float wgt = expf(ml[c].x - M);
+                    den = fmaf(wgt, ml[c].y, den);
+                    num[0] = fmaf(wgt, oa[c].x, num[0]); num[1] = fmaf(wgt, oa[c].y, num[1]);
+                    num[2] = fmaf(wgt, oa[c].z, num[2]); num[3] = fmaf(wgt, oa[c].w, num[3]);
+                    num[4] = fmaf(wgt, ob[c].x, num[4]); num[5] = fmaf(wgt, ob[c].y, num[5]);
+                    num[6] = fmaf(wgt, ob[c].z, num[6]); num[7] = fmaf(wgt, ob[c].w, num[7]);
+                }
+            }
+            if (live) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) xs[e0 + e] = (f16_t)(num[e] / den);
             }
         }
         __syncthreads();
@@ -542,35 +627,35 @@ constexpr int LUT_MAX_NV = 3;
 // Weight words a lane holds for one row-step; the host keeps it <= 32.
 constexpr int step_words(int BITS, int NMAT, int NV, int R) { return NMAT * R * NV * (BITS == 1 ? 1 : 4); }
 
-template <int BITS, int XDT, int NMAT, bool NORM, int EPI, int ODT, bool FAITH, int NV, bool LUT>
+template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH, int NV, bool LUT>
 void launch_r(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks) {
     dim3 grid(blocks), block(256);
     if (R == 8) {
         // long matrices only (the 1-bit LM head): more rows in flight per wave
         if constexpr (LUT && step_words(BITS, NMAT, NV, 8) <= 32)
-            qmv_kernel<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, 8, LUT><<<grid, block, 0, ctx->stream>>>(a);
+            qmv_kernel<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, 8, LUT><<<grid, block, 0, ctx->stream>>>(a);
         else R = 4;
     }
     if (R == 4) {
         if constexpr (step_words(BITS, NMAT, NV, 4) <= 32)
-            qmv_kernel<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, 4, LUT><<<grid, block, 0, ctx->stream>>>(a);
+            qmv_kernel<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, 4, LUT><<<grid, block, 0, ctx->stream>>>(a);
         else R = 1;
     } else if (R == 2) {
         if constexpr (step_words(BITS, NMAT, NV, 2) <= 32)
-            qmv_kernel<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, 2, LUT><<<grid, block, 0, ctx->stream>>>(a);
+            qmv_kernel<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, 2, LUT><<<grid, block, 0, ctx->stream>>>(a);
         else R = 1;
     }
     if (R == 1)
-        qmv_kernel<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, 1, LUT><<<grid, block, 0, ctx->stream>>>(a);
+        qmv_kernel<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, 1, LUT><<<grid, block, 0, ctx->stream>>>(a);
 }
 
-template <int BITS, int XDT, int NMAT, bool NORM, int EPI, int ODT, bool FAITH, int NV>
+template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH, int NV>
 int launch_nv(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks, bool lut) {
     if constexpr (BITS == 1 && NV <= LUT_MAX_NV) {
-        if (lut) launch_r<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, true>(ctx, a, R, blocks);
-        else launch_r<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, false>(ctx, a, R, blocks);
+        if (lut) launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, true>(ctx, a, R, blocks);
+        else launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false>(ctx, a, R, blocks);
     } else {
-        launch_r<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, NV, false>(ctx, a, R, blocks);
+        launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false>(ctx, a, R, blocks);
     }
     NNZ_LAUNCHED(ctx);
     return NNZ_OK;
@@ -578,10 +663,12 @@ int launch_nv(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks, bool lut) 
 
 // `w[0..nw)` are either a pair sharing rows (NMAT == 2) or row segments of
 // one concatenated matrix (NMAT == 1, seg_rows[s] rows each).
-template <int BITS, int XDT, int NMAT, bool NORM, int EPI, int ODT, bool FAITH>
+template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH>
 int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg_rows, int nw,
                   const void *x, const float *norm_w, void *const *out, nnz_qmv_dims d,
-                  const char *name) {
+                  const char *name, const MergeIn *merge = nullptr) {
+    constexpr bool NORM = XIN == XIN_NORM;
+    constexpr bool MERGE = XIN == XIN_MERGE;
     NNZ_CHECK_CTX(ctx);
     int rc = check_dims(ctx, d, name);
     if (rc) return rc;
@@ -597,8 +684,16 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
         total += rows;
     }
     if (NMAT == 1) NNZ_REQUIRE(ctx, total == d.M, NNZ_EINVAL, "%s: segments do not add up to M", name);
-    NNZ_REQUIRE(ctx, x != nullptr, NNZ_EINVAL, "%s: null input", name);
-    NNZ_REQUIRE(ctx, ((uintptr_t)x & 15) == 0, NNZ_EINVAL, "%s: input must be 16-byte aligned", name);
+    if (MERGE) {
+        NNZ_REQUIRE(ctx, merge && merge->part_o && merge->part_ml, NNZ_EINVAL, "%s: null partials", name);
+        NNZ_REQUIRE(ctx, merge->nchunks >= 1 && merge->nchunks <= (uint32_t)MERGE_MAX_CHUNKS &&
+                             merge->chunk > 0 && merge->head_dim % 8 == 0 && d.K % merge->head_dim == 0 &&
+                             ((uintptr_t)merge->part_o & 15) == 0 && ((uintptr_t)merge->part_ml & 7) == 0,
+                    NNZ_EUNSUPPORTED, "%s: bad attention partials", name);
+    } else {
+        NNZ_REQUIRE(ctx, x != nullptr, NNZ_EINVAL, "%s: null input", name);
+        NNZ_REQUIRE(ctx, ((uintptr_t)x & 15) == 0, NNZ_EINVAL, "%s: input must be 16-byte aligned", name);
+    }
     if (NORM) {
         NNZ_REQUIRE(ctx, norm_w != nullptr, NNZ_EINVAL, "%s: null norm_scale", name);
         NNZ_REQUIRE(ctx, ((uintptr_t)norm_w & 15) == 0, NNZ_EINVAL,
@@ -641,6 +736,11 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
     // that over several row-steps per wave.
     const uint32_t max_blocks = NORM ? 1024u : 2048u;
     if (blocks > max_blocks) blocks = max_blocks;
+    if (MERGE) {
+        // every block re-reads all partials: fewer, fuller blocks
+        while (R < 4 && NMAT * 2 * R * (int)nv * vec <= 32 && ceil_div(d.M, 4u * R * rpw) > 128) R <<= 1;
+        blocks = ceil_div(d.M, 4u * R * rpw);
+    }
     if (lut && NMAT * ceil_div(d.M, blocks * 4u) < 4u) lut = false;
 
     QmvArgs a{};
@@ -659,6 +759,7 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
     }
     a.x = x;
     a.norm_w = norm_w;
+    if (MERGE) a.mg = *merge;
     a.M = d.M;
     a.K = d.K;
     a.gs = d.group_size;
@@ -666,21 +767,21 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
     a.sdt = w[0]->scale_dtype;
     a.eps = 1e-6f;
     switch (nv) {
-    case 1: return launch_nv<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, 1>(ctx, a, R, blocks, lut);
-    case 2: return launch_nv<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, 2>(ctx, a, R, blocks, lut);
-    case 3: return launch_nv<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, 3>(ctx, a, R, blocks, lut);
-    default: return launch_nv<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH, 4>(ctx, a, R, blocks, lut);
+    case 1: return launch_nv<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, 1>(ctx, a, R, blocks, lut);
+    case 2: return launch_nv<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, 2>(ctx, a, R, blocks, lut);
+    case 3: return launch_nv<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, 3>(ctx, a, R, blocks, lut);
+    default: return launch_nv<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, 4>(ctx, a, R, blocks, lut);
     }
 }
 
-template <int BITS, int XDT, int NMAT, bool NORM, int EPI, int ODT, bool FAITH>
+template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH>
 int launch_qmv(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, const void *x,
                const float *norm_w, void *out0, void *out1, nnz_qmv_dims d, const char *name) {
     const nnz_qweight *w[2] = {wa, wb};
     void *out[2] = {out0, out1};
     const uint32_t rows[1] = {d.M};
     if (NMAT == 2) NNZ_REQUIRE(ctx, wb != nullptr, NNZ_EINVAL, "%s: null second weight", name);
-    return launch_qmv_ex<BITS, XDT, NMAT, NORM, EPI, ODT, FAITH>(ctx, w, rows, NMAT, x, norm_w, out, d,
+    return launch_qmv_ex<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH>(ctx, w, rows, NMAT, x, norm_w, out, d,
                                                                   name);
 }
 
@@ -710,6 +811,21 @@ int nnz_qmv_norm_f32out_launch(nnz_ctx *ctx, const nnz_qweight *w, const float *
     return launch_qmv<1, NNZ_F32, 1, true, EPI_STORE, NNZ_F32, false>(ctx, w, nullptr, residual,
                                                                        norm_w, out, nullptr, d,
                                                                        "norm_lm_head");
+}
+
+// O-projection with residual += whose input is merged from split-sequence
+// attention partials inside the kernel (f16-rounded, as the separate merge
+// would store it).
+int nnz_qmv_merge_resadd_launch(nnz_ctx *ctx, const nnz_qweight *w, const float *part_o,
+                                const float *part_ml, const uint32_t *d_seq, uint32_t seq_len,
+                                uint32_t nchunks, uint32_t chunk, uint32_t head_dim,
+                                float *residual, nnz_qmv_dims d) {
+    MergeIn mg{part_o, part_ml, d_seq, seq_len, nchunks, chunk, head_dim};
+    const nnz_qweight *ws[1] = {w};
+    void *out[1] = {residual};
+    const uint32_t rows[1] = {d.M};
+    return launch_qmv_ex<1, NNZ_F16, 1, XIN_MERGE, EPI_RESADD, NNZ_F32, false>(
+        ctx, ws, rows, 1, nullptr, nullptr, out, d, "merge_o_resadd", &mg);
 }
 
 extern "C" {

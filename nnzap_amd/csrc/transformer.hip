@@ -484,6 +484,7 @@ struct FusedAttnArgs {
     const uint32_t *d_seq;          // device seq_len (= position + 1) or null
     const float *inv_freq;          // [D/2] RoPE frequencies, or null (computed here)
     uint32_t seq_len, max_ctx, nchunks;
+    int direct;                     // one chunk and no consumer merge: write out
     float eps, theta, scale;
 };
 
@@ -695,7 +696,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
         float s = 0.f;
 #pragma unroll
         for (int p = 0; p < PARTS; ++p) s += ored[p][g][d];
-        if (a.nchunks == 1) {
+        if (a.direct) {
             a.out[(size_t)(h * G + g) * D + d] = (f16_t)(s / lval[g]);
         } else {
             const size_t slot = (size_t)(h * G + g) * a.nchunks + c;
@@ -1013,7 +1014,7 @@ int nnz_attn_fused1_launch(nnz_ctx *ctx, const void *q, const void *kr, const vo
                            const float *qn, const float *kn, void *kc, void *vc, void *out,
                            float *part_o, float *part_ml, const uint32_t *d_seq, uint32_t max_seq,
                            uint32_t hq, uint32_t hkv, uint32_t head_dim, uint32_t max_ctx, float eps,
-                           float theta, const float *inv_freq) {
+                           float theta, const float *inv_freq, bool partials_only) {
     NNZ_REQUIRE(ctx, q && kr && vr && qn && kn && kc && vc && out && part_o && part_ml,
                 NNZ_EINVAL, "gqa_fused_1pass: null buffer");
     NNZ_REQUIRE(ctx, hkv > 0 && hq % hkv == 0 && max_seq > 0 && max_seq <= max_ctx, NNZ_EINVAL,
@@ -1039,6 +1040,7 @@ int nnz_attn_fused1_launch(nnz_ctx *ctx, const void *q, const void *kr, const vo
     a.seq_len = max_seq;
     a.max_ctx = max_ctx;
     a.nchunks = ceil_div(max_seq, (uint32_t)FCHUNK);
+    a.direct = a.nchunks == 1 && !partials_only;
     a.eps = eps;
     a.theta = theta;
     a.scale = 1.0f / sqrtf((float)head_dim);
@@ -1059,7 +1061,7 @@ int nnz_attn_fused1_launch(nnz_ctx *ctx, const void *q, const void *kr, const vo
     }
 #undef FUSED
     NNZ_LAUNCHED(ctx);
-    if (a.nchunks > 1) {
+    if (a.nchunks > 1 && !partials_only) {
         attn_merge_kernel<<<hq, 128, 0, ctx->stream>>>(part_o, part_ml, (f16_t *)out, d_seq, max_seq,
                                                        a.nchunks, head_dim);
         NNZ_LAUNCHED(ctx);

@@ -212,7 +212,44 @@ def _kernel_cases():
                           dtype=f32, device="cuda")
         us = time_launches(dev, lambda i: ops.dispatch_gqa_attention_fused_1pass(
             dev, qr, kc, vc, att, kr, vr, qn, qn, scr, fd), n)
-        return us, 2 * 8 * seq * 128 * 2 + 16 * 128 * 4 + 8 * 128 * 8, 28
+        return us, 2 * 8 * seq * 128 * 2 + 16 * 128 * 4 + 8 * 128 * 8, None
+
+    def dec_attention_partials(dev, n):
+        # the decoder's attention launch: q/k norm + RoPE (frequency table),
+        # KV append, split-sequence attention to per-chunk partials, at the
+        # mean context of the timed steps (640 tokens)
+        seq, max_ctx = 640, 1024
+        kc = torch.randn(8, max_ctx, 128, device="cuda").to(f16)
+        vc = torch.randn(8, 128, max_ctx, device="cuda").to(f16)
+        qr = torch.randn(16 * 128, device="cuda").to(f16)
+        kr = torch.randn(8 * 128, device="cuda").to(f16)
+        vr = torch.randn(8 * 128, device="cuda").to(f16)
+        qn = torch.ones(128, dtype=f32, device="cuda")
+        freqs = torch.from_numpy((1e6 ** (-np.arange(0, 128, 2) / 128.0)).astype(np.float32)).cuda()
+        nch = ops.gqa_partial_chunks(seq)
+        po = torch.empty(16 * nch * 128, dtype=f32, device="cuda")
+        pm = torch.empty(16 * nch * 2, dtype=f32, device="cuda")
+        fd = L.GQAFusedDims(16, 8, 128, seq, max_ctx, 2, seq - 1, 1e-6, 1e6)
+        us = time_launches(dev, lambda i: ops.dispatch_gqa_attention_partials(
+            dev, qr, kc, vc, kr, vr, qn, qn, po, pm, fd, rope_inv_freq=freqs), n)
+        # K and V of 640 tokens x 8 heads, q/k/v in, new K/V row out, partials out
+        nbytes = 2 * 8 * seq * 128 * 2 + (16 + 16) * 128 * 2 + 8 * 128 * 4 + 16 * nch * 130 * 4
+        return us, nbytes, 28
+
+    def dec_o_merge(dev, n):
+        # the decoder's O projection: merge of the attention partials in the
+        # prologue, residual +=
+        seq = 640
+        nch = ops.gqa_partial_chunks(seq)
+        wo = cf.q1_matrix(H, QD, 128, 506, 507)
+        r = Rot(dev, wo, ROTATE_BYTES)
+        po = torch.randn(16 * nch * 128, dtype=f32, device="cuda")
+        pm = torch.stack([torch.randn(16 * nch, device="cuda"),
+                          1 + torch.rand(16 * nch, device="cuda")], 1).reshape(-1).contiguous()
+        resid = torch.zeros(H, dtype=f32, device="cuda")
+        us = time_launches(dev, lambda i: ops.dispatch_qmv_merge_f16io_resadd(
+            dev, r[i], po, pm, seq, 128, resid), n)
+        return us, wo.nbytes + 16 * nch * 130 * 4 + H * 8, 28
 
     def dec_o(dev, n):
         wo = cf.q1_matrix(H, QD, 128, 506, 507)
@@ -220,7 +257,7 @@ def _kernel_cases():
         x16 = torch.randn(QD, dtype=f16, device="cuda") * 0.05
         resid = torch.zeros(H, dtype=f32, device="cuda")
         us = time_launches(dev, lambda i: ops.dispatch_qmv_f16io_resadd(dev, r[i], x16, resid), n)
-        return us, wo.nbytes + QD * 2 + H * 8, 28
+        return us, wo.nbytes + QD * 2 + H * 8, None
 
     def dec_gate_up(dev, n):
         res_d, nw = act()
@@ -295,8 +332,9 @@ def _kernel_cases():
 
     return {
         "config1_q4mv": config1, "config2_qmv": config2, "config3_gate_up_silu": config3,
-        "dec_qkv_norm": dec_qkv, "dec_attention_seq640": dec_attention,
-        "dec_o_resadd": dec_o, "dec_gate_up_norm_silu": dec_gate_up,
+        "dec_qkv_norm": dec_qkv, "dec_attention_partials": dec_attention_partials,
+        "dec_o_merge_resadd": dec_o_merge, "dec_gate_up_norm_silu": dec_gate_up,
+        "attention_fused_seq640": dec_attention, "o_resadd": dec_o,
         "dec_down_resadd": dec_down, "dec_lm_head_norm": dec_lm_head,
         "dec_lm_head_f16in": dec_lm_head_f16in, "floor_residual_add": floor_small,
         "config4_attention_L512": config4(512), "config4_attention_L4096": config4(4096),

@@ -344,6 +344,31 @@ int nnz_dispatch_gqa_attention_fused_1pass(nnz_ctx *ctx, const void *q, void *k_
                                            size_t scratch_bytes, const uint32_t *d_seq_len,
                                            nnz_gqa_fused_dims dims);
 
+/* The two halves the decode step uses instead of the call above (no
+ * reference counterpart; transformer.zig:3244-3370 encodeAttentionGather
+ * followed by :1686 dispatchQMVf16io_resadd on the attention output):
+ *   nnz_dispatch_gqa_attention_partials: the same norm/RoPE/append and
+ *     attention, leaving per-chunk partials instead of the output --
+ *     part_o f32 [Hq][nchunks][D] (unnormalised P.V), part_ml f32
+ *     [Hq][nchunks][2] (max score, exp-sum), nchunks =
+ *     nnz_gqa_partial_chunks(dims.seq_len) (64-token chunks);
+ *     rope_inv_freq: f32 [D/2] frequencies theta^(-2p/D) or NULL (computed
+ *     in the kernel);
+ *   nnz_dispatch_qmv_merge_f16io_resadd: residual += W . merge(partials),
+ *     the merge rounded to f16 as the attention output would be; W is the
+ *     1-bit O projection [M x Hq*D]; at most 16 chunks.
+ * d_seq_len as for nnz_dispatch_gqa_attention_fused_1pass. */
+uint32_t nnz_gqa_partial_chunks(uint32_t seq_len);
+int nnz_dispatch_gqa_attention_partials(nnz_ctx *ctx, const void *q, void *k_cache, void *v_cache,
+                                        const void *k_raw, const void *v_raw,
+                                        const float *q_norm_scale, const float *k_norm_scale,
+                                        const float *rope_inv_freq, float *part_o, float *part_ml,
+                                        const uint32_t *d_seq_len, nnz_gqa_fused_dims dims);
+int nnz_dispatch_qmv_merge_f16io_resadd(nnz_ctx *ctx, const nnz_qweight *w, const float *part_o,
+                                        const float *part_ml, const uint32_t *d_seq_len,
+                                        uint32_t seq_len, uint32_t head_dim, float *residual,
+                                        nnz_qmv_dims dims);
+
 /* transformer.zig:1072 dispatchEmbeddingLookup (Q1 table, f32 out). */
 int nnz_dispatch_embedding_lookup(nnz_ctx *ctx, const uint32_t *token_ids, const void *packed_bits,
                                   const void *scales, float *output, nnz_embed_dims dims);

@@ -150,6 +150,10 @@ PROTOS = {
                                                    GQAFusedDims]),
     "nnz_dispatch_gqa_attention_fused_1pass": (C.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
                                                          sz, vp, GQAFusedDims]),
+    "nnz_gqa_partial_chunks": (u32, [u32]),
+    "nnz_dispatch_gqa_attention_partials": (C.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,
+                                                      vp, GQAFusedDims]),
+    "nnz_dispatch_qmv_merge_f16io_resadd": (C.c_int, [vp, QW, vp, vp, vp, u32, u32, vp, QMVDims]),
     "nnz_dispatch_embedding_lookup": (C.c_int, [vp, vp, vp, vp, vp, EmbedDims]),
     "nnz_dispatch_embedding_lookup_q4": (C.c_int, [vp, vp, vp, vp, vp, vp, EmbedDims]),
     "nnz_dispatch_embedding_lookup_bf16": (C.c_int, [vp, vp, vp, vp, EmbedDims]),

@@ -830,6 +830,17 @@ int nnz_qmv_merge_resadd_launch(nnz_ctx *ctx, const nnz_qweight *w, const float 
 
 extern "C" {
 
+int nnz_dispatch_qmv_merge_f16io_resadd(nnz_ctx *ctx, const nnz_qweight *w, const float *part_o,
+                                        const float *part_ml, const uint32_t *d_seq_len,
+                                        uint32_t seq_len, uint32_t head_dim, float *residual,
+                                        nnz_qmv_dims dims) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, seq_len > 0 && head_dim > 0, NNZ_EINVAL, "merge_o_resadd: zero dims");
+    const uint32_t chunk = nnz_attn_fused_chunk(seq_len, 1);
+    return nnz_qmv_merge_resadd_launch(ctx, w, part_o, part_ml, d_seq_len, seq_len,
+                                       ceil_div(seq_len, chunk), chunk, head_dim, residual, dims);
+}
+
 // ---------------------------- Q1 ------------------------------------------
 int nnz_dispatch_qmv(nnz_ctx *ctx, const nnz_qweight *w, const float *input, float *output,
                      nnz_qmv_dims dims) {

@@ -1015,7 +1015,7 @@ int nnz_attn_fused1_launch(nnz_ctx *ctx, const void *q, const void *kr, const vo
                            float *part_o, float *part_ml, const uint32_t *d_seq, uint32_t max_seq,
                            uint32_t hq, uint32_t hkv, uint32_t head_dim, uint32_t max_ctx, float eps,
                            float theta, const float *inv_freq, bool partials_only) {
-    NNZ_REQUIRE(ctx, q && kr && vr && qn && kn && kc && vc && out && part_o && part_ml,
+    NNZ_REQUIRE(ctx, q && kr && vr && qn && kn && kc && vc && (out || partials_only) && part_o && part_ml,
                 NNZ_EINVAL, "gqa_fused_1pass: null buffer");
     NNZ_REQUIRE(ctx, hkv > 0 && hq % hkv == 0 && max_seq > 0 && max_seq <= max_ctx, NNZ_EINVAL,
                 "gqa_fused_1pass: bad dims");
@@ -1292,6 +1292,28 @@ int nnz_dispatch_gqa_attention_fused_1pass(nnz_ctx *ctx, const void *q, void *k_
                                   output, part_o, part_ml, d_seq_len, fd.seq_len,
                                   fd.num_query_heads, fd.num_kv_heads, fd.head_dim,
                                   fd.max_context_length, fd.eps, fd.rope_theta, nullptr);
+}
+
+uint32_t nnz_gqa_partial_chunks(uint32_t seq_len) { return ceil_div(seq_len, (uint32_t)FCHUNK); }
+
+int nnz_dispatch_gqa_attention_partials(nnz_ctx *ctx, const void *q, void *k_cache, void *v_cache,
+                                        const void *k_raw, const void *v_raw,
+                                        const float *q_norm_scale, const float *k_norm_scale,
+                                        const float *rope_inv_freq, float *part_o, float *part_ml,
+                                        const uint32_t *d_seq_len, nnz_gqa_fused_dims fd) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, fd.num_kv_heads > 0 && fd.seq_len > 0 && fd.seq_len <= fd.max_context_length,
+                NNZ_EINVAL, "gqa_partials: bad seq_len");
+    NNZ_REQUIRE(ctx, d_seq_len || fd.seq_len == fd.position + 1, NNZ_EINVAL,
+                "gqa_partials: seq_len must be position + 1");
+    NNZ_REQUIRE(ctx, fd.heads_per_kv_group * fd.num_kv_heads == fd.num_query_heads, NNZ_EINVAL,
+                "gqa_partials: heads_per_kv_group mismatch");
+    NNZ_REQUIRE(ctx, ((uintptr_t)part_o & 15) == 0 && ((uintptr_t)part_ml & 7) == 0, NNZ_EINVAL,
+                "gqa_partials: part_o must be 16-byte and part_ml 8-byte aligned");
+    return nnz_attn_fused1_launch(ctx, q, k_raw, v_raw, q_norm_scale, k_norm_scale, k_cache, v_cache,
+                                  nullptr, part_o, part_ml, d_seq_len, fd.seq_len, fd.num_query_heads,
+                                  fd.num_kv_heads, fd.head_dim, fd.max_context_length, fd.eps,
+                                  fd.rope_theta, rope_inv_freq, true);
 }
 
 int nnz_dispatch_embedding_lookup(nnz_ctx *ctx, const uint32_t *ids, const void *bits,

@@ -335,6 +335,29 @@ def dispatch_gqa_attention_fused_1pass(dev, q, k_cache, v_cache, out, k_raw, v_r
              scratch.numel() * scratch.element_size(), _v(d_seq_len), dims)
 
 
+def gqa_partial_chunks(seq_len: int) -> int:
+    return int(L.lib().nnz_gqa_partial_chunks(seq_len))
+
+
+def dispatch_gqa_attention_partials(dev, q, k_cache, v_cache, k_raw, v_raw, q_norm, k_norm,
+                                    part_o, part_ml, dims: L.GQAFusedDims, d_seq_len=None,
+                                    rope_inv_freq=None):
+    """The decode step's attention half: transformer.zig:3244-3370 up to the
+    per-chunk partials (part_o [Hq][n][D], part_ml [Hq][n][2], n =
+    gqa_partial_chunks(seq_len))."""
+    dev.call("nnz_dispatch_gqa_attention_partials", _v(q), _v(k_cache), _v(v_cache), _v(k_raw),
+             _v(v_raw), _v(q_norm), _v(k_norm), _v(rope_inv_freq), _v(part_o), _v(part_ml),
+             _v(d_seq_len), dims)
+
+
+def dispatch_qmv_merge_f16io_resadd(dev, w, part_o, part_ml, seq_len, head_dim, residual,
+                                    d_seq_len=None, dims=None):
+    """residual += W . merge(partials), the merge rounded to f16 (the O
+    projection of transformer.zig:1686 on the attention output)."""
+    dev.call("nnz_dispatch_qmv_merge_f16io_resadd", w.ref, _v(part_o), _v(part_ml), _v(d_seq_len),
+             seq_len, head_dim, _v(residual), dims or w.dims())
+
+
 def dispatch_embedding_lookup(dev, ids, bits, scales, out, dims: L.EmbedDims):
     """transformer.zig:1072 dispatchEmbeddingLookup."""
     dev.call("nnz_dispatch_embedding_lookup", _v(ids), _v(bits), _v(scales), _v(out), dims)

@@ -10,7 +10,7 @@ from nnzap_amd import ops
 from nnzap_amd import synth as S
 from oracle import oracle as O
 
-from gpu_util import assert_close, from_bits16, host, tdev
+from gpu_util import assert_close, assert_close_normwise, from_bits16, host, tdev
 
 pytestmark = pytest.mark.gpu
 
@@ -90,9 +90,9 @@ def test_gqa_fused_norm_rope_kv(dev, pos):
 
 @pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (4, 2, 64), (8, 8, 128)])
 def test_gqa_fused_1pass_successive_positions(dev, hq, hkv, d):
-    """Single-launch fused attention at consecutive positions sharing one
-    scratch (exercises the merge counters being left at zero), with the
-    sequence length read from device memory as in graph replay."""
+    """Fused attention (one kernel, plus a merge kernel past one chunk) at
+    consecutive positions sharing one scratch, with the sequence length read
+    from device memory as in graph replay."""
     max_ctx, theta = 2048, 1e6
     qn = (1 + 0.1 * S.normal(417, d)).astype(np.float32)
     kn = (1 + 0.1 * S.normal(418, d)).astype(np.float32)
@@ -122,6 +122,60 @@ def test_gqa_fused_1pass_successive_positions(dev, hq, hkv, d):
         assert_close(host(out), O.f16(ref), what=f"1pass pos={pos}")
     assert_close(host(kcd)[:, start:start + 8], kc_ref[:, start:start + 8], what="k rows")
     assert np.array_equal(host(vcd)[:, :, start:start + 8], vc_ref[:, :, start:start + 8])
+
+
+@pytest.mark.parametrize("pos", [30, 700, 1023])
+@pytest.mark.parametrize("freq_table", [False, True])
+def test_attention_partials_merged_o_projection(dev, pos, freq_table):
+    """The decode step's two halves: attention to per-chunk partials, then the
+    1-bit O projection (residual +=) merging them in its prologue.  Checked
+    against the one-call fused attention + plain O projection on the GPU
+    (same f16 attention output, different QMV order: 1e-4), and against the
+    oracle (normwise, after the f16 rounding of the attention output)."""
+    hq, hkv, d, max_ctx, theta = 16, 8, 128, 1024, 1e6
+    H = 2048
+    qn = (1 + 0.1 * S.normal(461, d)).astype(np.float32)
+    kn = (1 + 0.1 * S.normal(462, d)).astype(np.float32)
+    kc = np.zeros((hkv, max_ctx, d), np.float16)
+    vc = np.zeros((hkv, d, max_ctx), np.float16)
+    kc[:, :pos] = (0.5 * S.normal(463, hkv * pos * d)).astype(np.float16).reshape(hkv, pos, d)
+    vc[:, :, :pos] = S.normal(464, hkv * pos * d).astype(np.float16).reshape(hkv, d, pos)
+    q = S.normal(465, hq * d).astype(np.float16).reshape(hq, d)
+    kr = S.normal(466, hkv * d).astype(np.float16).reshape(hkv, d)
+    vr = S.normal(467, hkv * d).astype(np.float16).reshape(hkv, d)
+    wo = cf.q1_matrix(H, hq * d, 128, 468, 469)
+    res0 = S.normal(470, H).astype(np.float32)
+    dwo = ops.DeviceQWeight(dev, wo)
+    seq = pos + 1
+    dims = L.GQAFusedDims(hq, hkv, d, seq, max_ctx, hq // hkv, pos, 1e-6, theta)
+    dseq = torch.full((1,), seq, dtype=torch.int32, device="cuda")
+    n = ops.gqa_partial_chunks(seq)
+    assert n == (seq + 63) // 64
+    part_o = torch.empty(hq * n * d, dtype=torch.float32, device="cuda")
+    part_ml = torch.empty(hq * n * 2, dtype=torch.float32, device="cuda")
+    freqs = tdev(O.rope_inv_freq(d, theta)) if freq_table else None
+    # path 1: partials + merged O projection
+    kc1, vc1, res1 = tdev(kc), tdev(vc), tdev(res0)
+    ops.dispatch_gqa_attention_partials(dev, tdev(q), kc1, vc1, tdev(kr), tdev(vr), tdev(qn),
+                                        tdev(kn), part_o, part_ml, dims, d_seq_len=dseq,
+                                        rope_inv_freq=freqs)
+    ops.dispatch_qmv_merge_f16io_resadd(dev, dwo, part_o, part_ml, seq, d, res1, d_seq_len=dseq)
+    # path 2: fused attention output + plain O projection
+    kc2, vc2, res2 = tdev(kc), tdev(vc), tdev(res0)
+    gd = L.GQADims(hq, hkv, d, seq, max_ctx, hq // hkv)
+    scr = torch.zeros(ops.gqa_scratch_bytes(gd) // 4 + 64, dtype=torch.float32, device="cuda")
+    att = torch.empty(hq * d, dtype=torch.float16, device="cuda")
+    ops.dispatch_gqa_attention_fused_1pass(dev, tdev(q), kc2, vc2, att, tdev(kr), tdev(vr),
+                                           tdev(qn), tdev(kn), scr, dims, d_seq_len=dseq)
+    ops.dispatch_qmv_f16io_resadd(dev, dwo, att, res2)
+    dev.sync()
+    assert np.array_equal(host(kc1), host(kc2)) and np.array_equal(host(vc1), host(vc2))
+    assert_close(host(res1), host(res2), rtol=1e-4, what=f"merged vs unmerged pos={pos}")
+    ref_att = O.f16(O.gqa_fused_step(q.astype(np.float64), kr.astype(np.float64),
+                                     vr.astype(np.float64), kc.astype(np.float64),
+                                     vc.astype(np.float64), qn, kn, pos, theta, v_transposed=True))
+    ref = res0.astype(np.float64) + O.qmv(wo, ref_att.reshape(-1))
+    assert_close_normwise(host(res1), ref, rtol=1e-3, what=f"oracle pos={pos}")
 
 
 # ------------------------------------------------------------------ norms ---

@@ -361,6 +361,22 @@ def bench_kernels(dev, quick=False, only=None):
     return res
 
 
+def load_traffic():
+    """HBM bytes per launch of the decode kernel cases, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/pmc_traffic.md):
+    fetch_KiB * fetch_scale + write_KiB * write_scale, the scales calibrated
+    on a copy of known size."""
+    path = os.path.join(ROOT, "profiles", "pmc_traffic.md")
+    out = {}
+    if not os.path.exists(path):
+        return out
+    for line in open(path):
+        f = line.split()
+        if len(f) == 6 and f[0] == "TRAFFIC":
+            out[f[1]] = int(round((float(f[2]) * float(f[4]) + float(f[3]) * float(f[5])) * 1024))
+    return out
+
+
 # ------------------------------------------------------------ CPU baseline --
 def cpu_baseline(sample_layers=2, tokens=3):
     """The numpy oracle's decode step on this host: `sample_layers` of the 28
@@ -433,9 +449,11 @@ def main():
     if dec_k:
         dom = max(dec_k, key=lambda k: dec_k[k]["us"] * dec_k[k]["per_token"])
         d = dec_k[dom]
+        traffic = load_traffic().get(dom)
         roofline = {"kernel": dom, "bound": "hbm", "achieved": d["GBs"], "peak": PEAK_HBM_GBS,
-                    "unit": "GB/s", "frac": round(d["GBs"] / PEAK_HBM_GBS, 4), "traffic": None,
-                    "avg_launch_us": d["us"], "algorithmic_bytes": d["bytes"]}
+                    "unit": "GB/s", "frac": round(d["GBs"] / PEAK_HBM_GBS, 4), "traffic": traffic,
+                    "avg_launch_us": d["us"], "algorithmic_bytes": d["bytes"],
+                    "traffic_source": "profiles/pmc_traffic.md" if traffic else None}
     cpu = None if args.skip_cpu else cpu_baseline()
 
     line = {

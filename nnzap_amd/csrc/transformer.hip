@@ -643,19 +643,31 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
     }
     __syncthreads();
 
-    // ---- softmax over the chunk, all G heads at once.  FCHUNK <= 64, so
-    // every wave sees the whole chunk and computes the same max and sum.
-    static_assert(FCHUNK <= 64, "softmax assumes one wave covers the chunk");
+    // ---- softmax over the chunk, all G heads at once: lane l holds tokens
+    // l, l + 64, ... so every wave sees the whole chunk and computes the
+    // same max and sum (no cross-wave step).
+    constexpr int TPL = (FCHUNK + 63) / 64;   // tokens per lane
     float mval[G], lval[G];
     {
         const int lane = tid & 63;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            const float sc = lane < FCHUNK ? ps[g][lane] : -INFINITY;
-            mval[g] = wave_max(sc);
-            const float e = lane < FCHUNK ? expf(sc - mval[g]) : 0.f;
-            lval[g] = wave_sum(e);
-            if (tid < FCHUNK) pe[g][lane] = e;
+            float sc[TPL];
+            float m = -INFINITY;
+#pragma unroll
+            for (int k = 0; k < TPL; ++k) {
+                sc[k] = lane + 64 * k < FCHUNK ? ps[g][lane + 64 * k] : -INFINITY;
+                m = fmaxf(m, sc[k]);
+            }
+            mval[g] = wave_max(m);
+            float l = 0.f;
+#pragma unroll
+            for (int k = 0; k < TPL; ++k) {
+                const float e = lane + 64 * k < FCHUNK ? expf(sc[k] - mval[g]) : 0.f;
+                l += e;
+                if (tid < 64 && lane + 64 * k < FCHUNK) pe[g][lane + 64 * k] = e;
+            }
+            lval[g] = wave_sum(l);
         }
     }
     __syncthreads();

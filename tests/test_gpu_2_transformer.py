@@ -150,7 +150,7 @@ def test_attention_partials_merged_o_projection(dev, pos, freq_table):
     dims = L.GQAFusedDims(hq, hkv, d, seq, max_ctx, hq // hkv, pos, 1e-6, theta)
     dseq = torch.full((1,), seq, dtype=torch.int32, device="cuda")
     n = ops.gqa_partial_chunks(seq)
-    assert n == (seq + 63) // 64
+    assert 1 <= n <= 16
     part_o = torch.empty(hq * n * d, dtype=torch.float32, device="cuda")
     part_ml = torch.empty(hq * n * 2, dtype=torch.float32, device="cuda")
     freqs = tdev(O.rope_inv_freq(d, theta)) if freq_table else None

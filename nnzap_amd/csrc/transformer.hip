@@ -484,6 +484,7 @@ struct FusedAttnArgs {
     const uint32_t *d_seq;          // device seq_len (= position + 1) or null
     const float *inv_freq;          // [D/2] RoPE frequencies, or null (computed here)
     uint32_t seq_len, max_ctx, nchunks;
+    uint32_t gfull;                 // query heads per KV head
     int direct;                     // one chunk and no consumer merge: write out
     float eps, theta, scale;
 };
@@ -507,7 +508,10 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
     __shared__ float hsum[G][4];
 
     const int tid = threadIdx.x;
-    const uint32_t c = blockIdx.x, h = blockIdx.y;
+    // block (c, y) serves query heads [qb, qb + G) of KV head h; when a KV
+    // group is split over several blocks, the first one appends to the cache
+    const uint32_t c = blockIdx.x, qb = blockIdx.y * G, h = qb / a.gfull;
+    const bool writer = qb % a.gfull == 0;
     const uint32_t seq = a.d_seq ? *a.d_seq : a.seq_len;
     const uint32_t pos = seq - 1;
     const uint32_t t0 = c * FCHUNK;
@@ -523,7 +527,7 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
     for (int k = 0; k < NQ; ++k) {
         const int i = tid + 256 * k;
         const int ic = i < G * D ? i : 0;
-        qv[k] = (float)a.q[(size_t)h * G * D + ic];
+        qv[k] = (float)a.q[(size_t)qb * D + ic];
         qnv[k] = a.qn[ic % D];
     }
     const int kd = tid < D ? tid : 0;
@@ -593,8 +597,10 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
         if (tid < D) {
             knew[tid] = kr;
             vnew[tid] = (float)vraw;
-            a.kc[(size_t)h * kv_stride + (size_t)pos * D + tid] = (f16_t)kr;
-            a.vc[(size_t)h * kv_stride + (size_t)tid * a.max_ctx + pos] = vraw;
+            if (writer) {
+                a.kc[(size_t)h * kv_stride + (size_t)pos * D + tid] = (f16_t)kr;
+                a.vc[(size_t)h * kv_stride + (size_t)tid * a.max_ctx + pos] = vraw;
+            }
         }
     }
     __syncthreads();
@@ -709,9 +715,9 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
 #pragma unroll
         for (int p = 0; p < PARTS; ++p) s += ored[p][g][d];
         if (a.direct) {
-            a.out[(size_t)(h * G + g) * D + d] = (f16_t)(s / lval[g]);
+            a.out[(size_t)(qb + g) * D + d] = (f16_t)(s / lval[g]);
         } else {
-            const size_t slot = (size_t)(h * G + g) * a.nchunks + c;
+            const size_t slot = (size_t)(qb + g) * a.nchunks + c;
             a.part_o[slot * D + d] = s;
             if (d == 0) {
                 a.part_ml[slot * 2] = mval[g];
@@ -1056,17 +1062,23 @@ int nnz_attn_fused1_launch(nnz_ctx *ctx, const void *q, const void *kr, const vo
     a.eps = eps;
     a.theta = theta;
     a.scale = 1.0f / sqrtf((float)head_dim);
-    dim3 grid(a.nchunks, hkv);
+    // Few chunks x KV heads leave CUs idle: split each KV group over blocks
+    // of one query head (K/V then read once per query head, the repeats
+    // from L2).
+    a.gfull = G;
+    const uint32_t gb = (a.nchunks * hkv < 128) ? 1u : G;
+    dim3 grid(a.nchunks, hq / gb);
 #define FUSED(DD, GG) attn_fused_kernel<DD, GG><<<grid, 256, 0, ctx->stream>>>(a)
-    if (head_dim == 128) {
-        if (G == 1) FUSED(128, 1);
-        else if (G == 2) FUSED(128, 2);
+    if (gb == 1) {
+        if (head_dim == 128) FUSED(128, 1);
+        else FUSED(64, 1);
+    } else if (head_dim == 128) {
+        if (G == 2) FUSED(128, 2);
         else if (G == 4) FUSED(128, 4);
         else if (G == 8) FUSED(128, 8);
         else return nnz_fail(ctx, NNZ_EUNSUPPORTED, "gqa_fused_1pass: group %u", G);
     } else {
-        if (G == 1) FUSED(64, 1);
-        else if (G == 2) FUSED(64, 2);
+        if (G == 2) FUSED(64, 2);
         else if (G == 4) FUSED(64, 4);
         else if (G == 8) FUSED(64, 8);
         else return nnz_fail(ctx, NNZ_EUNSUPPORTED, "gqa_fused_1pass: group %u", G);

@@ -738,7 +738,7 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
     if (blocks > max_blocks) blocks = max_blocks;
     if (MERGE) {
         // every block re-reads all partials: fewer, fuller blocks
-        while (R < 4 && NMAT * 2 * R * (int)nv * vec <= 32 && ceil_div(d.M, 4u * R * rpw) > 128) R <<= 1;
+        while (R < 4 && NMAT * 2 * R * (int)nv * vec <= 32 && ceil_div(d.M, 4u * R * rpw) > 256) R <<= 1;
         blocks = ceil_div(d.M, 4u * R * rpw);
     }
     if (lut && NMAT * ceil_div(d.M, blocks * 4u) < 4u) lut = false;

@@ -710,9 +710,11 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
     const uint32_t rpw = 64 / lpr;
     const int vec = BITS == 1 ? 1 : 4;
     int R = 4;
-    // Keep >= 2 waves of work per CU where the matrix allows, and bound the
-    // number of weight words a lane holds in flight (two steps are live).
-    while (R > 1 && (ceil_div(d.M, 4u * R * rpw) < 512 || NMAT * R * (int)nv * vec > 32)) R >>= 1;
+    // Rows per wave-step: as many as keep about one block per CU (pairs:
+    // two) -- measured best for the decode shapes -- bounded by the weight
+    // words a lane holds in flight (two steps are live).
+    const uint32_t min_blocks = NMAT == 2 ? 512u : 256u;
+    while (R > 1 && (ceil_div(d.M, 4u * R * rpw) < min_blocks || NMAT * R * (int)nv * vec > 32)) R >>= 1;
     // 1-bit full-wave rows may use the nibble tables.  Building them is a
     // fixed cost per block that pays off from about four matrix rows per
     // wave: pairs take two rows per wave; single matrices only when the

@@ -348,53 +348,79 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
             }
         }
     } else if constexpr (MERGE) {
-        // The block merges the attention partials into x once (8 outputs
-        // per thread per 2048 columns), stages it f16 in LDS, and every wave
-        // reads its slice -- the merge that would otherwise be a launch of
-        // its own.  The first MERGE_MAX_CHUNKS chunks' partials are loaded
-        // in one round, independently of the live length.
+        // The block merges the attention partials into x once and stages it
+        // f16 in LDS for every wave -- the merge that would otherwise be a
+        // launch of its own.  Phase 1: per (head, chunk) the weight
+        // exp(m_c - M) and per head the denominator, one thread per pair
+        // (a head's 16 chunk slots are one DPP row).  Phase 2: 8 outputs per
+        // thread per 2048 columns.  All partials of the first
+        // MERGE_MAX_CHUNKS chunks are loaded up front, independently of the
+        // live length.
+        static_assert(MERGE_MAX_CHUNKS == 16, "one DPP row per head");
         __shared__ __align__(16) f16_t xs[2048 * NV];
+        __shared__ float mw[(2048 * NV / 64) * MERGE_MAX_CHUNKS];   // >= heads x 16 (D >= 64)
+        __shared__ float mden[2048 * NV / 64];
         const MergeIn &mg = a.mg;
         const uint32_t D = mg.head_dim;
+        const uint32_t heads = K / D;
+        float4 oa[NV][MERGE_MAX_CHUNKS], ob[NV][MERGE_MAX_CHUNKS];
 #pragma unroll
         for (int kk = 0; kk < NV; ++kk) {
             const uint32_t e0 = (threadIdx.x + 256u * kk) * 8u;
-            const bool live = e0 < K;
-            const uint32_t ec = live ? e0 : 0u;
+            const uint32_t ec = e0 < K ? e0 : 0u;
             const size_t base = (size_t)(ec / D) * mg.nchunks;
             const uint32_t d0 = ec % D;
-            float4 oa[MERGE_MAX_CHUNKS], ob[MERGE_MAX_CHUNKS];
-            float2 ml[MERGE_MAX_CHUNKS];
 #pragma unroll
             for (int c = 0; c < MERGE_MAX_CHUNKS; ++c) {
                 if ((uint32_t)c < mg.nchunks) {   // launch bound: uniform
-                    const size_t cc = base + c;
-                    oa[c] = *(const float4 *)(mg.part_o + cc * D + d0);
-                    ob[c] = *(const float4 *)(mg.part_o + cc * D + d0 + 4);
-                    ml[c] = *(const float2 *)(mg.part_ml + cc * 2);
+                    oa[kk][c] = *(const float4 *)(mg.part_o + (base + c) * D + d0);
+                    ob[kk][c] = *(const float4 *)(mg.part_o + (base + c) * D + d0 + 4);
                 } else {
-                    oa[c] = ob[c] = make_float4(0.f, 0.f, 0.f, 0.f);
-                    ml[c] = make_float2(-INFINITY, 0.f);
+                    oa[kk][c] = ob[kk][c] = make_float4(0.f, 0.f, 0.f, 0.f);
                 }
             }
-            const uint32_t seq = mg.d_seq ? *mg.d_seq : mg.seq_len;
-            const uint32_t nch = min(mg.nchunks, ceil_div(seq, mg.chunk));
-            float M = -INFINITY;
-#pragma unroll
-            for (int c = 0; c < MERGE_MAX_CHUNKS; ++c) M = (uint32_t)c < nch ? fmaxf(M, ml[c].x) : M;
-            float num[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, den = 0.f;
-#pragma unroll
-            for (int c = 0; c < MERGE_MAX_CHUNKS; ++c) {
-                if ((uint32_t)c < nch) {
-                    const float wgt = expf(ml[c].x - M);
-                    den = fmaf(wgt, ml[c].y, den);
-                    num[0] = fmaf(wgt, oa[c].x, num[0]); num[1] = fmaf(wgt, oa[c].y, num[1]);
-                    num[2] = fmaf(wgt, oa[c].z, num[2]); num[3] = fmaf(wgt, oa[c].w, num[3]);
-                    num[4] = fmaf(wgt, ob[c].x, num[4]); num[5] = fmaf(wgt, ob[c].y, num[5]);
-                    num[6] = fmaf(wgt, ob[c].z, num[6]); num[7] = fmaf(wgt, ob[c].w, num[7]);
-                }
+        }
+        const uint32_t seq = mg.d_seq ? *mg.d_seq : mg.seq_len;
+        const uint32_t nch = min(mg.nchunks, ceil_div(seq, mg.chunk));
+        for (uint32_t p = threadIdx.x; p < ((heads * MERGE_MAX_CHUNKS + 255) / 256) * 256; p += 256) {
+            const uint32_t hd = p / MERGE_MAX_CHUNKS, c = p % MERGE_MAX_CHUNKS;
+            const bool on = hd < heads && c < nch;
+            const float2 ml = on ? *(const float2 *)(mg.part_ml + ((size_t)hd * mg.nchunks + c) * 2)
+                                 : make_float2(-INFINITY, 0.f);
+            float M = ml.x;   // max over the head's 16 lanes
+            M = fmaxf(M, dpp_move<DPP_XOR1>(M, -INFINITY));
+            M = fmaxf(M, dpp_move<DPP_XOR2>(M, -INFINITY));
+            M = fmaxf(M, dpp_move<DPP_ROW_HALF_MIRROR>(M, -INFINITY));
+            M = fmaxf(M, dpp_move<DPP_ROW_MIRROR>(M, -INFINITY));
+            const float wgt = on ? expf(ml.x - M) : 0.f;
+            float den = wgt * ml.y;
+            den += dpp_move<DPP_XOR1>(den, 0.f);
+            den += dpp_move<DPP_XOR2>(den, 0.f);
+            den += dpp_move<DPP_ROW_HALF_MIRROR>(den, 0.f);
+            den += dpp_move<DPP_ROW_MIRROR>(den, 0.f);
+            if (hd < heads) {
+                mw[p] = wgt;
+                if (c == 0) mden[hd] = den;
             }
-            if (live) {
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < NV; ++kk) {
+            const uint32_t e0 = (threadIdx.x + 256u * kk) * 8u;
+            if (e0 < K) {
+                const uint32_t hd = e0 / D;
+                float num[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int c = 0; c < MERGE_MAX_CHUNKS; ++c) {
+                    if ((uint32_t)c < mg.nchunks) {
+                        const float wgt = mw[hd * MERGE_MAX_CHUNKS + c];
+                        num[0] = fmaf(wgt, oa[kk][c].x, num[0]); num[1] = fmaf(wgt, oa[kk][c].y, num[1]);
+                        num[2] = fmaf(wgt, oa[kk][c].z, num[2]); num[3] = fmaf(wgt, oa[kk][c].w, num[3]);
+                        num[4] = fmaf(wgt, ob[kk][c].x, num[4]); num[5] = fmaf(wgt, ob[kk][c].y, num[5]);
+                        num[6] = fmaf(wgt, ob[kk][c].z, num[6]); num[7] = fmaf(wgt, ob[kk][c].w, num[7]);
+                    }
+                }
+                const float den = mden[hd];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) xs[e0 + e] = (f16_t)(num[e] / den);
             }
@@ -651,14 +677,19 @@ void launch_r(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks) {
 
 template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH, int NV>
 int launch_nv(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks, bool lut) {
-    if constexpr (BITS == 1 && NV <= LUT_MAX_NV) {
-        if (lut) launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, true>(ctx, a, R, blocks);
-        else launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false>(ctx, a, R, blocks);
+    if constexpr (XIN == XIN_MERGE && NV > 2) {
+        // the merge prologue keeps every chunk's partials in registers
+        return nnz_fail(ctx, NNZ_EUNSUPPORTED, "merge_o_resadd: K > 4096");
     } else {
-        launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false>(ctx, a, R, blocks);
+        if constexpr (BITS == 1 && NV <= LUT_MAX_NV) {
+            if (lut) launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, true>(ctx, a, R, blocks);
+            else launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false>(ctx, a, R, blocks);
+        } else {
+            launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false>(ctx, a, R, blocks);
+        }
+        NNZ_LAUNCHED(ctx);
+        return NNZ_OK;
     }
-    NNZ_LAUNCHED(ctx);
-    return NNZ_OK;
 }
 
 // `w[0..nw)` are either a pair sharing rows (NMAT == 2) or row segments of
@@ -743,7 +774,9 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
         while (R < 4 && NMAT * 2 * R * (int)nv * vec <= 32 && ceil_div(d.M, 4u * R * rpw) > 256) R <<= 1;
         blocks = ceil_div(d.M, 4u * R * rpw);
     }
-    if (lut && NMAT * ceil_div(d.M, blocks * 4u) < 4u) lut = false;
+    // measured: tables pay off from 4 row-units per wave for pairs, from 8
+    // rows per wave for single matrices
+    if (lut && ceil_div(d.M, blocks * 4u) * NMAT < (NMAT == 2 ? 4u : 8u)) lut = false;
 
     QmvArgs a{};
     for (int i = 0; i < nw; ++i) {

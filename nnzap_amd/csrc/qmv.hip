@@ -611,6 +611,110 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Split-K QMV for long 1-bit rows (K = 64*32*KS, KS = 2..4): the KS waves of
+// a block share R rows and wave k takes units [64k, 64k + 64), one per
+// lane, so each wave's x slice, bit loop and row reduction are a KS-th of
+// the full-row kernel's and a SIMD interleaves several short waves instead
+// of running one long one.  The KS row partials meet in LDS (double
+// buffered: one barrier per step).
+template <int XDT, int EPI, int ODT, int KS, int R>
+__global__ __launch_bounds__(64 * KS) void qmv1_splitk_kernel(QmvArgs a) {
+    static_assert(EPI == EPI_STORE || EPI == EPI_RESADD, "store or residual add");
+    const int lane = threadIdx.x & 63, kp = threadIdx.x >> 6;
+    const uint32_t K = a.K, units = K >> 5, G = K / a.gs, M = a.M;
+    const uint32_t u = (uint32_t)(kp * 64 + lane);
+    const bool uv = u < units;
+    const uint32_t uc = uv ? u : 0u;
+    const gptr<const uint32_t> codes = uniform_ptr(a.m0.codes);
+    const gptr<const uint16_t> scales = uniform_ptr(a.m0.scales);
+    float *const out = (float *)a.m0.out;
+    __shared__ float part[2][KS][R];
+
+    struct Step { uint32_t cw[R]; uint16_t sc[R]; float prev; };
+    auto load = [&](uint32_t base, Step &st) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t row = base + r;
+            const uint32_t lr = row < M ? row : 0u;
+            st.cw[r] = codes[(size_t)lr * units + uc];
+            st.sc[r] = scales[(size_t)lr * G + (uc * 32u) / a.gs];
+        }
+        if constexpr (EPI == EPI_RESADD) {   // residual row of lane r (wave 0)
+            const uint32_t row = base + (uint32_t)lane;
+            st.prev = (kp == 0 && lane < R && row < M) ? out[row] : 0.f;
+        }
+    };
+
+    uint32_t base = blockIdx.x * R;
+    const uint32_t stride = gridDim.x * R;
+    Step cur;
+    if (base < M) load(base, cur);
+
+    // this lane's 32 x values (unit 0 stands in past the row end; its scale
+    // is zeroed below)
+    float xr[32], xsum = 0.f;
+    if constexpr (XDT == NNZ_F32) {
+        const float4 *p = (const float4 *)((const float *)a.x + (size_t)uc * 32);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float4 v = p[i];
+            xr[4 * i] = v.x; xr[4 * i + 1] = v.y; xr[4 * i + 2] = v.z; xr[4 * i + 3] = v.w;
+        }
+    } else {
+        const uint4 *p = (const uint4 *)((const uint16_t *)a.x + (size_t)uc * 32);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint4 v = p[i];
+            const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint16_t lo = (uint16_t)(wv[t] & 0xFFFFu), hi = (uint16_t)(wv[t] >> 16);
+                if constexpr (XDT == NNZ_F16) {
+                    xr[8 * i + 2 * t] = (float)__builtin_bit_cast(f16_t, lo);
+                    xr[8 * i + 2 * t + 1] = (float)__builtin_bit_cast(f16_t, hi);
+                } else {
+                    xr[8 * i + 2 * t] = bf16_to_f32(lo);
+                    xr[8 * i + 2 * t + 1] = bf16_to_f32(hi);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 32; ++i) xsum += xr[i];
+
+    for (int it = 0; base < M; base += stride, ++it) {
+        Step nxt;
+        if (base + stride < M) load(base + stride, nxt);
+        const int buf = it & 1;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t w = cur.cw[r];
+            float sb = 0.f;
+#pragma unroll
+            for (int i = 0; i < 32; ++i) {
+                const int mask = ((int)(w << (31 - i))) >> 31;  // 0 or -1
+                sb += __int_as_float(mask & __float_as_int(xr[i]));
+            }
+            const float sc = uv ? (float)__builtin_bit_cast(f16_t, cur.sc[r]) : 0.f;
+            const float p = lane63(wave_sum_to_last(sc * (2.f * sb - xsum)));
+            if (lane == 0) part[buf][kp][r] = p;
+        }
+        __syncthreads();
+        if (kp == 0 && lane < R) {
+            float t = 0.f;
+#pragma unroll
+            for (int k = 0; k < KS; ++k) t += part[buf][k][lane];
+            const uint32_t row = base + (uint32_t)lane;
+            if (row < M) {
+                if constexpr (EPI == EPI_RESADD) out[row] = cur.prev + t;
+                else store_from_f32<ODT>(a.m0.out, row, t);
+            }
+        }
+        cur = nxt;
+    }
+}
+
 int check_weight(nnz_ctx *ctx, const nnz_qweight *w, int bits, uint32_t M, const nnz_qmv_dims &d,
                  const char *name) {
     NNZ_REQUIRE(ctx, w != nullptr, NNZ_EINVAL, "%s: null weight descriptor", name);
@@ -740,6 +844,33 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
     NNZ_REQUIRE(ctx, nv >= 1 && nv <= 4, NNZ_EUNSUPPORTED, "%s: K=%u needs %u units/lane", name, d.K, nv);
     const uint32_t rpw = 64 / lpr;
     const int vec = BITS == 1 ? 1 : 4;
+    if constexpr (BITS == 1 && XIN == XIN_X && NMAT == 1 && !FAITH &&
+                  (EPI == EPI_STORE || EPI == EPI_RESADD)) {
+        // long single-segment rows: split K over the waves of a block
+        if (nw == 1 && lpr == 64 && nv >= 2 && nv <= 4 && d.K % 2048 == 0) {
+            constexpr int SR = 2;
+            QmvArgs a{};
+            a.m0.codes = (const uint32_t *)w[0]->codes;
+            a.m0.scales = (const uint16_t *)w[0]->scales;
+            a.m0.out = out[0];
+            a.m0.seg_end = d.M;
+            a.nseg = 1;
+            a.x = x;
+            a.M = d.M;
+            a.K = d.K;
+            a.gs = d.group_size;
+            a.sdt = w[0]->scale_dtype;
+            uint32_t blocks = ceil_div(d.M, (uint32_t)SR);
+            if (blocks > 4096) blocks = 4096;
+            switch (nv) {
+            case 2: qmv1_splitk_kernel<XDT, EPI, ODT, 2, SR><<<blocks, 128, 0, ctx->stream>>>(a); break;
+            case 3: qmv1_splitk_kernel<XDT, EPI, ODT, 3, SR><<<blocks, 192, 0, ctx->stream>>>(a); break;
+            default: qmv1_splitk_kernel<XDT, EPI, ODT, 4, SR><<<blocks, 256, 0, ctx->stream>>>(a); break;
+            }
+            NNZ_LAUNCHED(ctx);
+            return NNZ_OK;
+        }
+    }
     int R = 4;
     // Rows per wave-step: as many as keep about one block per CU (pairs:
     // two) -- measured best for the decode shapes -- bounded by the weight

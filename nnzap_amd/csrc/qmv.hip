@@ -848,7 +848,7 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
                   (EPI == EPI_STORE || EPI == EPI_RESADD)) {
         // long single-segment rows: split K over the waves of a block
         if (nw == 1 && lpr == 64 && nv >= 2 && nv <= 4 && d.K % 2048 == 0) {
-            constexpr int SR = 2;
+            constexpr int SR = 4;
             QmvArgs a{};
             a.m0.codes = (const uint32_t *)w[0]->codes;
             a.m0.scales = (const uint16_t *)w[0]->scales;

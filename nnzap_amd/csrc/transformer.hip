@@ -637,10 +637,12 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
                 for (int g = 0; g < G; ++g) dot[g] = fmaf(qs[g][d + 1], k1, fmaf(qs[g][d], k0, dot[g]));
             }
         }
+        // the TPT lanes of a token are consecutive lanes of one quad
+        static_assert(TPT <= 4, "lanes per token within a DPP quad");
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-#pragma unroll
-            for (int o = TPT / 2; o >= 1; o >>= 1) dot[g] += __shfl_xor(dot[g], o, 64);
+            if constexpr (TPT >= 2) dot[g] += dpp_move<DPP_XOR1>(dot[g], 0.f);
+            if constexpr (TPT >= 4) dot[g] += dpp_move<DPP_XOR2>(dot[g], 0.f);
         }
         if (ksub == 0) {
 #pragma unroll
@@ -683,6 +685,9 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
         float o[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) o[g] = 0.f;
+        // full chunks without the new token (all but at most two) skip the
+        // end and new-token checks (block-uniform branch)
+        const bool plain = !owns_new && len == (uint32_t)FCHUNK;
 #pragma unroll
         for (int v = 0; v < VV4; ++v) {
             const uint32_t wv[4] = {vreg[v].x, vreg[v].y, vreg[v].z, vreg[v].w};
@@ -691,11 +696,13 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
                 const int t = vpart * VT + v * 8 + 2 * e;
                 float v0, v1;
                 unpack2<NNZ_F16>(wv[e], v0, v1);
-                // past the end: weight 0, value 0 (never NaN * 0)
-                v0 = (uint32_t)t < len ? v0 : 0.f;
-                v1 = (uint32_t)t + 1 < len ? v1 : 0.f;
-                if (owns_new && t0 + t == pos) v0 = vnew[vd];
-                if (owns_new && t0 + t + 1 == pos) v1 = vnew[vd];
+                if (!plain) {
+                    // past the end: weight 0, value 0 (never NaN * 0)
+                    v0 = (uint32_t)t < len ? v0 : 0.f;
+                    v1 = (uint32_t)t + 1 < len ? v1 : 0.f;
+                    if (owns_new && t0 + t == pos) v0 = vnew[vd];
+                    if (owns_new && t0 + t + 1 == pos) v1 = vnew[vd];
+                }
 #pragma unroll
                 for (int g = 0; g < G; ++g) o[g] = fmaf(pe[g][t + 1], v1, fmaf(pe[g][t], v0, o[g]));
             }

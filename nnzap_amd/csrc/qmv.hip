@@ -275,15 +275,24 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
 #pragma unroll
     for (int j = 0; j < NV; ++j) uvalid[j] = (uint32_t)ll + (uint32_t)(LPR * j) < units;
 
-    const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
     const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
     const uint32_t rows_per_iter = (uint32_t)(R * RPW);
     uint32_t base = wave * rows_per_iter;
 
-    // ---- first weight loads, before the x prologue ------------------------
+    // ---- load order ----------------------------------------------------------
+    // The prologue's own loads (x, or the residual and norm weights, or the
+    // attention partials) are issued first and the first row-step's weights
+    // right after them: loads complete in issue order, so the prologue then
+    // waits only for its own data while the weights are still in flight.
+    // The weight loads are never branched around (a branch makes the wait
+    // at its join cover every load issued before it): past the end, a step
+    // re-reads rows that are valid, and their values go unused.
     StepRegs<NMAT, R, NV, VEC> cur;
-    if (base < a.M)
-        load_step<BITS, NMAT, R, NV, EPI == EPI_RESADD>(a, cur, base, RPW, rr, ll, LPR, uvalid, units, G);
+    auto first_weights = [&]() {
+        load_step<BITS, NMAT, R, NV, EPI == EPI_RESADD>(a, cur, base < a.M ? base : 0u, RPW, rr, ll, LPR,
+                                                        uvalid, units, G);
+    };
 
     // ---- x slice for the owned units, kept in registers -------------------
     // A unit past the row end holds unit 0's (finite) values; its scale is
@@ -310,6 +319,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
             rv[k] = res4[ic];
             wv[k] = nw4[ic];
         }
+        first_weights();
         float ss = 0.f;
 #pragma unroll
         for (int k = 0; k < P4; ++k) {
@@ -369,6 +379,18 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
         const MergeIn &mg = a.mg;
         const uint32_t D = mg.head_dim;
         const uint32_t heads = K / D;
+        const uint32_t seq = mg.d_seq ? *mg.d_seq : mg.seq_len;
+        // (m, l) of this thread's (head, chunk) pairs p = tid + 256 i, then
+        // the partial outputs, then the weights
+        constexpr int PI = 2 * NV;   // heads x 16 <= 512 NV pairs
+        float2 mlv[PI];
+#pragma unroll
+        for (int i = 0; i < PI; ++i) {
+            const uint32_t p = threadIdx.x + 256u * i;
+            const uint32_t hd = p / MERGE_MAX_CHUNKS, c = p % MERGE_MAX_CHUNKS;
+            const bool ok = hd < heads && c < mg.nchunks;
+            mlv[i] = *(const float2 *)(mg.part_ml + (ok ? ((size_t)hd * mg.nchunks + c) * 2 : 0));
+        }
         float4 oa[NV][MERGE_MAX_CHUNKS], ob[NV][MERGE_MAX_CHUNKS];
 #pragma unroll
         for (int kk = 0; kk < NV; ++kk) {
@@ -386,13 +408,15 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                 }
             }
         }
-        const uint32_t seq = mg.d_seq ? *mg.d_seq : mg.seq_len;
+        first_weights();
         const uint32_t nch = min(mg.nchunks, ceil_div(seq, mg.chunk));
-        for (uint32_t p = threadIdx.x; p < ((heads * MERGE_MAX_CHUNKS + 255) / 256) * 256; p += 256) {
+#pragma unroll
+        for (int i = 0; i < PI; ++i) {
+            const uint32_t p = threadIdx.x + 256u * i;
+            if (p >= ((heads * MERGE_MAX_CHUNKS + 255) / 256) * 256) break;   // uniform
             const uint32_t hd = p / MERGE_MAX_CHUNKS, c = p % MERGE_MAX_CHUNKS;
             const bool on = hd < heads && c < nch;
-            const float2 ml = on ? *(const float2 *)(mg.part_ml + ((size_t)hd * mg.nchunks + c) * 2)
-                                 : make_float2(-INFINITY, 0.f);
+            const float2 ml = on ? mlv[i] : make_float2(-INFINITY, 0.f);
             float M = ml.x;   // max over the head's 16 lanes
             M = fmaxf(M, dpp_move<DPP_XOR1>(M, -INFINITY));
             M = fmaxf(M, dpp_move<DPP_XOR2>(M, -INFINITY));
@@ -448,23 +472,32 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
             }
         }
     } else {
+        // unconditional loads (unit 0 stands in past the row end): raw
+        // 16-byte vectors first, converted after the weight loads are out
+        constexpr int XV = XDT == NNZ_F32 ? 8 : 4;   // 16-byte loads per unit
+        uint4 xraw[NV][XV];
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
-            // unconditional loads (unit 0 stands in past the row end)
             const uint32_t u = uvalid[j] ? (uint32_t)ll + (uint32_t)(LPR * j) : 0u;
+            const uint4 *p = XDT == NNZ_F32 ? (const uint4 *)((const float *)a.x + (size_t)u * 32)
+                                            : (const uint4 *)((const uint16_t *)a.x + (size_t)u * 32);
+#pragma unroll
+            for (int i = 0; i < XV; ++i) xraw[j][i] = p[i];
+        }
+        first_weights();
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
             if constexpr (XDT == NNZ_F32) {
-                const float4 *p = (const float4 *)((const float *)a.x + (size_t)u * 32);
 #pragma unroll
                 for (int i = 0; i < 8; ++i) {
-                    const float4 v = p[i];
-                    xr[j][4 * i] = v.x; xr[j][4 * i + 1] = v.y;
-                    xr[j][4 * i + 2] = v.z; xr[j][4 * i + 3] = v.w;
+                    const uint4 v = xraw[j][i];
+                    xr[j][4 * i] = __uint_as_float(v.x); xr[j][4 * i + 1] = __uint_as_float(v.y);
+                    xr[j][4 * i + 2] = __uint_as_float(v.z); xr[j][4 * i + 3] = __uint_as_float(v.w);
                 }
             } else {
-                const uint4 *p = (const uint4 *)((const uint16_t *)a.x + (size_t)u * 32);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const uint4 v = p[i];
+                    const uint4 v = xraw[j][i];
                     uint32_t wv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
@@ -523,8 +556,8 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
     for (; base < a.M; base += nwaves * rows_per_iter) {
         const uint32_t next = base + nwaves * rows_per_iter;
         StepRegs<NMAT, R, NV, VEC> nxt;
-        if (next < a.M)
-            load_step<BITS, NMAT, R, NV, EPI == EPI_RESADD>(a, nxt, next, RPW, rr, ll, LPR, uvalid, units, G);
+        load_step<BITS, NMAT, R, NV, EPI == EPI_RESADD>(a, nxt, next < a.M ? next : base, RPW, rr, ll, LPR,
+                                                        uvalid, units, G);
 
         float acc[NMAT][R];
 #pragma unroll
@@ -654,25 +687,31 @@ __global__ __launch_bounds__(64 * KS) void qmv1_splitk_kernel(QmvArgs a) {
 
     uint32_t base = blockIdx.x * R;
     const uint32_t stride = gridDim.x * R;
-    Step cur;
-    if (base < M) load(base, cur);
 
-    // this lane's 32 x values (unit 0 stands in past the row end; its scale
-    // is zeroed below)
+    // this lane's 32 x values first (unit 0 stands in past the row end; its
+    // scale is zeroed below), then the first step's weights: loads complete
+    // in issue order, so the x conversion does not wait for the weights
+    constexpr int XV = XDT == NNZ_F32 ? 8 : 4;
+    uint4 xraw[XV];
+    {
+        const uint4 *p = XDT == NNZ_F32 ? (const uint4 *)((const float *)a.x + (size_t)uc * 32)
+                                        : (const uint4 *)((const uint16_t *)a.x + (size_t)uc * 32);
+#pragma unroll
+        for (int i = 0; i < XV; ++i) xraw[i] = p[i];
+    }
+    Step cur;
+    load(base < M ? base : 0u, cur);   // never branched around (see qmv_kernel)
     float xr[32], xsum = 0.f;
     if constexpr (XDT == NNZ_F32) {
-        const float4 *p = (const float4 *)((const float *)a.x + (size_t)uc * 32);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const float4 v = p[i];
-            xr[4 * i] = v.x; xr[4 * i + 1] = v.y; xr[4 * i + 2] = v.z; xr[4 * i + 3] = v.w;
+            xr[4 * i] = __uint_as_float(xraw[i].x); xr[4 * i + 1] = __uint_as_float(xraw[i].y);
+            xr[4 * i + 2] = __uint_as_float(xraw[i].z); xr[4 * i + 3] = __uint_as_float(xraw[i].w);
         }
     } else {
-        const uint4 *p = (const uint4 *)((const uint16_t *)a.x + (size_t)uc * 32);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const uint4 v = p[i];
-            const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+            const uint32_t wv[4] = {xraw[i].x, xraw[i].y, xraw[i].z, xraw[i].w};
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const uint16_t lo = (uint16_t)(wv[t] & 0xFFFFu), hi = (uint16_t)(wv[t] >> 16);
@@ -691,7 +730,7 @@ __global__ __launch_bounds__(64 * KS) void qmv1_splitk_kernel(QmvArgs a) {
 
     for (int it = 0; base < M; base += stride, ++it) {
         Step nxt;
-        if (base + stride < M) load(base + stride, nxt);
+        load(base + stride < M ? base + stride : base, nxt);
         const int buf = it & 1;
 #pragma unroll
         for (int r = 0; r < R; ++r) {

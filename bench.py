@@ -35,6 +35,19 @@ if ROOT not in sys.path:
 PEAK_HBM_GBS = 8000.0
 BASELINE_TOKS = 182.8  # reference decode tok/s, Bonsai-1.7B Q1 bs1 (README.md:71-77)
 ROTATE_BYTES = 640 << 20
+MIN_COPIES = 64
+
+
+def random_copies(shape, dtype, per_copy_bytes, seed):
+    """Independently drawn N(0,1) device tensors (cast to dtype), at least
+    MIN_COPIES of them and at least ROTATE_BYTES in all."""
+    import torch
+    n = max(MIN_COPIES, int(ROTATE_BYTES // per_copy_bytes) + 1)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    out = [torch.randn(shape, device="cuda", generator=g).to(dtype) for _ in range(n)]
+    torch.cuda.synchronize()
+    return out
 
 
 def log(*a):
@@ -91,13 +104,15 @@ def bench_decode(args, dev):
 # --------------------------------------------------------------- kernels ----
 class Rot:
     """Distinct device copies of one quantised matrix (same values, distinct
-    addresses), enough to exceed the on-die caches when cycled."""
+    addresses): at least MIN_COPIES and at least ``total_bytes`` in all, so
+    that cycling through them streams every launch from HBM (the 256 MB
+    Infinity Cache holds any single working set)."""
 
     def __init__(self, dev, w, total_bytes):
         import torch
         from nnzap_amd import ops
         base = ops.DeviceQWeight(dev, w)
-        self.n = max(2, int(total_bytes // max(1, w.nbytes)) + 1)
+        self.n = max(MIN_COPIES, int(total_bytes // max(1, w.nbytes)) + 1)
         self.ws = [base]
         for _ in range(self.n - 1):
             c = object.__new__(ops.DeviceQWeight)
@@ -200,8 +215,8 @@ def _kernel_cases():
         # one decode layer's attention: q/k norm + RoPE, KV append, attention
         # over 640 tokens (the mean context of the timed steps), merge
         seq, max_ctx = 640, 1024
-        kc = torch.randn(8, max_ctx, 128, device="cuda").to(f16)
-        vc = torch.randn(8, 128, max_ctx, device="cuda").to(f16)
+        kcs = random_copies((8, max_ctx, 128), f16, 8 * max_ctx * 128 * 4, 23)
+        vcs = random_copies((8, 128, max_ctx), f16, 8 * max_ctx * 128 * 4, 24)
         qr = torch.randn(16 * 128, device="cuda").to(f16)
         kr = torch.randn(8 * 128, device="cuda").to(f16)
         vr = torch.randn(8 * 128, device="cuda").to(f16)
@@ -211,7 +226,7 @@ def _kernel_cases():
         scr = torch.zeros(ops.gqa_scratch_bytes(L.GQADims(16, 8, 128, seq, max_ctx, 2)) // 4 + 64,
                           dtype=f32, device="cuda")
         us = time_launches(dev, lambda i: ops.dispatch_gqa_attention_fused_1pass(
-            dev, qr, kc, vc, att, kr, vr, qn, qn, scr, fd), n)
+            dev, qr, kcs[i % len(kcs)], vcs[i % len(vcs)], att, kr, vr, qn, qn, scr, fd), n)
         return us, 2 * 8 * seq * 128 * 2 + 16 * 128 * 4 + 8 * 128 * 8, None
 
     def dec_attention_partials(dev, n):
@@ -219,8 +234,8 @@ def _kernel_cases():
         # KV append, split-sequence attention to per-chunk partials, at the
         # mean context of the timed steps (640 tokens)
         seq, max_ctx = 640, 1024
-        kc = torch.randn(8, max_ctx, 128, device="cuda").to(f16)
-        vc = torch.randn(8, 128, max_ctx, device="cuda").to(f16)
+        kcs = random_copies((8, max_ctx, 128), f16, 8 * max_ctx * 128 * 4, 21)
+        vcs = random_copies((8, 128, max_ctx), f16, 8 * max_ctx * 128 * 4, 22)
         qr = torch.randn(16 * 128, device="cuda").to(f16)
         kr = torch.randn(8 * 128, device="cuda").to(f16)
         vr = torch.randn(8 * 128, device="cuda").to(f16)
@@ -231,7 +246,8 @@ def _kernel_cases():
         pm = torch.empty(16 * nch * 2, dtype=f32, device="cuda")
         fd = L.GQAFusedDims(16, 8, 128, seq, max_ctx, 2, seq - 1, 1e-6, 1e6)
         us = time_launches(dev, lambda i: ops.dispatch_gqa_attention_partials(
-            dev, qr, kc, vc, kr, vr, qn, qn, po, pm, fd, rope_inv_freq=freqs), n)
+            dev, qr, kcs[i % len(kcs)], vcs[i % len(vcs)], kr, vr, qn, qn, po, pm, fd,
+            rope_inv_freq=freqs), n)
         # K and V of 640 tokens x 8 heads, q/k/v in, new K/V row out, partials out
         nbytes = 2 * 8 * seq * 128 * 2 + (16 + 16) * 128 * 2 + 8 * 128 * 4 + 16 * nch * 130 * 4
         return us, nbytes, 28
@@ -304,15 +320,17 @@ def _kernel_cases():
 
     def config4(L_):
         def run(dev, n):
-            kb = torch.randn(8, L_, 128, device="cuda").to(torch.bfloat16)
-            vb = torch.randn(8, L_, 128, device="cuda").to(torch.bfloat16)
+            per = 8 * L_ * 128 * 2
+            kbs = random_copies((8, L_, 128), torch.bfloat16, 2 * per, 40 + L_)
+            vbs = random_copies((8, L_, 128), torch.bfloat16, 2 * per, 41 + L_)
             qb = torch.randn(16, 128, device="cuda").to(torch.bfloat16)
             ob = torch.empty(16, 128, dtype=f32, device="cuda")
             d4 = L.GQADims(16, 8, 128, L_, L_, 2)
             s4 = torch.empty(ops.gqa_scratch_bytes(d4) // 4 + 64, dtype=f32, device="cuda")
             us = time_launches(dev, lambda i: ops.dispatch_gqa_attention(
-                dev, qb, kb, vb, ob, s4, d4, v_transposed=False, rope_position=L_,
-                rope_theta=1e6), max(16, n // 4))
+                dev, qb, kbs[i % len(kbs)], vbs[i % len(vbs)], ob, s4, d4, v_transposed=False,
+                rope_position=L_, rope_theta=1e6), max(16, n // 4))
+            del kbs, vbs
             return us, 4096 * L_ + 12288, None
         return run
 

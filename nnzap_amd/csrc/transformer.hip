@@ -438,23 +438,61 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     }
 }
 
-// Combine the per-chunk partials of one query head (grid = (Hq, Z), block = D).
-__global__ __launch_bounds__(128) void attn_combine_kernel(AttnArgs a, uint32_t D) {
-    const uint32_t qh = blockIdx.x, z = blockIdx.y, d = threadIdx.x;
-    if (d >= D) return;
+// Combine the per-chunk partials of one query head (grid = (Hq, Z), 256
+// threads).  The chunk maxima and weighted exp-sums are folded block-wide;
+// then 256/(D/4) groups of D/4 lanes each sum a disjoint, strided subset of
+// the chunks' o rows with 16-byte loads (several in flight per lane), and the
+// groups are folded in LDS.  part_o rows are 16-byte aligned (D % 4 == 0 and
+// an aligned base, checked by the launcher).
+template <int D>
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
+    constexpr int NV = D / 4, PARTS = 256 / NV;
+    __shared__ float red[4];
+    __shared__ float4 acc[256];
+    const uint32_t qh = blockIdx.x, z = blockIdx.y, tid = threadIdx.x;
     const uint32_t seq = (a.d_seq ? *a.d_seq : a.seq_len) + z;
     const uint32_t nch = min(a.nchunks, ceil_div(seq, a.chunk));
     const size_t base = ((size_t)z * a.hq + qh) * a.nchunks;
-    const float *ml = a.part_ml + base * 2;
-    float M = -INFINITY;
-    for (uint32_t c = 0; c < nch; ++c) M = fmaxf(M, ml[2 * c]);
-    float num = 0.f, den = 0.f;
-    for (uint32_t c = 0; c < nch; ++c) {
-        const float w = expf(ml[2 * c] - M);
-        den = fmaf(w, ml[2 * c + 1], den);
-        num = fmaf(w, a.part_o[(base + c) * D + d], num);
+    const float2 *ml = (const float2 *)(a.part_ml + base * 2);
+    float m = -INFINITY;
+    for (uint32_t c = tid; c < nch; c += 256) m = fmaxf(m, ml[c].x);
+    const float M = block_max_256(m, red);
+    float den = 0.f;
+    for (uint32_t c = tid; c < nch; c += 256) {
+        const float2 v = ml[c];
+        den = fmaf(expf(v.x - M), v.y, den);
     }
-    store_dt(a.out, (size_t)z * a.o_stride + (size_t)qh * D + d, num / den, a.odt);
+    den = block_sum_256(den, red);
+
+    const uint32_t dv = tid % NV, p = tid / NV;
+    const float4 *po = (const float4 *)(a.part_o + base * D) + dv;
+    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 4
+    for (uint32_t c = p; c < nch; c += PARTS) {
+        const float w = expf(ml[c].x - M);
+        const float4 o = po[(size_t)c * NV];
+        s.x = fmaf(w, o.x, s.x);
+        s.y = fmaf(w, o.y, s.y);
+        s.z = fmaf(w, o.z, s.z);
+        s.w = fmaf(w, o.w, s.w);
+    }
+    acc[tid] = s;
+    __syncthreads();
+    if (tid < (uint32_t)NV) {
+#pragma unroll
+        for (int q = 1; q < PARTS; ++q) {
+            const float4 o = acc[q * NV + tid];
+            s.x += o.x;
+            s.y += o.y;
+            s.z += o.z;
+            s.w += o.w;
+        }
+        const size_t ob = (size_t)z * a.o_stride + (size_t)qh * D + 4 * tid;
+        store_dt(a.out, ob + 0, s.x / den, a.odt);
+        store_dt(a.out, ob + 1, s.y / den, a.odt);
+        store_dt(a.out, ob + 2, s.z / den, a.odt);
+        store_dt(a.out, ob + 3, s.w / den, a.odt);
+    }
 }
 
 // ------------------------------------------------- fused decode attention --
@@ -485,6 +523,8 @@ struct FusedAttnArgs {
     const float *inv_freq;          // [D/2] RoPE frequencies, or null (computed here)
     uint32_t seq_len, max_ctx, nchunks;
     uint32_t gfull;                 // query heads per KV head
+    uint32_t units;                 // nchunks * Hkv (chunk, KV head) pairs
+    uint32_t parts;                 // blocks per unit (query-head groups of G)
     int direct;                     // one chunk and no consumer merge: write out
     float eps, theta, scale;
 };
@@ -508,10 +548,16 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
     __shared__ float hsum[G][4];
 
     const int tid = threadIdx.x;
-    // block (c, y) serves query heads [qb, qb + G) of KV head h; when a KV
-    // group is split over several blocks, the first one appends to the cache
-    const uint32_t c = blockIdx.x, qb = blockIdx.y * G, h = qb / a.gfull;
-    const bool writer = qb % a.gfull == 0;
+    // 1-D grid.  Unit u = (chunk c, KV head h); its `parts` blocks serve the
+    // query heads [qb, qb + G) of h and sit 8 ids apart, so that workgroups
+    // dispatched round-robin over the 8 XCDs put them on one XCD and its L2
+    // serves their shared K/V lines once.  The first part appends to the cache.
+    const uint32_t bid = blockIdx.x, span = 8 * a.parts;
+    const uint32_t j = a.parts == 1 ? 0u : (bid % span) / 8;
+    const uint32_t u = a.parts == 1 ? bid : (bid / span) * 8 + bid % 8;
+    if (u >= a.units) return;
+    const uint32_t c = u % a.nchunks, h = u / a.nchunks, qb = h * a.gfull + j * G;
+    const bool writer = j == 0;
     const uint32_t seq = a.d_seq ? *a.d_seq : a.seq_len;
     const uint32_t pos = seq - 1;
     const uint32_t t0 = c * FCHUNK;
@@ -916,7 +962,7 @@ static int launch_attn_t(nnz_ctx *ctx, const AttnArgs &a, uint32_t hkv, uint32_t
     attn_split_kernel<D, G, KVDT, VT><<<grid, 256, 0, ctx->stream>>>(a);
     NNZ_LAUNCHED(ctx);
     if (a.nchunks > 1) {
-        attn_combine_kernel<<<dim3(a.hq, nq), 128, 0, ctx->stream>>>(a, D);
+        attn_combine_kernel<D><<<dim3(a.hq, nq), 256, 0, ctx->stream>>>(a);
         NNZ_LAUNCHED(ctx);
     }
     return NNZ_OK;
@@ -966,6 +1012,8 @@ int nnz_attn_launch_ex(nnz_ctx *ctx, const NnzAttnCall &c) {
                 NNZ_EINVAL, "gqa: bad dtype");
     NNZ_REQUIRE(ctx, ((uintptr_t)c.kc & 15) == 0 && ((uintptr_t)c.vc & 15) == 0, NNZ_EINVAL,
                 "gqa: caches must be 16-byte aligned");
+    NNZ_REQUIRE(ctx, ((uintptr_t)c.part_o & 15) == 0 && ((uintptr_t)c.part_ml & 7) == 0, NNZ_EINVAL,
+                "gqa: partial buffers must be 16-byte (o) and 8-byte (m, l) aligned");
     NNZ_REQUIRE(ctx, c.chunk >= 8 && c.chunk % 8 == 0 && c.chunk <= (uint32_t)ATT_MAX_CHUNK &&
                          c.nchunks >= 1 && c.nq >= 1,
                 NNZ_EINVAL, "gqa: bad chunking");
@@ -1070,11 +1118,12 @@ int nnz_attn_fused1_launch(nnz_ctx *ctx, const void *q, const void *kr, const vo
     a.theta = theta;
     a.scale = 1.0f / sqrtf((float)head_dim);
     // Few chunks x KV heads leave CUs idle: split each KV group over blocks
-    // of one query head (K/V then read once per query head, the repeats
-    // from L2).
+    // of one query head, placed on one XCD so the K/V repeats hit its L2.
     a.gfull = G;
     const uint32_t gb = (a.nchunks * hkv < 128) ? 1u : G;
-    dim3 grid(a.nchunks, hq / gb);
+    a.units = a.nchunks * hkv;
+    a.parts = G / gb;
+    const dim3 grid(a.parts == 1 ? a.units : ceil_div(a.units, 8u) * 8u * a.parts);
 #define FUSED(DD, GG) attn_fused_kernel<DD, GG><<<grid, 256, 0, ctx->stream>>>(a)
     if (gb == 1) {
         if (head_dim == 128) FUSED(128, 1);

@@ -236,6 +236,9 @@ struct AttnArgs {
 };
 
 constexpr int ATT_MAX_CHUNK = 512;
+#ifndef NNZ_DEC_TARGET_BLOCKS
+#define NNZ_DEC_TARGET_BLOCKS 1024u
+#endif
 
 __device__ __forceinline__ float load_dt(const void *p, size_t i, int dt) {
     if (dt == NNZ_F32) return ((const float *)p)[i];
@@ -439,36 +442,60 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
 }
 
 // Combine the per-chunk partials of one query head (grid = (Hq, Z), 256
-// threads).  The chunk maxima and weighted exp-sums are folded block-wide;
-// then 256/(D/4) groups of D/4 lanes each sum a disjoint, strided subset of
-// the chunks' o rows with 16-byte loads (several in flight per lane), and the
-// groups are folded in LDS.  part_o rows are 16-byte aligned (D % 4 == 0 and
-// an aligned base, checked by the launcher).
-template <int D>
+// threads) in one round of loads: every thread issues its (m, l) pair (one
+// chunk per thread) and, as one of 256/(D/4) groups of D/4 lanes, the o
+// rows of up to PRE chunks of its strided subset with 16-byte loads,
+// before any of them is used; longer sequences loop over the rest.  The
+// chunk maxima and weighted exp-sums are folded block-wide, the o sums in
+// LDS.  Indices past the live chunk count are clamped to a written chunk
+// and masked by selection (never multiplied), so stale partials cannot
+// leak in.  part_o rows are 16-byte aligned (checked by the launcher); the
+// launcher picks PRE to cover the chunk count (launch_combine).
+template <int D, int PRE>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     constexpr int NV = D / 4, PARTS = 256 / NV;
     __shared__ float red[4];
     __shared__ float4 acc[256];
     const uint32_t qh = blockIdx.x, z = blockIdx.y, tid = threadIdx.x;
-    const uint32_t seq = (a.d_seq ? *a.d_seq : a.seq_len) + z;
-    const uint32_t nch = min(a.nchunks, ceil_div(seq, a.chunk));
+    const uint32_t dv = tid % NV, p = tid / NV;
     const size_t base = ((size_t)z * a.hq + qh) * a.nchunks;
     const float2 *ml = (const float2 *)(a.part_ml + base * 2);
-    float m = -INFINITY;
-    for (uint32_t c = tid; c < nch; c += 256) m = fmaxf(m, ml[c].x);
+    const float4 *po = (const float4 *)(a.part_o + base * D) + dv;
+    const uint32_t last = a.nchunks - 1;
+    const float2 mine = ml[min(tid, last)];
+    float2 mlk[PRE];
+    float4 ok[PRE];
+#pragma unroll
+    for (int k = 0; k < PRE; ++k) {
+        const uint32_t c = min(p + (uint32_t)(PARTS * k), last);
+        mlk[k] = ml[c];
+        ok[k] = po[(size_t)c * NV];
+    }
+    const uint32_t seq = (a.d_seq ? *a.d_seq : a.seq_len) + z;
+    const uint32_t nch = min(a.nchunks, ceil_div(seq, a.chunk));
+
+    float m = tid < nch ? mine.x : -INFINITY;
+    for (uint32_t c = tid + 256; c < nch; c += 256) m = fmaxf(m, ml[c].x);
     const float M = block_max_256(m, red);
-    float den = 0.f;
-    for (uint32_t c = tid; c < nch; c += 256) {
+    float den = tid < nch ? expf(mine.x - M) * mine.y : 0.f;
+    for (uint32_t c = tid + 256; c < nch; c += 256) {
         const float2 v = ml[c];
         den = fmaf(expf(v.x - M), v.y, den);
     }
     den = block_sum_256(den, red);
 
-    const uint32_t dv = tid % NV, p = tid / NV;
-    const float4 *po = (const float4 *)(a.part_o + base * D) + dv;
     float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < PRE; ++k) {
+        const bool live = p + (uint32_t)(PARTS * k) < nch;
+        const float w = expf(mlk[k].x - M);
+        s.x = live ? fmaf(w, ok[k].x, s.x) : s.x;
+        s.y = live ? fmaf(w, ok[k].y, s.y) : s.y;
+        s.z = live ? fmaf(w, ok[k].z, s.z) : s.z;
+        s.w = live ? fmaf(w, ok[k].w, s.w) : s.w;
+    }
 #pragma unroll 4
-    for (uint32_t c = p; c < nch; c += PARTS) {
+    for (uint32_t c = p + PARTS * PRE; c < nch; c += PARTS) {
         const float w = expf(ml[c].x - M);
         const float4 o = po[(size_t)c * NV];
         s.x = fmaf(w, o.x, s.x);
@@ -828,6 +855,253 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const float *part_o, co
     out[(size_t)qh * D + d] = (f16_t)(num / den);
 }
 
+// ------------------------------------------------- single-query attention --
+// GQA attention of one query over a cache it does not modify (the public
+// gqa entry point): f16 or bf16 caches, V as [Hkv][D][max_ctx] (VT) or
+// [Hkv][max_ctx][D], optional RoPE of q, any q/output dtype.
+//   * 1-D grid of units (chunk c of `sub` x FCHUNK tokens, KV head h) x
+//     parts, placed as in attn_fused_kernel (a unit's parts on one XCD);
+//   * a block walks its chunk FCHUNK tokens at a time with an online
+//     softmax; the next sub-chunk's K and V are loaded into the other of two
+//     register sets while the current one is used, and all loads of a
+//     sub-chunk are issued before the first of them is consumed;
+//   * scores with 256/FCHUNK lanes per token, P.V from registers;
+//   * one chunk: the output; several: partials for attn_combine_kernel.
+struct DecAttnArgs {
+    const void *q;                  // [Hq][D] in qdt
+    const uint16_t *kc, *vc;        // caches (f16 or bf16 bits)
+    void *out;                      // [Hq][D] in odt
+    float *part_o, *part_ml;        // [Hq][nchunks][D], [Hq][nchunks][2]
+    const uint32_t *d_seq;          // device seq_len or null
+    uint32_t seq_len, max_ctx, nchunks, sub, gfull, units, parts;
+    int32_t rope_pos;
+    int qdt, odt;
+    float rope_theta, scale;
+};
+
+template <int D, int G, int KVDT, bool VT>
+__global__ __launch_bounds__(256) void attn_decode_kernel(DecAttnArgs a) {
+    constexpr int NQ = (G * D + 255) / 256;
+    constexpr int TPT = 256 / FCHUNK;            // lanes per token (scores)
+    constexpr int KV4 = D / 8 / TPT;             // K: 16-byte vectors per lane
+    constexpr int PARTS = 256 / D;               // VT: token parts per d
+    constexpr int VTOK = FCHUNK / PARTS;         // VT: tokens per thread
+    constexpr int DP = D / 8, TG = 256 / DP;     // !VT: lanes per row, token groups
+    constexpr int VV4 = VT ? VTOK / 8 : FCHUNK / TG;
+    constexpr int NRED = VT ? PARTS : 4;
+    static_assert(KV4 >= 1 && VV4 >= 1 && TPT <= 4 && FCHUNK == 64, "chunk/head_dim");
+    __shared__ float qs[G][D];
+    __shared__ float ps[G][FCHUNK];
+    __shared__ float pe[G][FCHUNK];
+    __shared__ float ored[NRED][G][D];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const uint32_t bid = blockIdx.x, span = 8 * a.parts;
+    const uint32_t j = a.parts == 1 ? 0u : (bid % span) / 8;
+    const uint32_t u = a.parts == 1 ? bid : (bid / span) * 8 + bid % 8;
+    if (u >= a.units) return;
+    const uint32_t c = u % a.nchunks, h = u / a.nchunks, qb = h * a.gfull + j * G;
+    const uint32_t seq = a.d_seq ? *a.d_seq : a.seq_len;
+    const uint32_t c0 = c * a.sub * FCHUNK;
+    if (c0 >= seq) return;  // the combine step reads chunks < ceil(seq / chunk) only
+    const uint32_t ns = min(a.sub, ceil_div(seq - c0, (uint32_t)FCHUNK));
+
+    float qv[NQ];
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+        const int i = tid + 256 * k;
+        qv[k] = load_dt(a.q, (size_t)qb * D + (i < G * D ? i : 0), a.qdt);
+    }
+
+    const size_t kv_stride = (size_t)a.max_ctx * D;
+    const uint16_t *kb = a.kc + h * kv_stride, *vb = a.vc + h * kv_stride;
+    const int kt = tid / TPT, ksub = tid % TPT;
+    const int vd = tid % D, vpart = tid / D;      // VT roles
+    const int dp = tid % DP, tg = tid / DP;       // !VT roles
+    // Loads of sub-chunk s (s < ns): tokens past the end read an in-range
+    // token (K: the last one; V: group 0 or the last row) and are masked.
+    auto load = [&](uint4 (&kr)[KV4], uint4 (&vr)[VV4], uint32_t s) {
+        const uint32_t t0 = c0 + s * FCHUNK, len = min((uint32_t)FCHUNK, seq - t0);
+        const uint4 *kp = (const uint4 *)(kb + (size_t)(t0 + min((uint32_t)kt, len - 1)) * D) + ksub * KV4;
+#pragma unroll
+        for (int v = 0; v < KV4; ++v) kr[v] = kp[v];
+        if constexpr (VT) {
+            const uint16_t *row = vb + (size_t)vd * a.max_ctx + t0;
+#pragma unroll
+            for (int v = 0; v < VV4; ++v) {
+                const uint32_t g0 = (uint32_t)(vpart * VTOK + v * 8);
+                vr[v] = *(const uint4 *)(row + (g0 < len ? g0 : 0u));
+            }
+        } else {
+#pragma unroll
+            for (int v = 0; v < VV4; ++v) {
+                const uint32_t t = min((uint32_t)(v * TG + tg), len - 1);
+                vr[v] = *((const uint4 *)(vb + (size_t)(t0 + t) * D) + dp);
+            }
+        }
+    };
+    uint4 kA[KV4], vA[VV4], kB[KV4], vB[VV4];
+    load(kA, vA, 0);
+
+    // q (optionally RoPE-rotated at rope_pos) -> LDS
+#pragma unroll
+    for (int k = 0; k < NQ; ++k) {
+        const int i = tid + 256 * k;
+        float v = i < G * D ? qv[k] : 0.f;
+        if (a.rope_pos >= 0) {
+            const float partner = __shfl_xor(v, 1, 64);  // all lanes take part
+            v = rope_rotate(v, partner, i % D, (uint32_t)a.rope_pos, D, a.rope_theta);
+        }
+        if (i < G * D) qs[i / D][i % D] = v;
+    }
+    __syncthreads();
+
+    float m_run[G], l_run[G];
+    float o[G][VT ? 1 : 8];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m_run[g] = -INFINITY;
+        l_run[g] = 0.f;
+#pragma unroll
+        for (int e = 0; e < (VT ? 1 : 8); ++e) o[g][e] = 0.f;
+    }
+
+    // One sub-chunk from (kr, vr); the caller has already issued the next
+    // sub-chunk's loads into the other register set.
+    auto compute = [&](const uint4 (&kr)[KV4], const uint4 (&vr)[VV4], uint32_t s) {
+        const uint32_t t0 = c0 + s * FCHUNK, len = min((uint32_t)FCHUNK, seq - t0);
+        {
+            float dot[G];
+#pragma unroll
+            for (int g = 0; g < G; ++g) dot[g] = 0.f;
+#pragma unroll
+            for (int v = 0; v < KV4; ++v) {
+                const uint32_t wv[4] = {kr[v].x, kr[v].y, kr[v].z, kr[v].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int d = (ksub * KV4 + v) * 8 + 2 * e;
+                    float k0, k1;
+                    unpack2<KVDT>(wv[e], k0, k1);
+#pragma unroll
+                    for (int g = 0; g < G; ++g) dot[g] = fmaf(qs[g][d + 1], k1, fmaf(qs[g][d], k0, dot[g]));
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                if constexpr (TPT >= 2) dot[g] += dpp_move<DPP_XOR1>(dot[g], 0.f);
+                if constexpr (TPT >= 4) dot[g] += dpp_move<DPP_XOR2>(dot[g], 0.f);
+            }
+            if (ksub == 0) {
+#pragma unroll
+                for (int g = 0; g < G; ++g) ps[g][kt] = (uint32_t)kt < len ? dot[g] * a.scale : -INFINITY;
+            }
+        }
+        __syncthreads();
+        // online softmax: every wave sees the whole sub-chunk (one token per
+        // lane) and computes the same running max and sum
+        float alpha[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            const float sc = ps[g][lane];
+            const float mn = fmaxf(m_run[g], wave_max(sc));
+            alpha[g] = expf(m_run[g] - mn);
+            const float e = expf(sc - mn);
+            if (tid < 64) pe[g][lane] = e;
+            l_run[g] = fmaf(l_run[g], alpha[g], wave_sum(e));
+            m_run[g] = mn;
+        }
+        __syncthreads();
+        const bool plain = len == (uint32_t)FCHUNK;  // block-uniform
+        if constexpr (VT) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) o[g][0] *= alpha[g];
+#pragma unroll
+            for (int v = 0; v < VV4; ++v) {
+                const uint32_t wv[4] = {vr[v].x, vr[v].y, vr[v].z, vr[v].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int t = vpart * VTOK + v * 8 + 2 * e;
+                    float v0, v1;
+                    unpack2<KVDT>(wv[e], v0, v1);
+                    if (!plain) {  // past the end: weight 0 and value 0 (never NaN * 0)
+                        v0 = (uint32_t)t < len ? v0 : 0.f;
+                        v1 = (uint32_t)t + 1 < len ? v1 : 0.f;
+                    }
+#pragma unroll
+                    for (int g = 0; g < G; ++g) o[g][0] = fmaf(pe[g][t + 1], v1, fmaf(pe[g][t], v0, o[g][0]));
+                }
+            }
+        } else {
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[g][e] *= alpha[g];
+#pragma unroll
+            for (int v = 0; v < VV4; ++v) {
+                const int t = v * TG + tg;   // rows past the end are an in-range row, weight 0
+                const uint32_t wv[4] = {vr[v].x, vr[v].y, vr[v].z, vr[v].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float v0, v1;
+                    unpack2<KVDT>(wv[e], v0, v1);
+#pragma unroll
+                    for (int g = 0; g < G; ++g) {
+                        const float p = pe[g][t];
+                        o[g][2 * e] = fmaf(p, v0, o[g][2 * e]);
+                        o[g][2 * e + 1] = fmaf(p, v1, o[g][2 * e + 1]);
+                    }
+                }
+            }
+        }
+    };
+
+    // Sub-chunks in pairs so the two register sets alternate without moves;
+    // loads are never branched around (a clamped index re-reads the last
+    // sub-chunk, from L2), only the compute of a missing odd step is skipped.
+    for (uint32_t s = 0; s < ns; s += 2) {
+        load(kB, vB, min(s + 1, ns - 1));
+        compute(kA, vA, s);
+        load(kA, vA, min(s + 2, ns - 1));
+        if (s + 1 < ns) compute(kB, vB, s + 1);
+    }
+
+    // fold the partial P.V sums of the block
+    if constexpr (VT) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) ored[vpart][g][vd] = o[g][0];
+    } else {
+#pragma unroll
+        for (int off = DP; off < 64; off <<= 1)
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[g][e] += __shfl_xor(o[g][e], off, 64);
+        if (lane < DP) {
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ored[tid >> 6][g][dp * 8 + e] = o[g][e];
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < G * D; i += 256) {
+        const int g = i / D, d = i % D;
+        float s = 0.f;
+#pragma unroll
+        for (int p = 0; p < NRED; ++p) s += ored[p][g][d];
+        if (a.nchunks == 1) {
+            store_dt(a.out, (size_t)(qb + g) * D + d, s / l_run[g], a.odt);
+        } else {
+            const size_t slot = (size_t)(qb + g) * a.nchunks + c;
+            a.part_o[slot * D + d] = s;
+            if (d == 0) {
+                a.part_ml[slot * 2] = m_run[g];
+                a.part_ml[slot * 2 + 1] = l_run[g];
+            }
+        }
+    }
+}
+
 // -------------------------------------------------------------- embedding --
 // transformer.metal:428-481: flat bit index row*hidden + d, group flat/gs.
 __global__ void embed_q1_kernel(const uint32_t *ids, const uint8_t *bits, const uint16_t *scales,
@@ -956,13 +1230,27 @@ size_t nnz_attn_scratch_bytes_impl(uint32_t hq, uint32_t head_dim, uint32_t seq_
     return ((size_t)hq * nch * head_dim + (size_t)hq * nch * 2 + (size_t)hq * head_dim) * 4 + 256;
 }
 
+// The combine step for Hq x nq queries: the preload depth covers the chunks
+// each lane group folds (ceil(nchunks / (256 / (D/4)))), up to 16.
+template <int D>
+static void launch_combine(nnz_ctx *ctx, const AttnArgs &a, uint32_t nq) {
+    constexpr uint32_t PARTS = 256 / (D / 4);
+    const uint32_t per = ceil_div(a.nchunks, PARTS);
+    const dim3 grid(a.hq, nq);
+    if (per <= 1) attn_combine_kernel<D, 1><<<grid, 256, 0, ctx->stream>>>(a);
+    else if (per <= 2) attn_combine_kernel<D, 2><<<grid, 256, 0, ctx->stream>>>(a);
+    else if (per <= 4) attn_combine_kernel<D, 4><<<grid, 256, 0, ctx->stream>>>(a);
+    else if (per <= 8) attn_combine_kernel<D, 8><<<grid, 256, 0, ctx->stream>>>(a);
+    else attn_combine_kernel<D, 16><<<grid, 256, 0, ctx->stream>>>(a);
+}
+
 template <int D, int G, int KVDT, bool VT>
 static int launch_attn_t(nnz_ctx *ctx, const AttnArgs &a, uint32_t hkv, uint32_t nq) {
     dim3 grid(a.nchunks, hkv, nq);
     attn_split_kernel<D, G, KVDT, VT><<<grid, 256, 0, ctx->stream>>>(a);
     NNZ_LAUNCHED(ctx);
     if (a.nchunks > 1) {
-        attn_combine_kernel<D><<<dim3(a.hq, nq), 256, 0, ctx->stream>>>(a);
+        launch_combine<D>(ctx, a, nq);
         NNZ_LAUNCHED(ctx);
     }
     return NNZ_OK;
@@ -990,7 +1278,7 @@ static int launch_attn_d(nnz_ctx *ctx, const AttnArgs &a, uint32_t hkv, uint32_t
 
 // Full-control attention launch used by the public entry points and by the
 // decoder (prefill: nq causal queries; decode graph: seq_len read from d_seq).
-int nnz_attn_launch_ex(nnz_ctx *ctx, const NnzAttnCall &c) {
+static int attn_validate(nnz_ctx *ctx, const NnzAttnCall &c) {
     const nnz_gqa_dims &d = c.dims;
     NNZ_REQUIRE(ctx, c.q && c.kc && c.vc && c.out && c.part_o && c.part_ml, NNZ_EINVAL,
                 "gqa: null buffer");
@@ -1014,6 +1302,12 @@ int nnz_attn_launch_ex(nnz_ctx *ctx, const NnzAttnCall &c) {
                 "gqa: caches must be 16-byte aligned");
     NNZ_REQUIRE(ctx, ((uintptr_t)c.part_o & 15) == 0 && ((uintptr_t)c.part_ml & 7) == 0, NNZ_EINVAL,
                 "gqa: partial buffers must be 16-byte (o) and 8-byte (m, l) aligned");
+    return NNZ_OK;
+}
+
+int nnz_attn_launch_ex(nnz_ctx *ctx, const NnzAttnCall &c) {
+    const nnz_gqa_dims &d = c.dims;
+    if (int rc = attn_validate(ctx, c)) return rc;
     NNZ_REQUIRE(ctx, c.chunk >= 8 && c.chunk % 8 == 0 && c.chunk <= (uint32_t)ATT_MAX_CHUNK &&
                          c.nchunks >= 1 && c.nq >= 1,
                 NNZ_EINVAL, "gqa: bad chunking");
@@ -1055,6 +1349,13 @@ int nnz_attn_launch(nnz_ctx *ctx, const void *q, int qdt, const void *kc, const 
                                                     d.num_kv_heads);
     NNZ_REQUIRE(ctx, scratch && scratch_bytes >= need, NNZ_EINVAL,
                 "gqa: scratch of %zu bytes needed, %zu given", need, scratch_bytes);
+    // chunks of `sub` x FCHUNK tokens: sub doubles (up to 8) while at least
+    // NNZ_DEC_TARGET_BLOCKS (chunk, KV head) units remain, so long contexts
+    // keep every CU busy with few partials to combine
+    const uint32_t nch64 = ceil_div(d.seq_len, (uint32_t)FCHUNK);
+    uint32_t sub = 1;
+    while (sub < 8 && (uint64_t)ceil_div(nch64, 2 * sub) * d.num_kv_heads >= NNZ_DEC_TARGET_BLOCKS)
+        sub *= 2;
     NnzAttnCall c{};
     c.q = q;
     c.qdt = qdt;
@@ -1064,8 +1365,8 @@ int nnz_attn_launch(nnz_ctx *ctx, const void *q, int qdt, const void *kc, const 
     c.vt = vt;
     c.out = out;
     c.odt = odt;
-    c.chunk = nnz_attn_chunk(d.seq_len, d.num_kv_heads);
-    c.nchunks = ceil_div(d.seq_len, c.chunk);
+    c.chunk = sub * FCHUNK;
+    c.nchunks = ceil_div(nch64, sub);  // <= the ceil(seq / FCHUNK) the scratch is sized for
     float *base = (float *)(((uintptr_t)scratch + 255) & ~(uintptr_t)255);
     c.part_o = base;
     c.part_ml = base + (size_t)d.num_query_heads * c.nchunks * d.head_dim;
@@ -1073,7 +1374,69 @@ int nnz_attn_launch(nnz_ctx *ctx, const void *q, int qdt, const void *kc, const 
     c.rope_pos = rope_pos;
     c.rope_theta = theta;
     c.dims = d;
-    return nnz_attn_launch_ex(ctx, c);
+    if (int rc = attn_validate(ctx, c)) return rc;
+
+    const uint32_t G = d.heads_per_kv_group;
+    DecAttnArgs a{};
+    a.q = q;
+    a.kc = (const uint16_t *)kc;
+    a.vc = (const uint16_t *)vc;
+    a.out = out;
+    a.part_o = c.part_o;
+    a.part_ml = c.part_ml;
+    a.d_seq = nullptr;
+    a.seq_len = d.seq_len;
+    a.max_ctx = d.max_context_length;
+    a.nchunks = c.nchunks;
+    a.sub = sub;
+    a.gfull = G;
+    a.units = c.nchunks * d.num_kv_heads;
+    // few units leave CUs idle: split each KV group over blocks of one query head
+    const uint32_t gb = a.units < 128 ? 1u : G;
+    a.parts = G / gb;
+    a.rope_pos = rope_pos;
+    a.qdt = qdt;
+    a.odt = odt;
+    a.rope_theta = theta;
+    a.scale = 1.0f / sqrtf((float)d.head_dim);
+    const uint32_t blocks = a.parts == 1 ? a.units : ceil_div(a.units, 8u) * 8u * a.parts;
+#define DEC(DD, GG, KK, VV) attn_decode_kernel<DD, GG, KK, VV><<<blocks, 256, 0, ctx->stream>>>(a)
+#define DEC_KV(DD, GG)                                                       \
+    do {                                                                     \
+        if (kvdt == NNZ_F16) { if (vt) DEC(DD, GG, NNZ_F16, true); else DEC(DD, GG, NNZ_F16, false); } \
+        else { if (vt) DEC(DD, GG, NNZ_BF16, true); else DEC(DD, GG, NNZ_BF16, false); }             \
+    } while (0)
+#define DEC_G(DD)                                                            \
+    do {                                                                     \
+        switch (gb) {                                                        \
+        case 1: DEC_KV(DD, 1); break;                                        \
+        case 2: DEC_KV(DD, 2); break;                                        \
+        case 4: DEC_KV(DD, 4); break;                                        \
+        default: DEC_KV(DD, 8); break;                                       \
+        }                                                                    \
+    } while (0)
+    if (d.head_dim == 128) DEC_G(128);
+    else DEC_G(64);
+#undef DEC_G
+#undef DEC_KV
+#undef DEC
+    NNZ_LAUNCHED(ctx);
+    if (a.nchunks > 1) {
+        AttnArgs m{};
+        m.out = out;
+        m.part_o = c.part_o;
+        m.part_ml = c.part_ml;
+        m.seq_len = d.seq_len;
+        m.chunk = c.chunk;
+        m.nchunks = c.nchunks;
+        m.hq = d.num_query_heads;
+        m.o_stride = d.num_query_heads * d.head_dim;
+        m.odt = odt;
+        if (d.head_dim == 128) launch_combine<128>(ctx, m, 1);
+        else launch_combine<64>(ctx, m, 1);
+        NNZ_LAUNCHED(ctx);
+    }
+    return NNZ_OK;
 }
 
 // Chunk length of the fused decode attention (fixed: the kernel prefetches
@@ -1160,8 +1523,9 @@ int nnz_rope_table_launch(nnz_ctx *ctx, float *out, uint32_t head_dim, float the
 
 // q buffer (f32) inside the attention scratch, used by the fused path.
 float *nnz_attn_scratch_q(void *scratch, const nnz_gqa_dims &d) {
-    const uint32_t chunk = nnz_attn_chunk(d.seq_len, d.num_kv_heads);
-    const uint32_t nch = ceil_div(d.seq_len, chunk);
+    // after the partials of the finest chunking any launcher uses (FCHUNK
+    // tokens), as nnz_attn_scratch_bytes_impl sizes them
+    const uint32_t nch = ceil_div(d.seq_len, (uint32_t)FCHUNK);
     float *base = (float *)(((uintptr_t)scratch + 255) & ~(uintptr_t)255);
     return base + (size_t)d.num_query_heads * nch * d.head_dim + (size_t)d.num_query_heads * nch * 2;
 }

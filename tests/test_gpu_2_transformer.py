@@ -56,6 +56,28 @@ def test_gqa_transposed_v_f16(dev, L_, max_ctx, hq, hkv, d):
     assert_close(host(out), O.f16(ref), what=f"gqa L={L_}")
 
 
+@pytest.mark.parametrize("vt", [False, True])
+def test_gqa_long_ragged_bf16(dev, vt):
+    """16397 tokens (16384 + 13): the launcher walks chunks of two 64-token
+    sub-chunks with an online softmax, the last chunk holding one ragged
+    sub-chunk; bf16 caches in both V layouts, f32 q roped at 16397, f32 out."""
+    L_, max_ctx, hq, hkv, d = 16397, 16400, 16, 8, 128
+    print(f"gqa long ragged vt={vt}", flush=True)
+    q = S.normal(410, hq * d).astype(np.float32).reshape(hq, d)
+    kb = S.f32_to_bf16_bits(S.normal(411, hkv * max_ctx * d).astype(np.float32)).reshape(hkv, max_ctx, d)
+    vb = S.f32_to_bf16_bits(S.normal(412, hkv * max_ctx * d).astype(np.float32))
+    vb = vb.reshape(hkv, d, max_ctx) if vt else vb.reshape(hkv, max_ctx, d)
+    out = torch.empty(hq, d, dtype=torch.float32, device="cuda")
+    dims = L.GQADims(hq, hkv, d, L_, max_ctx, hq // hkv)
+    ops.dispatch_gqa_attention(dev, tdev(q), from_bits16(kb, "bf16"), from_bits16(vb, "bf16"), out,
+                               _scratch(dims), dims, v_transposed=vt, rope_position=L_,
+                               rope_theta=1e6)
+    dev.sync()
+    qf = O.rope(q.astype(np.float64), L_, 1e6)
+    ref = O.attention_decode(qf, S.bf16_bits_to_f32(kb), S.bf16_bits_to_f32(vb), L_, vt)
+    assert_close(host(out), ref, what=f"gqa long vt={vt}")
+
+
 @pytest.mark.parametrize("pos", [0, 5, 600, 1500])
 def test_gqa_fused_norm_rope_kv(dev, pos):
     """transformer.metal:1467-1695 semantics: q/k per-head RMSNorm + RoPE, K/V

@@ -10,13 +10,19 @@ stream synchronisation.
 
 Also reported (same JSON line):
   roofline      the dominant decode kernel: algorithmic bytes / average launch
-                duration (HIP events on the library's stream, weights rotated
-                through >= 512 MB of copies so every launch streams from HBM);
-  qmv           configs 1-3 (4-bit QMV, 1-bit QMV, fused gate/up+SiLU) in the
-                same way;
-  cpu_baseline  the numpy oracle's decode step on this host, bounded sample.
+                duration, the "stacked" figure: N launches back to back in one
+                hipGraph, HIP events on the library's stream around the replay,
+                every working set (weights, KV caches) rotated through >= 64
+                distinct copies and >= 640 MB so every launch streams from HBM;
+                per-dispatch device durations from rocprofv3 are in profiles/;
+  qmv           configs 1-4 (4-bit QMV, 1-bit QMV, fused gate/up+SiLU, GQA
+                decode attention at L = 512/4096/32768) in the same way;
+  cpu_baseline  the numpy oracle's decode step on this host, bounded sample;
+  cpu_configs   configs 1-4 through the numpy oracle on this host (median of
+                7 after 2 warm-ups; --cpu-full: median of 30 after 5).
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--lm-head q1|tied] [--quick]
+                [--cpu-full]
 """
 from __future__ import annotations
 
@@ -427,6 +433,75 @@ def cpu_baseline(sample_layers=2, tokens=3):
                        f"per-token time = LM head + 28 x measured per-layer time")}
 
 
+def _median_time(fn, warmup=5, runs=30):
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_configs(full=False):
+    """Configs 1-4 through the numpy oracle on this host: 2 warm-up calls,
+    then the median of 7 (with full=True: 5 and the median of 30).  Two
+    variants per config: dequantise (or widen the bf16 caches) on every
+    call, and the same product on pre-dequantised float64 operands."""
+    from nnzap_amd import configs as cf
+    from nnzap_amd import synth as S
+    from oracle import oracle as O
+
+    wu, nr = (5, 30) if full else (2, 7)
+    out = {}
+    w1, x1 = cf.config1()
+    d1 = O.dequant(w1)
+    out["config1_q4mv"] = (lambda: O.qmv(w1, x1), lambda: O.qmv(w1, x1, d1), w1.nbytes + 8192 + 24576)
+    w2, x2 = cf.config2()
+    d2 = O.dequant(w2)
+    out["config2_qmv"] = (lambda: O.qmv(w2, x2), lambda: O.qmv(w2, x2, d2), w2.nbytes + 24576 + 8192)
+    wg, wup, x3 = cf.config3()
+    dg, du = O.dequant(wg), O.dequant(wup)
+    x3d = np.asarray(x3, np.float64)
+    out["config3_gate_up_silu"] = (lambda: O.qmv_pair_silu(wg, wup, x3),
+                                   lambda: O.silu(dg @ x3d) * (du @ x3d),
+                                   wg.nbytes + wup.nbytes + 8192 + 24576)
+    for L_ in (512, 4096, 32768):
+        q, k, v = cf.config4(L_)
+
+        def widen(q=q, k=k, v=v, L_=L_):
+            qf = O.rope(S.bf16_bits_to_f32(q).astype(np.float64), L_, 1e6)
+            return O.attention_decode(qf, S.bf16_bits_to_f32(k), S.bf16_bits_to_f32(v), L_, False)
+
+        qf = O.rope(S.bf16_bits_to_f32(q).astype(np.float64), L_, 1e6)
+        kf, vf = S.bf16_bits_to_f32(k).astype(np.float64), S.bf16_bits_to_f32(v).astype(np.float64)
+        out[f"config4_attention_L{L_}"] = (widen, lambda qf=qf, kf=kf, vf=vf, L_=L_:
+                                           O.attention_decode(qf, kf, vf, L_, False),
+                                           4096 * L_ + 12288)
+    res = {}
+    for name, (f_dq, f_pre, nbytes) in out.items():
+        t_dq = _median_time(f_dq, wu, nr)
+        t_pre = _median_time(f_pre, wu, nr)
+        res[name] = {"us_dequant_each_call": round(t_dq * 1e6, 1),
+                     "us_predequantised": round(t_pre * 1e6, 1),
+                     "GBs_dequant_each_call": round(nbytes / t_dq / 1e9, 3)}
+        log(f"cpu {name:26s} {t_dq * 1e6:12.1f} us (dequant each call) {t_pre * 1e6:12.1f} us (pre-dequantised)")
+    return {"kind": "port", "impl": "numpy float64 oracle", "warmup": wu, "runs": nr,
+            "stat": "median", "threads": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)),
+            "cpu_model": cpu_model(), "cpu_count": os.cpu_count(), "configs": res}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -436,6 +511,8 @@ def main():
     ap.add_argument("--lm-head", choices=("q1", "tied"), default="q1")
     ap.add_argument("--quick", action="store_true", help="fewer kernel timing iterations")
     ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--cpu-full", action="store_true",
+                    help="per-config CPU timings with 5 warm-ups and the median of 30")
     ap.add_argument("--skip-kernels", action="store_true")
     ap.add_argument("--skip-decode", action="store_true",
                     help="kernel timings only (profiling runs); no JSON line")
@@ -473,6 +550,7 @@ def main():
                     "avg_launch_us": d["us"], "algorithmic_bytes": d["bytes"],
                     "traffic_source": "profiles/pmc_traffic.md" if traffic else None}
     cpu = None if args.skip_cpu else cpu_baseline()
+    cpu_cfg = None if args.skip_cpu else cpu_configs(full=args.cpu_full)
 
     line = {
         "metric": "decode tok/s (Bonsai-1.7B, bs1) + QMV achieved HBM GB/s vs peak",
@@ -494,6 +572,7 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_configs": cpu_cfg,
         "decode": dec,
         "qmv": {k: v for k, v in kern.items() if k.startswith("config")},
         "decode_kernels": dec_k,

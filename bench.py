@@ -39,6 +39,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
+PEAK_F16_TFLOPS = 2500.0   # MI355X dense f16/bf16 MFMA
 BASELINE_TOKS = 182.8  # reference decode tok/s, Bonsai-1.7B Q1 bs1 (README.md:71-77)
 ROTATE_BYTES = 640 << 20
 MIN_COPIES = 64
@@ -340,6 +341,25 @@ def _kernel_cases():
             return us, 4096 * L_ + 12288, None
         return run
 
+    def prefill_gemm(M_, K_, mode, pair=False):
+        # one prefill dequant-GEMM of the decoder at a 512-token prompt:
+        # C[512 x M] = A[512 x K] . W^T (1-bit W, f16 A), reported as MFMA
+        # throughput; weights rotated like the QMV cases
+        def run(dev, n):
+            P = 512
+            wa = cf.q1_matrix(M_, K_, 128, 600, 601)
+            ra = Rot(dev, wa, ROTATE_BYTES // (2 if pair else 1))
+            rb = Rot(dev, cf.q1_matrix(M_, K_, 128, 602, 603), ROTATE_BYTES // 2) if pair else None
+            a16 = (torch.randn(P, K_, device="cuda") * 0.5).to(f16)
+            o = torch.empty(P, M_, dtype=f16 if mode in (L.GEMM_STORE_F16, L.GEMM_SILU_PAIR) else f32,
+                            device="cuda")
+            us = time_launches(dev, lambda i: ops.dispatch_dequant_gemm(
+                dev, ra[i], a16, o, mode, wb=rb[i] if pair else None), max(16, n // 8))
+            flops = 2 * P * M_ * K_ * (2 if pair else 1)
+            nbytes = wa.nbytes * (2 if pair else 1) + P * K_ * 2 + P * M_ * o.element_size()
+            return us, nbytes, None, flops
+        return run
+
     def copy_calib(dev, n):
         # a plain device copy of known size: the scale for FETCH/WRITE_SIZE
         a = torch.ones(64 << 20, dtype=f32, device="cuda")
@@ -363,6 +383,11 @@ def _kernel_cases():
         "dec_lm_head_f16in": dec_lm_head_f16in, "floor_residual_add": floor_small,
         "config4_attention_L512": config4(512), "config4_attention_L4096": config4(4096),
         "config4_attention_L32768": config4(32768), "copy_256MiB": copy_calib,
+        "prefill_gemm_q": prefill_gemm(QD, H, L.GEMM_STORE_F16),
+        "prefill_gemm_kv": prefill_gemm(KVD, H, L.GEMM_STORE_F16),
+        "prefill_gemm_o_resadd": prefill_gemm(H, QD, L.GEMM_RESADD),
+        "prefill_gemm_gate_up_silu": prefill_gemm(I, H, L.GEMM_SILU_PAIR, pair=True),
+        "prefill_gemm_down_resadd": prefill_gemm(H, I, L.GEMM_RESADD),
     }
 
 
@@ -374,9 +399,16 @@ def bench_kernels(dev, quick=False, only=None):
     names = [n for n in cases if n != "copy_256MiB"] if not only else only.split(",")
     res = {}
     for name in names:
-        us, nbytes, per_token = cases[name](dev, n_iter)
+        r = cases[name](dev, n_iter)
+        us, nbytes, per_token = r[:3]
         torch.cuda.synchronize()
         gbs = nbytes / (us * 1e-6) / 1e9
+        if len(r) > 3:   # MFMA-bound: FLOP/s against the dense f16 peak
+            tf = r[3] / (us * 1e-6) / 1e12
+            res[name] = {"us": round(us, 3), "flops": int(r[3]), "TFLOPs": round(tf, 1),
+                         "frac": round(tf / PEAK_F16_TFLOPS, 4)}
+            log(f"{name:28s} {us:8.2f} us  {tf:8.1f} TFLOP/s  ({r[3]} FLOP)")
+            continue
         res[name] = {"us": round(us, 3), "bytes": int(nbytes), "GBs": round(gbs, 1),
                      "frac": round(gbs / PEAK_HBM_GBS, 4)}
         if per_token is not None:
@@ -575,6 +607,7 @@ def main():
         "cpu_configs": cpu_cfg,
         "decode": dec,
         "qmv": {k: v for k, v in kern.items() if k.startswith("config")},
+        "prefill_gemm": {k: v for k, v in kern.items() if k.startswith("prefill_gemm")},
         "decode_kernels": dec_k,
     }
     if args.details:

@@ -22,112 +22,186 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // register arrays of 16-byte pieces
 
-constexpr int BM = 64, BN = 64, BK = 64, LDS_STRIDE = BK + 8;  // halfs per LDS row
+constexpr int BM = 64, BN = 64, BK = 64, LDS_STRIDE = BK + 8;  // halfs per B LDS row
+constexpr int GROUP = 4;  // K-steps whose global loads are issued together, one group ahead
+
+// waitcnt immediate for gfx9: lgkmcnt = 0 only (the wave's LDS stores done)
+constexpr int LGKM0_IMM = 15 | (3 << 14) | (7 << 4);
+
+// Workgroup barrier for the pipelined loop: the wave's own LDS stores are
+// waited for, then s_barrier.  __syncthreads() would add a release fence,
+// which also waits for the next group's global loads still in flight.  The
+// empty asm statements keep the compiler from moving LDS accesses across.
+__device__ __forceinline__ void step_barrier() {
+    __builtin_amdgcn_s_waitcnt(LGKM0_IMM);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
 
 template <int MODE, int NMAT>
-__global__ __launch_bounds__(256) void dq_gemm_kernel(const f16_t *A, const uint32_t *codes0,
+__global__ __launch_bounds__(512) void dq_gemm_kernel(const f16_t *A, const uint32_t *codes0,
                                                       const uint16_t *scales0,
                                                       const uint32_t *codes1,
                                                       const uint16_t *scales1, void *out,
                                                       uint32_t P, uint32_t M, uint32_t K,
-                                                      uint32_t gs) {
-    __shared__ __attribute__((aligned(16))) f16_t As[BM * LDS_STRIDE];
-    __shared__ __attribute__((aligned(16))) f16_t Bs[NMAT][BN * LDS_STRIDE];
+                                                      uint32_t gs_log2) {
+    // A tile of a K-step: 64 rows x 128 bytes, the eight 16-byte pieces of
+    // row r stored at slot (piece ^ (r & 7)) so the MFMA fragment reads (16
+    // rows, one piece each) spread over the banks.  B: dequantised W rows,
+    // padded by 16 bytes.  Both double-buffered by step parity.
+    __shared__ __attribute__((aligned(16))) f16_t As[2][BM * BK];
+    __shared__ __attribute__((aligned(16))) f16_t Bs[2][NMAT][BN * LDS_STRIDE];
+    // sign table: for a byte of weight bits, four words whose halves carry
+    // 0x8000 where the bit is clear -- XORed into (s, s) they give +-s
+    __shared__ __attribute__((aligned(16))) u32x4 sgn[256];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 2, wn = wave & 3;   // 8 waves: 2 x 4, each 32 rows x 16 columns
     const uint32_t p0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-    const uint32_t words_per_row = K / 32, groups_per_row = K / gs;
+    const uint32_t words_per_row = K / 32, groups_per_row = K >> gs_log2;
+    const uint32_t nk = K / BK;
+    if (tid < 256) {
+        const uint32_t b = tid;
+        u32x4 e;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            e[q] = (((b >> (2 * q)) & 1u) ? 0u : 0x8000u) | (((b >> (2 * q + 1)) & 1u) ? 0u : 0x80000000u);
+        sgn[b] = e;
+    }
 
-    float4v acc[NMAT][2][2];
+    float4v acc[NMAT][2];
 #pragma unroll
     for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2; ++i) acc[m][i] = (float4v){0.f, 0.f, 0.f, 0.f};
+
+    // Loader roles (per step): thread -> row tid/8 and piece tid%8: A's
+    // 16-byte piece (rows past P re-read row P-1, discarded at the store),
+    // W's 8 columns at 8*(tid%8).
+    const int lr = tid >> 3, lq = tid & 7, lc = lq * 8;
+    const f16_t *arow = A + (size_t)min(p0 + (uint32_t)lr, P - 1) * K + lc;
+    const uint32_t *wrow0 = codes0 + (size_t)(n0 + lr) * words_per_row;
+    const uint32_t *wrow1 = NMAT == 2 ? codes1 + (size_t)(n0 + lr) * words_per_row : wrow0;
+    const uint16_t *srow0 = scales0 + (size_t)(n0 + lr) * groups_per_row;
+    const uint16_t *srow1 = NMAT == 2 ? scales1 + (size_t)(n0 + lr) * groups_per_row : srow0;
+    const uint32_t ngroups = ceil_div(nk, (uint32_t)GROUP);
+
+    // One group's registers: A pieces, W words, scales (two sets, used in
+    // turn, so no register is copied).
+    u32x4 aA[GROUP], aB[GROUP];
+    uint32_t wA[GROUP][NMAT], wB[GROUP][NMAT];
+    uint32_t sA[GROUP][NMAT], sB[GROUP][NMAT];
+    auto issue = [&](u32x4 (&a)[GROUP], uint32_t (&w)[GROUP][NMAT], uint32_t (&sc)[GROUP][NMAT],
+                     uint32_t g) __attribute__((always_inline)) {
+        // steps past the last one re-read the last step (loads are never
+        // branched around; those steps are skipped in run_group)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) acc[m][i][j] = (float4v){0.f, 0.f, 0.f, 0.f};
-
-    // Loader roles: A: thread -> (row tid/4, 16 halfs at (tid%4)*16);
-    // W: thread -> (row tid/4, 16 columns at (tid%4)*16).
-    const int lr = tid >> 2, lc = (tid & 3) * 16;
-
-    for (uint32_t k0 = 0; k0 < K; k0 += BK) {
-        {
-            const uint32_t p = p0 + lr;
-            uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
-            if (p < P) {
-                const uint4 *src = (const uint4 *)(A + (size_t)p * K + k0 + lc);
-                v0 = src[0];
-                v1 = src[1];
+        for (int t = 0; t < GROUP; ++t) a[t] = *(const u32x4 *)(arow + min(g * GROUP + t, nk - 1) * BK);
+#pragma unroll
+        for (int t = 0; t < GROUP; ++t) {
+            const uint32_t col = min(g * GROUP + t, nk - 1) * BK + lc;
+            w[t][0] = wrow0[col / 32];
+            sc[t][0] = srow0[col >> gs_log2];
+            if constexpr (NMAT == 2) {
+                w[t][1] = wrow1[col / 32];
+                sc[t][1] = srow1[col >> gs_log2];
             }
-            uint4 *dst = (uint4 *)(As + lr * LDS_STRIDE + lc);
-            dst[0] = v0;
-            dst[1] = v1;
         }
+    };
+    // Stage step ks (registers -> LDS buffer ks & 1): the A piece swizzled,
+    // the byte of W bits expanded to +-s through the sign table.
+    auto stage = [&](const u32x4 &a, const uint32_t (&w)[NMAT], const uint32_t (&sc)[NMAT],
+                     uint32_t ks) __attribute__((always_inline)) {
+        const int buf = ks & 1;
+        ((u32x4 *)(As[buf] + lr * BK))[lq ^ (lr & 7)] = a;
 #pragma unroll
         for (int m = 0; m < NMAT; ++m) {
-            const uint32_t *codes = m == 0 ? codes0 : codes1;
-            const uint16_t *scales = m == 0 ? scales0 : scales1;
-            const uint32_t n = n0 + lr;
-            const uint32_t col = k0 + lc;
-            const uint32_t w = codes[(size_t)n * words_per_row + col / 32];
-            const uint32_t bits = (w >> (col & 31)) & 0xFFFFu;
-            const f16_t s = __builtin_bit_cast(f16_t, scales[(size_t)n * groups_per_row + col / gs]);
-            half8 h0, h1;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                h0[i] = ((bits >> i) & 1) ? s : (f16_t)-s;
-                h1[i] = ((bits >> (8 + i)) & 1) ? s : (f16_t)-s;
-            }
-            half8 *dst = (half8 *)(Bs[m] + lr * LDS_STRIDE + lc);
-            dst[0] = h0;
-            dst[1] = h1;
+            const uint32_t byte = (w[m] >> (lc & 31)) & 0xFFu;
+            const uint32_t s2 = sc[m] | (sc[m] << 16);
+            *(u32x4 *)(Bs[buf][m] + lr * LDS_STRIDE + lc) = sgn[byte] ^ s2;
         }
-        __syncthreads();
-
+    };
+    auto compute = [&](uint32_t ks) __attribute__((always_inline)) {
+        const int buf = ks & 1;
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 32) {
-            const int kofs = kk + 8 * (lane >> 4);
+            const int piece = kk / 8 + (lane >> 4);
             half8 af[2];
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-                af[i] = *(const half8 *)(As + (wm * 32 + i * 16 + (lane & 15)) * LDS_STRIDE + kofs);
+            for (int i = 0; i < 2; ++i) {
+                const int r = wm * 32 + i * 16 + (lane & 15);
+                af[i] = *(const half8 *)(As[buf] + r * BK + 8 * (piece ^ (r & 7)));
+            }
 #pragma unroll
             for (int m = 0; m < NMAT; ++m) {
+                const half8 bf = *(const half8 *)(Bs[buf][m] + (wn * 16 + (lane & 15)) * LDS_STRIDE +
+                                                  kk + 8 * (lane >> 4));
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const half8 bf =
-                        *(const half8 *)(Bs[m] + (wn * 32 + j * 16 + (lane & 15)) * LDS_STRIDE + kofs);
-#pragma unroll
-                    for (int i = 0; i < 2; ++i)
-                        acc[m][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf, acc[m][i][j], 0, 0, 0);
-                }
+                for (int i = 0; i < 2; ++i)
+                    acc[m][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf, acc[m][i], 0, 0, 0);
             }
         }
-        __syncthreads();
+    };
+    // Steps 4g..4g+3 of group g (registers `cur`): each iteration stages
+    // the NEXT step (from `cur`, or for the last one from `nxt`, the next
+    // group's set) while the MFMAs of the current step run, then one
+    // barrier.  The buffer a step stages into was last read two steps
+    // earlier, before the previous barrier.  Steps past the end are skipped
+    // (block-uniform).
+    auto run_group = [&](const u32x4 (&ca)[GROUP], const uint32_t (&cw)[GROUP][NMAT],
+                         const uint32_t (&cs)[GROUP][NMAT], const u32x4 (&na)[GROUP],
+                         const uint32_t (&nw)[GROUP][NMAT], const uint32_t (&ns)[GROUP][NMAT],
+                         uint32_t g) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < GROUP; ++t) {
+            const uint32_t ks = g * GROUP + t;
+            if (ks >= nk) break;   // block-uniform
+            if (ks + 1 < nk) {
+                if (t + 1 < GROUP) stage(ca[t + 1], cw[t + 1], cs[t + 1], ks + 1);
+                else stage(na[0], nw[0], ns[0], ks + 1);
+            }
+            compute(ks);
+            step_barrier();
+        }
+    };
+
+    // Group pipeline: the loads of group g+1 are issued before group g's
+    // steps run, so they have a group's worth of compute to arrive.  Two
+    // groups per pass, the register sets in turn.
+    static_assert(GROUP % 2 == 0, "step parity across groups");
+    issue(aA, wA, sA, 0);
+    step_barrier();   // the sign table
+    stage(aA[0], wA[0], sA[0], 0);
+    step_barrier();
+    for (uint32_t g = 0; g < ngroups; g += 2) {
+        issue(aB, wB, sB, g + 1);
+        run_group(aA, wA, sA, aB, wB, sB, g);
+        issue(aA, wA, sA, g + 2);
+        run_group(aB, wB, sB, aA, wA, sA, g + 1);
     }
 
     // D layout: lane holds rows 4*(lane/16)+r, column lane%16 of each 16x16 tile.
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t p = p0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
-                const uint32_t n = n0 + wn * 32 + j * 16 + (lane & 15);
-                if (p >= P) continue;
-                const size_t o = (size_t)p * M + n;
-                const float c = acc[0][i][j][r];
-                if constexpr (MODE == NNZ_GEMM_STORE_F16) ((f16_t *)out)[o] = (f16_t)c;
-                else if constexpr (MODE == NNZ_GEMM_STORE_F32) ((float *)out)[o] = c;
-                else if constexpr (MODE == NNZ_GEMM_RESADD) ((float *)out)[o] += c;
-                else {
-                    const float u = acc[NMAT - 1][i][j][r];
-                    ((f16_t *)out)[o] = (f16_t)(c / (1.f + expf(-c)) * u);
-                }
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t p = p0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
+            const uint32_t n = n0 + wn * 16 + (lane & 15);
+            if (p >= P) continue;
+            const size_t o = (size_t)p * M + n;
+            const float c = acc[0][i][r];
+            if constexpr (MODE == NNZ_GEMM_STORE_F16) ((f16_t *)out)[o] = (f16_t)c;
+            else if constexpr (MODE == NNZ_GEMM_STORE_F32) ((float *)out)[o] = c;
+            else if constexpr (MODE == NNZ_GEMM_RESADD) ((float *)out)[o] += c;
+            else {
+                const float u = acc[NMAT - 1][i][r];
+                ((f16_t *)out)[o] = (f16_t)(c / (1.f + expf(-c)) * u);
             }
+        }
 }
 
 }  // namespace
@@ -139,8 +213,9 @@ int nnz_gemm_launch(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, 
                 "dequant_gemm: Q1 weights only");
     NNZ_REQUIRE(ctx, (uint64_t)wa->packed_count == (uint64_t)d.M * d.K && wa->group_size == d.group_size,
                 NNZ_EINVAL, "dequant_gemm: descriptor does not match dims");
-    NNZ_REQUIRE(ctx, d.M % BN == 0 && d.K % BK == 0 && d.group_size % BK == 0 && d.K % d.group_size == 0,
-                NNZ_EUNSUPPORTED, "dequant_gemm: need M%%64 == K%%64 == gs%%64 == 0");
+    NNZ_REQUIRE(ctx, d.M % BN == 0 && d.K % BK == 0 && d.group_size % BK == 0 &&
+                         d.K % d.group_size == 0,
+                NNZ_EUNSUPPORTED, "dequant_gemm: need M %% 64 == 0, K %% 64 == 0, group size %% 64 == 0");
     NNZ_REQUIRE(ctx, ((uintptr_t)a & 15) == 0, NNZ_EINVAL, "dequant_gemm: A must be 16-byte aligned");
     const bool pair = mode == NNZ_GEMM_SILU_PAIR;
     if (pair) {
@@ -149,23 +224,26 @@ int nnz_gemm_launch(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, 
                              wb->group_size == d.group_size,
                     NNZ_EINVAL, "dequant_gemm: bad second weight for SILU_PAIR");
     }
+    NNZ_REQUIRE(ctx, (d.group_size & (d.group_size - 1)) == 0, NNZ_EUNSUPPORTED,
+                "dequant_gemm: group size must be a power of two");
+    const uint32_t gl = (uint32_t)__builtin_ctz(d.group_size);
     dim3 grid(d.M / BN, ceil_div(P, BM));
     const f16_t *A = (const f16_t *)a;
     const uint32_t *c0 = (const uint32_t *)wa->codes;
     const uint16_t *s0 = (const uint16_t *)wa->scales;
     switch (mode) {
     case NNZ_GEMM_STORE_F16:
-        dq_gemm_kernel<NNZ_GEMM_STORE_F16, 1><<<grid, 256, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, d.group_size);
+        dq_gemm_kernel<NNZ_GEMM_STORE_F16, 1><<<grid, 512, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl);
         break;
     case NNZ_GEMM_STORE_F32:
-        dq_gemm_kernel<NNZ_GEMM_STORE_F32, 1><<<grid, 256, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, d.group_size);
+        dq_gemm_kernel<NNZ_GEMM_STORE_F32, 1><<<grid, 512, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl);
         break;
     case NNZ_GEMM_RESADD:
-        dq_gemm_kernel<NNZ_GEMM_RESADD, 1><<<grid, 256, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, d.group_size);
+        dq_gemm_kernel<NNZ_GEMM_RESADD, 1><<<grid, 512, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl);
         break;
     case NNZ_GEMM_SILU_PAIR:
-        dq_gemm_kernel<NNZ_GEMM_SILU_PAIR, 2><<<grid, 256, 0, ctx->stream>>>(
-            A, c0, s0, (const uint32_t *)wb->codes, (const uint16_t *)wb->scales, out, P, d.M, d.K, d.group_size);
+        dq_gemm_kernel<NNZ_GEMM_SILU_PAIR, 2><<<grid, 512, 0, ctx->stream>>>(
+            A, c0, s0, (const uint32_t *)wb->codes, (const uint16_t *)wb->scales, out, P, d.M, d.K, gl);
         break;
     default:
         return nnz_fail(ctx, NNZ_EINVAL, "dequant_gemm: unknown mode %d", mode);

@@ -75,6 +75,13 @@ class DecoderModel:
         ``embed_on_device`` the bf16 embedding table is generated on the GPU
         from the same seeded stream instead of being uploaded."""
         cfg = self.cfg
+        for l, layer in enumerate(w.layers):
+            for name in PROJS:
+                if layer[name].bits != 1:
+                    raise ValueError(f"layer {l} {name}: this decoder holds 1-bit projections, "
+                                     f"got {layer[name].bits}-bit")
+        if len(w.layers) != cfg.num_layers:
+            raise ValueError(f"{len(w.layers)} layers given, config has {cfg.num_layers}")
         if cfg.embed_kind == L.EMBED_BF16:
             if embed_on_device:
                 ptr, nbytes = self.tensor(T_EMBED_CODES)
@@ -82,6 +89,11 @@ class DecoderModel:
                               S.SEED_MODEL_BASE + 0, 0.02)
             else:
                 self.upload(T_EMBED_CODES, 0, w.embed_bf16)
+        else:
+            if w.embed_q1 is None or w.embed_q1.bits != 1:
+                raise ValueError("config asks for a 1-bit embedding table")
+            self.upload(T_EMBED_CODES, 0, w.embed_q1.codes)
+            self.upload(T_EMBED_SCALES, 0, w.embed_q1.scales)
         if cfg.lm_head_kind == L.LMHEAD_Q1:
             self.upload(T_LM_CODES, 0, w.lm_head.codes)
             self.upload(T_LM_SCALES, 0, w.lm_head.scales)
@@ -96,6 +108,26 @@ class DecoderModel:
             self.upload(T_Q_NORM, l, layer["q_norm"])
             self.upload(T_K_NORM, l, layer["k_norm"])
         self.dev.sync()
+
+    def load_weights(self, paths, quant: str = "q1", tie_word_embeddings: bool = True,
+                     strict: bool = True) -> None:
+        """loadWeights(file_paths) (model.zig:196-242): read an MLX-format
+        checkpoint (shard files or a model directory) straight from the
+        mapped shards into device memory."""
+        from contextlib import ExitStack
+        import os
+        from . import checkpoint as ck
+        from .safetensors import SafetensorsFile
+        cfg = self.cfg
+        if cfg.embed_kind != L.EMBED_Q1 or cfg.lm_head_kind != L.LMHEAD_Q1:
+            raise ValueError("checkpoint models need embed_kind EMBED_Q1, lm_head_kind LMHEAD_Q1")
+        if isinstance(paths, (str, os.PathLike)):
+            paths = ck.find_shards(paths) if os.path.isdir(paths) else [paths]
+        with ExitStack() as stack:
+            files = [stack.enter_context(SafetensorsFile.open(p)) for p in paths]
+            w = ck.read_weights(files, cfg, quant, tie_word_embeddings, strict)
+            self.load(w)
+            del w
 
     def forward_decode(self, token: int, position: int) -> np.ndarray:
         self._mcall("nnz_model_forward_decode", token, position)

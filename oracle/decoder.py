@@ -46,6 +46,12 @@ class OracleDecoder:
     def embed_rows(self, ids) -> np.ndarray:
         cfg = self.cfg
         ids = [int(i) for i in ids]
+        e = self.w.embed_q1
+        if e is not None:
+            # embedding_lookup (transformer.metal:428-481): +-s of row `id`
+            return O.embed_q1(ids, e.codes.view(np.uint8).reshape(-1),
+                              e.scales.view(np.float16).reshape(-1), cfg.hidden_size,
+                              e.group_size)
         if self.w.embed_bf16 is not None:
             return S.bf16_bits_to_f32(self.w.embed_bf16[ids]).astype(np.float64)
         out = []

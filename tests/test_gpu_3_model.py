@@ -141,3 +141,72 @@ def test_config5_golden_tokens(mdev):
     first_bad = int(np.argmax(toks != ref)) if np.any(toks != ref) else -1
     assert first_bad == -1, (f"first mismatch at step {first_bad}: got {toks[first_bad]}, "
                             f"want {ref[first_bad]} (oracle margin {gold['margins'][first_bad]:.3e})")
+
+
+# -- MLX checkpoint -> device (loadWeights, model.zig:196-242) ------------------
+
+CKPT_CFG = cf.DecoderConfig(vocab_size=500, hidden_size=256, intermediate_size=512, num_layers=2,
+                            num_query_heads=4, num_kv_heads=2, head_dim=64,
+                            max_context_length=256, max_prefill_length=64, group_size=128,
+                            rope_theta=10000.0, embed_kind=0, lm_head_kind=0)
+
+
+@pytest.mark.parametrize("tie", [True, False])
+def test_checkpoint_model_matches_oracle(mdev, tmp_path, tie):
+    """Shards written in MLX form, loaded straight from the mapped files into
+    device memory: 1-bit embedding table, 1-bit LM head (tied to the table or
+    its own matrix), ragged vocabulary (500).  Prefill logits, decode logits
+    and 24 greedy tokens against the oracle run on the host-side load of the
+    same shards."""
+    from nnzap_amd import checkpoint as ck
+    from ckpt_util import write_mlx_checkpoint
+    cfg = CKPT_CFG
+    write_mlx_checkpoint(tmp_path, cfg, bits=1, tie=tie)
+    w = ck.load_checkpoint(tmp_path, cfg, tie_word_embeddings=tie)
+    m = DecoderModel(mdev, cfg)
+    try:
+        m.load_weights(tmp_path, tie_word_embeddings=tie)
+        ids = cf.prompt_ids(cfg, 24)
+        ref = OracleDecoder(w)
+        ref_logits = ref.forward(list(ids), 0)[-1]
+        assert_close_normwise(m.prefill(ids, 0), ref_logits, what="checkpoint prefill")
+        r = ref.forward([499], len(ids))[0]
+        assert_close_normwise(m.forward_decode(499, len(ids)), r, what="checkpoint decode")
+        toks, margins, _ = m.generate(ids, 24)
+        ref_toks, ref_margins = OracleDecoder(w).generate(ids, 24)
+        assert np.array_equal(toks, ref_toks), (toks, ref_toks, ref_margins)
+        assert np.max(np.abs(margins - ref_margins)) < 2e-3
+    finally:
+        m.close()
+
+
+# nnmetal/examples/bonsai_golden.zig:30-43: PrismML Bonsai-1.7B (1-bit MLX),
+# prompt "The capital of France is" in the chat template, greedy.
+BONSAI_GOLDEN_PROMPT = "The capital of France is"
+BONSAI_GOLDEN_TOKENS = [151667, 198, 151668, 271, 785, 6722, 315, 9625, 374, 12095, 13]
+
+
+@pytest.mark.skipif(not os.environ.get("NNZAP_BONSAI_DIR"),
+                    reason="set NNZAP_BONSAI_DIR to a Bonsai-1.7B (1-bit MLX) model directory")
+def test_bonsai_golden_tokens(mdev):
+    """The reference's golden run on the real checkpoint (needs the weights,
+    config.json and tokenizer.json in NNZAP_BONSAI_DIR)."""
+    from tokenizers import Tokenizer
+    from nnzap_amd import checkpoint as ck
+    d = os.environ["NNZAP_BONSAI_DIR"]
+    cfg, quant, tie = ck.config_from_hf(d, max_context_length=1024)
+    if quant != ck.QUANT_Q1:
+        pytest.skip("the decoder model holds 1-bit projections")
+    tok = Tokenizer.from_file(os.path.join(d, "tokenizer.json"))
+    enc = lambda s: tok.encode(s, add_special_tokens=False).ids
+    im_start, im_end = tok.token_to_id("<|im_start|>"), tok.token_to_id("<|im_end|>")
+    # applyChatTemplate (nnmetal/src/tokenizer.zig:330-367), piece by piece
+    ids = ([im_start] + enc("user\n") + enc(BONSAI_GOLDEN_PROMPT) + [im_end] + enc("\n")
+           + [im_start] + enc("assistant\n"))
+    m = DecoderModel(mdev, cfg)
+    try:
+        m.load_weights(d, quant, tie)
+        toks, _, _ = m.generate(np.array(ids, dtype=np.uint32), len(BONSAI_GOLDEN_TOKENS))
+    finally:
+        m.close()
+    assert list(map(int, toks)) == BONSAI_GOLDEN_TOKENS

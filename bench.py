@@ -360,6 +360,25 @@ def _kernel_cases():
             return us, nbytes, None, flops
         return run
 
+    def sample(T, k, p, peaked=False):
+        # device sampling over the 151,936 logits the LM head just wrote
+        # (sampleToken on device: temperature, top-k, top-p, one draw);
+        # logits N(0, 2.5^2), "peaked": 8 tokens raised by 12
+        def run(dev, n):
+            g = np.random.default_rng(3)
+            x = g.normal(0.0, 2.5, V).astype(np.float32)
+            if peaked:
+                x[g.integers(0, V, 8)] += 12.0
+            logits = torch.from_numpy(x).cuda()
+            ws = torch.empty(ops.sample_workspace_bytes(V), dtype=torch.uint8, device="cuda")
+            rng = torch.zeros(4, dtype=torch.int64, device="cuda")
+            out = torch.zeros(1, dtype=torch.int32, device="cuda")
+            ops.rng_seed(dev, 42, rng)
+            us = time_launches(dev, lambda i: ops.dispatch_sample(dev, logits, out, rng, ws, T, k, p),
+                               max(16, n // 8))
+            return us, V * 4, None
+        return run
+
     def copy_calib(dev, n):
         # a plain device copy of known size: the scale for FETCH/WRITE_SIZE
         a = torch.ones(64 << 20, dtype=f32, device="cuda")
@@ -388,6 +407,10 @@ def _kernel_cases():
         "prefill_gemm_o_resadd": prefill_gemm(H, QD, L.GEMM_RESADD),
         "prefill_gemm_gate_up_silu": prefill_gemm(I, H, L.GEMM_SILU_PAIR, pair=True),
         "prefill_gemm_down_resadd": prefill_gemm(H, I, L.GEMM_RESADD),
+        "sample_topk40_topp095": sample(0.8, 40, 0.95),
+        "sample_topp090": sample(1.0, 0, 0.9),
+        "sample_topp090_peaked": sample(1.0, 0, 0.9, peaked=True),
+        "sample_temperature_only": sample(0.7, 0, 1.0),
     }
 
 

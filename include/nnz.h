@@ -388,6 +388,33 @@ int nnz_dispatch_residual_add(nnz_ctx *ctx, float *residual, const float *additi
 int nnz_dispatch_argmax(nnz_ctx *ctx, const float *logits, uint32_t count, uint32_t *out_index,
                         float *out_value);
 
+/* ---- sampling (transformer.zig:3692-3908) --------------------------------
+ * SamplingParams (transformer.zig:3652-3657): temperature 0 = greedy argmax;
+ * top_k 0 = off; top_p >= 1 = off; seed of the random stream. */
+typedef struct {
+    float temperature;
+    uint32_t top_k;
+    float top_p;
+    uint32_t reserved; /* 0 */
+    uint64_t seed;
+} nnz_sampling_params;
+
+/* Workspace bytes nnz_dispatch_sample needs for `count` logits. */
+size_t nnz_sample_workspace_bytes(uint32_t count);
+/* std.Random.DefaultPrng.init(seed) (generate, transformer.zig:3969): write
+ * the 4-word xoshiro256++ state expanded by SplitMix64 to device memory
+ * d_state[4] (synchronous). */
+int nnz_rng_seed(nnz_ctx *ctx, uint64_t seed, uint64_t *d_state);
+/* sampleToken (transformer.zig:3860-3894) on device: temperature, top-k,
+ * top-p, softmax, inverse-CDF draw with r = the next float of d_rng (the
+ * state advances on device).  logits (device f32[count]) are not modified.
+ * out_index: device uint32; out_prob (optional): device f32, the chosen
+ * token's final probability.  temperature 0 is argmax (no rng, no
+ * workspace needed).  count <= 4,194,304. */
+int nnz_dispatch_sample(nnz_ctx *ctx, const float *logits, uint32_t count,
+                        const nnz_sampling_params *params, uint64_t *d_rng, void *workspace,
+                        size_t workspace_bytes, uint32_t *out_index, float *out_prob);
+
 /* ---- decoder model: forwardDecode / generate (transformer.zig:2389-4135) -- */
 
 typedef struct {
@@ -448,13 +475,16 @@ int nnz_model_forward_decode(nnz_model *m, uint32_t token_id, uint32_t position)
  * start..start+n-1 via the dequant-GEMM; leaves the last token's logits in
  * NNZ_T_LOGITS.  `tokens_host` is a host array. */
 int nnz_model_prefill(nnz_model *m, const uint32_t *tokens_host, uint32_t n, uint32_t start);
-/* Greedy generate (transformer.zig:3942 with temperature 0): prefill the
- * prompt, then `n_new` decode steps; each step is one replay of a captured
- * hipGraph and an on-device argmax.  Writes n_new token ids (host) and, if
- * non-NULL, the per-step top-2 logit margin and per-step wall ms. */
+/* generate (transformer.zig:3942): prefill the prompt, then up to `n_new`
+ * decode steps; each step is one replay of a captured hipGraph that picks
+ * the next token on the device (argmax, or the sampler set by
+ * nnz_model_set_sampling).  Stops early at a stop token (nnz_model_set_eos).
+ * Writes the emitted token ids (host), their number to *out_count (optional)
+ * and, if non-NULL, per token the top-2 logit margin (greedy) or the
+ * sampled token's probability (sampling), and per-step wall ms. */
 int nnz_model_generate(nnz_model *m, const uint32_t *prompt_host, uint32_t n_prompt,
                        uint32_t n_new, uint32_t *out_tokens, float *out_margins,
-                       float *out_step_ms, int use_graph);
+                       float *out_step_ms, int use_graph, uint32_t *out_count);
 /* The same loop split for streaming callers and benchmarks (decodeOneToken,
  * transformer.zig:4072, without the per-token host sync):
  *   nnz_model_decode_begin: prefill the prompt, take the greedy first token,
@@ -468,6 +498,18 @@ int nnz_model_decode_begin(nnz_model *m, const uint32_t *prompt_host, uint32_t n
 int nnz_model_decode_steps(nnz_model *m, uint32_t n);
 int nnz_model_decode_read(nnz_model *m, uint32_t n, uint32_t *out_tokens, float *out_margins);
 int nnz_model_decode_end(nnz_model *m);
+/* Sampling of the decode loop (GenerateOpts.params, transformer.zig:3930):
+ * applies from the next generate / decode_begin, which re-seeds the random
+ * stream with params->seed.  Default: greedy. */
+int nnz_model_set_sampling(nnz_model *m, const nnz_sampling_params *params);
+/* Stop tokens (GenerateOpts.eos_ids; isEosToken, transformer.zig:4126): a
+ * sampled stop token ends the stream and is not emitted.  n <= 8; n = 0
+ * clears them. */
+int nnz_model_set_eos(nnz_model *m, const uint32_t *ids, uint32_t n);
+/* Tokens emitted so far by the current / last decode stream
+ * (GenerateResult.tokens_generated) and whether a stop token ended it;
+ * synchronises the stream. */
+int nnz_model_decode_status(nnz_model *m, uint32_t *emitted, int *stopped);
 
 /* ---- synthetic data (no reference counterpart) ---------------------------
  * Fill out[0..n) with bf16(scale * N(0,1)) from the counter-based

@@ -75,6 +75,12 @@ class QWeightDesc(C.Structure):
                 ("group_size", u32), ("bits", u32), ("scale_dtype", u32)]
 
 
+class SamplingParams(C.Structure):
+    """nnz_sampling_params (SamplingParams, transformer.zig:3652-3657)."""
+    _fields_ = [("temperature", f32), ("top_k", u32), ("top_p", f32), ("reserved", u32),
+                ("seed", C.c_uint64)]
+
+
 class ModelConfig(C.Structure):
     _fields_ = [("vocab_size", u32), ("hidden_size", u32), ("intermediate_size", u32),
                 ("num_layers", u32), ("num_query_heads", u32), ("num_kv_heads", u32),
@@ -159,17 +165,23 @@ PROTOS = {
     "nnz_dispatch_embedding_lookup_bf16": (C.c_int, [vp, vp, vp, vp, EmbedDims]),
     "nnz_dispatch_residual_add": (C.c_int, [vp, vp, vp, u32]),
     "nnz_dispatch_argmax": (C.c_int, [vp, vp, u32, vp, vp]),
+    "nnz_sample_workspace_bytes": (sz, [u32]),
+    "nnz_rng_seed": (C.c_int, [vp, C.c_uint64, vp]),
+    "nnz_dispatch_sample": (C.c_int, [vp, vp, u32, vp, vp, vp, sz, vp, vp]),
     # model
     "nnz_model_create": (C.c_int, [vp, P(ModelConfig), P(vp)]),
     "nnz_model_destroy": (C.c_int, [vp]),
     "nnz_model_tensor": (C.c_int, [vp, C.c_int, u32, P(vp), P(sz)]),
     "nnz_model_forward_decode": (C.c_int, [vp, u32, u32]),
     "nnz_model_prefill": (C.c_int, [vp, vp, u32, u32]),
-    "nnz_model_generate": (C.c_int, [vp, vp, u32, u32, vp, vp, vp, C.c_int]),
+    "nnz_model_generate": (C.c_int, [vp, vp, u32, u32, vp, vp, vp, C.c_int, vp]),
     "nnz_model_decode_begin": (C.c_int, [vp, vp, u32, u32]),
     "nnz_model_decode_steps": (C.c_int, [vp, u32]),
     "nnz_model_decode_read": (C.c_int, [vp, u32, vp, vp]),
     "nnz_model_decode_end": (C.c_int, [vp]),
+    "nnz_model_set_sampling": (C.c_int, [vp, vp]),
+    "nnz_model_set_eos": (C.c_int, [vp, vp, u32]),
+    "nnz_model_decode_status": (C.c_int, [vp, vp, vp]),
     "nnz_synth_normal_bf16": (C.c_int, [vp, vp, C.c_uint64, C.c_uint64, C.c_double]),
 }
 

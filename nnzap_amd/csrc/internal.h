@@ -54,3 +54,48 @@ int nnz_qmv_norm_f32out_launch(nnz_ctx *ctx, const nnz_qweight *w, const float *
                                const float *norm_w, float *out, nnz_qmv_dims d);
 int nnz_gemm_launch(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, const void *a,
                     uint32_t P, void *out, int mode, const nnz_qmv_dims &d);
+
+// Decode state block of the model's device-resident loop: {token, position,
+// sequence length, emitted count, done}.
+enum { NNZ_ST_TOKEN = 0, NNZ_ST_POS = 1, NNZ_ST_SEQ = 2, NNZ_ST_STEP = 3, NNZ_ST_DONE = 4 };
+constexpr uint32_t NNZ_MAX_EOS = 8;
+
+// Where a picked token goes: the state block, the emitted-token and
+// per-token value arrays (capacity `cap`) and the stop tokens.
+struct NnzPick {
+    uint32_t *state = nullptr;
+    uint32_t *tokens = nullptr;
+    float *values = nullptr;
+    uint32_t cap = 0;
+    uint32_t n_eos = 0;
+    uint32_t eos[NNZ_MAX_EOS] = {};
+};
+
+// Record token `tok` (one thread): an EOS id ends the stream without being
+// emitted, and after that nothing is emitted or advanced (generate,
+// transformer.zig:3992, isEosToken :4126).
+__device__ __forceinline__ void nnz_pick_advance(const NnzPick &p, uint32_t tok, float value) {
+    uint32_t *st = p.state;
+    if (st[NNZ_ST_DONE]) return;
+    for (uint32_t i = 0; i < p.n_eos; ++i)
+        if (tok == p.eos[i]) {
+            st[NNZ_ST_DONE] = 1;
+            return;
+        }
+    const uint32_t step = st[NNZ_ST_STEP];
+    if (step < p.cap) {
+        p.tokens[step] = tok;
+        p.values[step] = value;
+    }
+    st[NNZ_ST_TOKEN] = tok;
+    st[NNZ_ST_POS] += 1;
+    st[NNZ_ST_SEQ] += 1;
+    st[NNZ_ST_STEP] = step + 1;
+}
+
+// Device sampling (sample.hip).
+void nnz_rng_seed_words(uint64_t seed, uint64_t out[4]);
+size_t nnz_sample_ws_bytes(uint32_t n);
+int nnz_sample_launch(nnz_ctx *ctx, const float *logits, uint32_t n, const nnz_sampling_params &p,
+                      uint64_t *rng, void *ws, uint32_t *out_index, float *out_prob,
+                      const NnzPick *pick);

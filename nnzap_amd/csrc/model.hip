@@ -40,8 +40,10 @@ int nnz_dispatch_qmv_f16in(nnz_ctx *, const nnz_qweight *, const void *, float *
 
 namespace {
 
-// Device state block: token id, position, visible sequence length, step.
-enum { ST_TOKEN = 0, ST_POS = 1, ST_SEQ = 2, ST_STEP = 3 };
+// Device state block: token id, position, visible sequence length, emitted
+// count, stopped flag.
+enum { ST_TOKEN = NNZ_ST_TOKEN, ST_POS = NNZ_ST_POS, ST_SEQ = NNZ_ST_SEQ, ST_STEP = NNZ_ST_STEP,
+       ST_DONE = NNZ_ST_DONE, ST_WORDS = 5 };
 
 __global__ void embed_state_q1_kernel(const uint32_t *state, const uint8_t *bits,
                                       const uint16_t *scales, float *out, uint32_t hidden,
@@ -177,25 +179,12 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float *x, uin
     if (threadIdx.x == 0) part[blockIdx.x] = r;
 }
 
-__global__ __launch_bounds__(256) void argmax_final_advance_kernel(const Top2 *part, uint32_t *state,
-                                                                   uint32_t *tokens, float *margins,
-                                                                   uint32_t cap) {
+__global__ __launch_bounds__(256) void argmax_final_advance_kernel(const Top2 *part, NnzPick pick) {
     __shared__ Top2 sh[256];
     Top2 t{-INFINITY, -INFINITY, 0xFFFFFFFFu};
     for (uint32_t i = threadIdx.x; i < (uint32_t)ARGMAX_BLOCKS; i += 256) t = top2_merge(t, part[i]);
     const Top2 r = block_top2_256(t, sh);
-    if (threadIdx.x == 0) {
-        const uint32_t tok = r.idx == 0xFFFFFFFFu ? 0u : r.idx;
-        const uint32_t step = state[ST_STEP];
-        if (step < cap) {
-            tokens[step] = tok;
-            margins[step] = r.best - r.second;
-        }
-        state[ST_TOKEN] = tok;
-        state[ST_POS] += 1;
-        state[ST_SEQ] += 1;
-        state[ST_STEP] = step + 1;
-    }
+    if (threadIdx.x == 0) nnz_pick_advance(pick, r.idx == 0xFFFFFFFFu ? 0u : r.idx, r.best - r.second);
 }
 
 struct Proj {
@@ -231,6 +220,11 @@ struct nnz_model {
     uint32_t *tokens_out = nullptr;
     float *margins_out = nullptr;
     uint32_t out_cap = 0;
+    // token choice of the decode loop: greedy unless sp.temperature != 0
+    nnz_sampling_params sp{};
+    uint64_t *rng = nullptr;        // xoshiro256 state [4]
+    void *sample_ws = nullptr;
+    uint32_t n_eos = 0, eos[NNZ_MAX_EOS] = {};
     // prefill activations (allocated on first use, sized for max_prefill_length)
     float *p_res = nullptr, *p_qf = nullptr, *p_part_o = nullptr, *p_part_ml = nullptr;
     size_t p_part_floats = 0;
@@ -371,13 +365,28 @@ int enqueue_decode_step(nnz_model *m, uint32_t max_seq) {
     return lm_head(m, m->xn, m->logits);
 }
 
-// Greedy sampling of the logits into the state block (two passes).
+NnzPick pick_of(const nnz_model *m) {
+    NnzPick p;
+    p.state = m->state;
+    p.tokens = m->tokens_out;
+    p.values = m->margins_out;
+    p.cap = m->out_cap;
+    p.n_eos = m->n_eos;
+    for (uint32_t i = 0; i < m->n_eos; ++i) p.eos[i] = m->eos[i];
+    return p;
+}
+
+// Pick the next token from the logits into the state block: argmax (two
+// passes) or the sampler (sampleToken, transformer.zig:3860-3894).
 int enqueue_argmax_advance(nnz_model *m) {
+    const NnzPick pick = pick_of(m);
+    if (m->sp.temperature != 0.f)
+        return nnz_sample_launch(m->ctx, m->logits, m->c.vocab_size, m->sp, m->rng, m->sample_ws,
+                                 nullptr, nullptr, &pick);
     argmax_partial_kernel<<<ARGMAX_BLOCKS, 256, 0, m->ctx->stream>>>(m->logits, m->c.vocab_size,
                                                                      m->top2);
     NNZ_LAUNCHED(m->ctx);
-    argmax_final_advance_kernel<<<1, 256, 0, m->ctx->stream>>>(m->top2, m->state, m->tokens_out,
-                                                               m->margins_out, m->out_cap);
+    argmax_final_advance_kernel<<<1, 256, 0, m->ctx->stream>>>(m->top2, pick);
     NNZ_LAUNCHED(m->ctx);
     return NNZ_OK;
 }
@@ -499,6 +508,8 @@ int nnz_model_create(nnz_ctx *ctx, const nnz_model_config *cfg, nnz_model **out)
         m->part_ml = parts + (size_t)c.num_query_heads * m->part_chunks * c.head_dim;
         MALLOC(m->top2, (size_t)ARGMAX_BLOCKS * sizeof(Top2));
         MALLOC(m->state, 64);
+        MALLOC(m->rng, 32);
+        MALLOC(m->sample_ws, nnz_sample_ws_bytes(c.vocab_size));
         MALLOC(m->rope_inv, (size_t)c.head_dim / 2 * 4);
         RC(nnz_rope_table_launch(ctx, m->rope_inv, c.head_dim, c.rope_theta));
         m->out_cap = c.max_context_length + 1;
@@ -583,7 +594,7 @@ int nnz_model_forward_decode(nnz_model *m, uint32_t token_id, uint32_t position)
                 "forward_decode: position %u >= max_context_length", position);
     NNZ_REQUIRE(ctx, token_id < m->c.vocab_size, NNZ_EINVAL, "forward_decode: token id out of range");
     NNZ_REQUIRE(ctx, !ctx->capturing, NNZ_ESTATE, "forward_decode: use generate() for graphs");
-    const uint32_t st[4] = {token_id, position, position + 1, 0};
+    const uint32_t st[ST_WORDS] = {token_id, position, position + 1, 0, 0};
     NNZ_HIP(ctx, hipMemcpyAsync(m->state, st, sizeof(st), hipMemcpyHostToDevice, ctx->stream));
     NNZ_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return enqueue_decode_step(m, position + 1);
@@ -669,10 +680,15 @@ int begin_decode(nnz_model *m, const uint32_t *prompt, uint32_t n_prompt, uint32
         const uint32_t n = n_prompt - s < c.max_prefill_length ? n_prompt - s : c.max_prefill_length;
         RC(nnz_model_prefill(m, prompt + s, n, s));
     }
-    // state = (-, n_prompt - 1, n_prompt, 0); the advance kernel stores t0 and
-    // moves to (t0, n_prompt, n_prompt + 1, 1).
-    const uint32_t st[4] = {0, n_prompt - 1, n_prompt, 0};
+    // state = (-, n_prompt - 1, n_prompt, 0, 0); the advance kernel stores t0
+    // and moves to (t0, n_prompt, n_prompt + 1, 1, 0).
+    const uint32_t st[ST_WORDS] = {0, n_prompt - 1, n_prompt, 0, 0};
     NNZ_HIP(ctx, hipMemcpyAsync(m->state, st, sizeof(st), hipMemcpyHostToDevice, ctx->stream));
+    if (m->sp.temperature != 0.f) {  // generate: DefaultPrng.init(params.seed)
+        uint64_t rs[4];
+        nnz_rng_seed_words(m->sp.seed, rs);
+        NNZ_HIP(ctx, hipMemcpyAsync(m->rng, rs, sizeof(rs), hipMemcpyHostToDevice, ctx->stream));
+    }
     RC(enqueue_argmax_advance(m));
     *max_seq = n_prompt + max_new;
     uint32_t chunk, nch;
@@ -681,16 +697,16 @@ int begin_decode(nnz_model *m, const uint32_t *prompt, uint32_t n_prompt, uint32
     return NNZ_OK;
 }
 
-// One greedy decode step: forwardDecode of the state's token, then argmax
+// One decode step: forwardDecode of the state's token, then the token pick
 // and state advance.  Graph-capturable (no host data, no allocation).
-int greedy_step(nnz_model *m, uint32_t max_seq) {
+int pick_step(nnz_model *m, uint32_t max_seq) {
     RC(enqueue_decode_step(m, max_seq));
     return enqueue_argmax_advance(m);
 }
 
 int capture_step(nnz_model *m, uint32_t max_seq, nnz_graph **g) {
     RC(nnz_graph_begin(m->ctx));
-    const int brc = greedy_step(m, max_seq);
+    const int brc = pick_step(m, max_seq);
     const int erc = nnz_graph_end(m->ctx, g);
     return brc ? brc : erc;
 }
@@ -700,7 +716,8 @@ int capture_step(nnz_model *m, uint32_t max_seq, nnz_graph **g) {
 extern "C" {
 
 int nnz_model_generate(nnz_model *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t n_new,
-                       uint32_t *out_tokens, float *out_margins, float *out_step_ms, int use_graph) {
+                       uint32_t *out_tokens, float *out_margins, float *out_step_ms, int use_graph,
+                       uint32_t *out_count) {
     if (!m) return NNZ_EINVAL;
     nnz_ctx *ctx = m->ctx;
     NNZ_REQUIRE(ctx, out_tokens, NNZ_EINVAL, "generate: null output");
@@ -714,22 +731,72 @@ int nnz_model_generate(nnz_model *m, const uint32_t *prompt, uint32_t n_prompt, 
             if (!rc && hipEventCreate(&e) != hipSuccess) rc = NNZ_EHIP;
     }
     // The reference decodes every emitted token (transformer.zig:3982-4016):
-    // n_new forward passes for n_new output tokens.
+    // n_new forward passes for n_new output tokens.  With stop tokens the
+    // host looks at the state block every POLL steps and stops queueing
+    // once the stream has ended.
+    constexpr uint32_t POLL = 8;
     nnz_graph *g = nullptr;
     if (!rc && use_graph) rc = capture_step(m, max_seq, &g);
     if (!rc && out_step_ms && hipEventRecord(ev[0], ctx->stream) != hipSuccess) rc = NNZ_EHIP;
+    uint32_t done_steps = 0;
     for (uint32_t i = 0; i < n_new && !rc; ++i) {
-        rc = use_graph ? nnz_graph_replay(ctx, g) : greedy_step(m, max_seq);
+        if (m->n_eos && i % POLL == 0) {
+            uint32_t st[ST_WORDS];
+            rc = nnz_stream_sync(ctx, 600000);
+            if (!rc && hipMemcpy(st, m->state, sizeof(st), hipMemcpyDeviceToHost) != hipSuccess)
+                rc = NNZ_EHIP;
+            if (rc || st[ST_DONE]) break;
+        }
+        rc = use_graph ? nnz_graph_replay(ctx, g) : pick_step(m, max_seq);
         if (!rc && out_step_ms && hipEventRecord(ev[i + 1], ctx->stream) != hipSuccess) rc = NNZ_EHIP;
+        done_steps = i + 1;
     }
     if (!rc) rc = nnz_stream_sync(ctx, 600000);
     if (!rc && out_step_ms)
-        for (uint32_t i = 0; i < n_new; ++i) hipEventElapsedTime(&out_step_ms[i], ev[i], ev[i + 1]);
+        for (uint32_t i = 0; i < n_new; ++i)
+            if (i < done_steps) hipEventElapsedTime(&out_step_ms[i], ev[i], ev[i + 1]);
+            else out_step_ms[i] = 0.f;
     for (auto &e : ev)
         if (e) hipEventDestroy(e);
     if (g) nnz_graph_destroy(g);
     if (rc) return rc;
-    return nnz_model_decode_read(m, n_new, out_tokens, out_margins);
+    uint32_t emitted;
+    int stopped;
+    RC(nnz_model_decode_status(m, &emitted, &stopped));
+    if (emitted > n_new) emitted = n_new;
+    if (out_count) *out_count = emitted;
+    return nnz_model_decode_read(m, emitted, out_tokens, out_margins);
+}
+
+int nnz_model_set_sampling(nnz_model *m, const nnz_sampling_params *p) {
+    if (!m) return NNZ_EINVAL;
+    NNZ_REQUIRE(m->ctx, p, NNZ_EINVAL, "set_sampling: null params");
+    NNZ_REQUIRE(m->ctx, p->temperature >= 0.f && p->temperature <= 3.0e38f, NNZ_EINVAL,
+                "set_sampling: temperature must be >= 0");
+    NNZ_REQUIRE(m->ctx, !m->step_graph, NNZ_ESTATE, "set_sampling: a decode stream is active");
+    m->sp = *p;
+    return NNZ_OK;
+}
+
+int nnz_model_set_eos(nnz_model *m, const uint32_t *ids, uint32_t n) {
+    if (!m) return NNZ_EINVAL;
+    NNZ_REQUIRE(m->ctx, n <= NNZ_MAX_EOS && (n == 0 || ids), NNZ_EINVAL,
+                "set_eos: at most %u stop tokens", NNZ_MAX_EOS);
+    NNZ_REQUIRE(m->ctx, !m->step_graph, NNZ_ESTATE, "set_eos: a decode stream is active");
+    m->n_eos = n;
+    for (uint32_t i = 0; i < n; ++i) m->eos[i] = ids[i];
+    return NNZ_OK;
+}
+
+int nnz_model_decode_status(nnz_model *m, uint32_t *emitted, int *stopped) {
+    if (!m) return NNZ_EINVAL;
+    nnz_ctx *ctx = m->ctx;
+    RC(nnz_stream_sync(ctx, 600000));
+    uint32_t st[ST_WORDS];
+    NNZ_HIP(ctx, hipMemcpy(st, m->state, sizeof(st), hipMemcpyDeviceToHost));
+    if (emitted) *emitted = st[ST_STEP];
+    if (stopped) *stopped = (int)st[ST_DONE];
+    return NNZ_OK;
 }
 
 int nnz_model_decode_begin(nnz_model *m, const uint32_t *prompt, uint32_t n_prompt,

@@ -158,14 +158,38 @@ class DecoderModel:
     def decode_end(self) -> None:
         self._mcall("nnz_model_decode_end")
 
+    def set_sampling(self, temperature: float = 0.0, top_k: int = 0, top_p: float = 1.0,
+                     seed: int = 42) -> None:
+        """GenerateOpts.params (SamplingParams, transformer.zig:3652-3657);
+        temperature 0 is greedy."""
+        p = L.SamplingParams(temperature, top_k, top_p, 0, seed)
+        self._mcall("nnz_model_set_sampling", C.byref(p))
+
+    def set_eos(self, ids) -> None:
+        """GenerateOpts.eos_ids: a picked stop token ends generation unemitted."""
+        a = np.ascontiguousarray(list(ids), dtype=np.uint32)
+        self._mcall("nnz_model_set_eos", a.ctypes.data_as(C.c_void_p) if len(a) else None, len(a))
+
+    def decode_status(self):
+        """(tokens emitted, stopped by a stop token) of the current stream."""
+        n, stopped = C.c_uint32(), C.c_int()
+        self._mcall("nnz_model_decode_status", C.byref(n), C.byref(stopped))
+        return n.value, bool(stopped.value)
+
     def generate(self, prompt: np.ndarray, n_new: int, use_graph: bool = True,
                  step_ms: bool = False):
-        """Greedy generate; returns (tokens, top-2 margins, per-step ms or None)."""
+        """generate (transformer.zig:3942): up to n_new tokens, fewer when a
+        stop token ends the stream.  Returns (tokens, per-token values,
+        per-step ms or None); the values are top-2 logit margins (greedy) or
+        the sampled tokens' probabilities."""
         p = np.ascontiguousarray(prompt, dtype=np.uint32)
         toks = np.zeros(n_new, dtype=np.uint32)
         margins = np.zeros(n_new, dtype=np.float32)
         ms = np.zeros(n_new, dtype=np.float32) if step_ms else None
+        count = C.c_uint32()
         self._mcall("nnz_model_generate", p.ctypes.data_as(C.c_void_p), len(p), n_new,
                     toks.ctypes.data_as(C.c_void_p), margins.ctypes.data_as(C.c_void_p),
-                    ms.ctypes.data_as(C.c_void_p) if ms is not None else None, int(use_graph))
-        return toks, margins, ms
+                    ms.ctypes.data_as(C.c_void_p) if ms is not None else None, int(use_graph),
+                    C.byref(count))
+        n = count.value
+        return toks[:n], margins[:n], (ms[:n] if ms is not None else None)

@@ -383,5 +383,24 @@ def dispatch_argmax(dev, logits, out_index, out_value=None):
     dev.call("nnz_dispatch_argmax", _v(logits), logits.numel(), _v(out_index), _v(out_value))
 
 
+def sample_workspace_bytes(count: int) -> int:
+    return int(L.lib().nnz_sample_workspace_bytes(count))
+
+
+def rng_seed(dev, seed: int, state):
+    """std.Random.DefaultPrng.init(seed) into a device uint64[4] (int64 tensor)."""
+    dev.call("nnz_rng_seed", C.c_uint64(seed & (2**64 - 1)), _v(state))
+
+
+def dispatch_sample(dev, logits, out_index, rng, workspace, temperature: float,
+                    top_k: int = 0, top_p: float = 1.0, out_prob=None):
+    """transformer.zig:3860 sampleToken, on device (one draw from ``rng``)."""
+    p = L.SamplingParams(temperature, top_k, top_p, 0, 0)
+    dev.call("nnz_dispatch_sample", _v(logits), logits.numel(), C.byref(p), _v(rng),
+             _v(workspace), workspace.numel() * workspace.element_size() if workspace is not None
+             else 0, _v(out_index), _v(out_prob))
+
+
 __all__ = [n for n in dir() if n.startswith("dispatch_")] + ["Device", "DeviceQWeight",
-                                                             "NnzError", "gqa_scratch_bytes"]
+                                                             "NnzError", "gqa_scratch_bytes",
+                                                             "rng_seed", "sample_workspace_bytes"]

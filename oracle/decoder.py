@@ -112,17 +112,41 @@ class OracleDecoder:
         xf = O.f16(O.rmsnorm(res, self.w.final_norm, cfg.rms_eps))
         return self.lm_head(xf)
 
-    def generate(self, prompt, n_new: int):
+    def generate(self, prompt, n_new: int, eos=()):
         """Greedy generate with the reference's loop (transformer.zig:3942-4030):
-        returns (tokens, top-2 margins) -- n_new tokens, n_new decode passes."""
+        returns (tokens, top-2 margins) -- up to n_new tokens, one decode pass
+        per emitted token; a stop token in ``eos`` ends it unemitted (:3992)."""
         logits = self.forward(list(prompt), 0)[-1]
         pos = len(prompt)
         toks, margins = [], []
         for _ in range(n_new):
             t = O.argmax_first(logits)
+            if t in eos:
+                break
             srt = np.sort(logits)
             toks.append(t)
             margins.append(float(srt[-1] - srt[-2]))
             logits = self.forward([t], pos)[0]
             pos += 1
         return np.array(toks, dtype=np.uint32), np.array(margins)
+
+    def generate_sampled(self, prompt, n_new: int, temperature: float, top_k: int, top_p: float,
+                         seed: int, eos=()):
+        """generate with SamplingParams (transformer.zig:3969-4016): returns
+        (tokens, sampled probabilities, per-step decision margins)."""
+        from .sampling import ZigPrng, sample_token
+        prng = ZigPrng(seed)
+        logits = self.forward(list(prompt), 0)[-1]
+        pos = len(prompt)
+        toks, probs, margins = [], [], []
+        for _ in range(n_new):
+            t, pr, mg = sample_token(logits.astype(np.float32), temperature, top_k, top_p, prng)
+            mg = min(mg, 1.0)
+            if t in eos:
+                break
+            toks.append(t)
+            probs.append(pr)
+            margins.append(mg)
+            logits = self.forward([t], pos)[0]
+            pos += 1
+        return np.array(toks, dtype=np.uint32), np.array(probs), np.array(margins)

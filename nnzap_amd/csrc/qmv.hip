@@ -651,7 +651,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Split-K QMV for long 1-bit rows (K = 64*32*KS, KS = 2..4): the KS waves of
+// Split-K QMV for long 1-bit rows (64*32*(KS-1) < K <= 64*32*KS, KS = 2..8): the KS waves of
 // a block share R rows and wave k takes units [64k, 64k + 64), one per
 // lane, so each wave's x slice, bit loop and row reduction are a KS-th of
 // the full-row kernel's and a SIMD interleaves several short waves instead
@@ -792,7 +792,7 @@ int check_dims(nnz_ctx *ctx, const nnz_qmv_dims &d, const char *name) {
                 d.K, d.group_size);
     NNZ_REQUIRE(ctx, d.group_size % 32 == 0, NNZ_EUNSUPPORTED,
                 "%s: group_size %u must be a multiple of 32", name, d.group_size);
-    NNZ_REQUIRE(ctx, d.K <= 8192, NNZ_EUNSUPPORTED, "%s: K=%u > 8192 not supported", name, d.K);
+    NNZ_REQUIRE(ctx, d.K <= 16384, NNZ_EUNSUPPORTED, "%s: K=%u > 16384 not supported", name, d.K);
     return NNZ_OK;
 }
 
@@ -886,13 +886,14 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
     int lpr_log2 = 0;
     while ((1u << lpr_log2) < lpr) ++lpr_log2;
     const uint32_t nv = ceil_div(units, lpr);
-    NNZ_REQUIRE(ctx, nv >= 1 && nv <= 4, NNZ_EUNSUPPORTED, "%s: K=%u needs %u units/lane", name, d.K, nv);
+    NNZ_REQUIRE(ctx, nv >= 1 && nv <= 8, NNZ_EUNSUPPORTED, "%s: K=%u needs %u units/lane", name, d.K, nv);
     const uint32_t rpw = 64 / lpr;
     const int vec = BITS == 1 ? 1 : 4;
     if constexpr (BITS == 1 && XIN == XIN_X && NMAT == 1 && !FAITH &&
                   (EPI == EPI_STORE || EPI == EPI_RESADD)) {
-        // long single-segment rows: split K over the waves of a block
-        if (nw == 1 && lpr == 64 && nv >= 2 && nv <= 4 && d.K % 2048 == 0) {
+        // long single-segment rows: split K over the waves of a block (the
+        // last wave may be partly idle: K = 9728 is 4 full waves + 48 units)
+        if (nw == 1 && lpr == 64 && nv >= 2 && nv <= 8) {
             constexpr int SR = 4;
             QmvArgs a{};
             a.m0.codes = (const uint32_t *)w[0]->codes;
@@ -910,12 +911,19 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
             switch (nv) {
             case 2: qmv1_splitk_kernel<XDT, EPI, ODT, 2, SR><<<blocks, 128, 0, ctx->stream>>>(a); break;
             case 3: qmv1_splitk_kernel<XDT, EPI, ODT, 3, SR><<<blocks, 192, 0, ctx->stream>>>(a); break;
-            default: qmv1_splitk_kernel<XDT, EPI, ODT, 4, SR><<<blocks, 256, 0, ctx->stream>>>(a); break;
+            case 4: qmv1_splitk_kernel<XDT, EPI, ODT, 4, SR><<<blocks, 256, 0, ctx->stream>>>(a); break;
+            case 5: qmv1_splitk_kernel<XDT, EPI, ODT, 5, SR><<<blocks, 320, 0, ctx->stream>>>(a); break;
+            case 6: qmv1_splitk_kernel<XDT, EPI, ODT, 6, SR><<<blocks, 384, 0, ctx->stream>>>(a); break;
+            case 7: qmv1_splitk_kernel<XDT, EPI, ODT, 7, SR><<<blocks, 448, 0, ctx->stream>>>(a); break;
+            default: qmv1_splitk_kernel<XDT, EPI, ODT, 8, SR><<<blocks, 512, 0, ctx->stream>>>(a); break;
             }
             NNZ_LAUNCHED(ctx);
             return NNZ_OK;
         }
     }
+    // the full-row kernel holds up to 4 units per lane (K <= 8192)
+    NNZ_REQUIRE(ctx, nv <= 4, NNZ_EUNSUPPORTED, "%s: K=%u needs %u units/lane (this form: K <= 8192)",
+                name, d.K, nv);
     int R = 4;
     // Rows per wave-step: as many as keep about one block per CU (pairs:
     // two) -- measured best for the decode shapes -- bounded by the weight

@@ -210,3 +210,38 @@ def test_bonsai_golden_tokens(mdev):
     finally:
         m.close()
     assert list(map(int, toks)) == BONSAI_GOLDEN_TOKENS
+
+
+# The reference's other model shapes (transformer.zig:300-326): Bonsai-4B
+# (hidden 2560, MLP 9728, 32 query heads) and Bonsai-8B (hidden 4096, MLP
+# 12288, untied LM head), 2 layers and a small vocabulary so the oracle stays
+# fast; every projection shape of those models goes through the kernels.
+REF_SHAPES = {
+    "bonsai4b": dict(hidden_size=2560, intermediate_size=9728, num_query_heads=32, rope_theta=5e6),
+    "bonsai8b": dict(hidden_size=4096, intermediate_size=12288, num_query_heads=32, rope_theta=1e6),
+}
+
+
+@pytest.mark.parametrize("shape", list(REF_SHAPES))
+def test_reference_model_shapes(mdev, shape):
+    cfg = cf.DecoderConfig(vocab_size=3000, num_layers=2, num_kv_heads=8, head_dim=128,
+                           max_context_length=256, max_prefill_length=64, group_size=128,
+                           **REF_SHAPES[shape])
+    w = cf.decoder_weights(cfg, norm_mode="unit")
+    print(f"shape {shape}: hidden {cfg.hidden_size} mlp {cfg.intermediate_size}", flush=True)
+    m = DecoderModel(mdev, cfg)
+    try:
+        m.load(w)
+        ids = cf.prompt_ids(cfg, 20)
+        ref = OracleDecoder(w)
+        assert_close_normwise(m.prefill(ids, 0), ref.forward(list(ids), 0)[-1],
+                              what=f"{shape} prefill")
+        for i, t in enumerate([7, 2999]):
+            pos = len(ids) + i
+            assert_close_normwise(m.forward_decode(t, pos), ref.forward([t], pos)[0],
+                                  what=f"{shape} decode {pos}")
+        toks, _, _ = m.generate(ids, 12)
+        ref_toks, _ = OracleDecoder(w).generate(ids, 12)
+        assert np.array_equal(toks, ref_toks), (toks, ref_toks)
+    finally:
+        m.close()

@@ -190,23 +190,22 @@ BONSAI_GOLDEN_TOKENS = [151667, 198, 151668, 271, 785, 6722, 315, 9625, 374, 120
                     reason="set NNZAP_BONSAI_DIR to a Bonsai-1.7B (1-bit MLX) model directory")
 def test_bonsai_golden_tokens(mdev):
     """The reference's golden run on the real checkpoint (needs the weights,
-    config.json and tokenizer.json in NNZAP_BONSAI_DIR)."""
-    from tokenizers import Tokenizer
+    config.json and tokenizer.json in NNZAP_BONSAI_DIR): the prompt through
+    this build's tokenizer and chat template (tokenizer.zig:330-367), greedy,
+    stopping at <|endoftext|> / <|im_end|> (bonsai_golden.zig:142-146)."""
     from nnzap_amd import checkpoint as ck
+    from nnzap_amd.tokenizer import Tokenizer
     d = os.environ["NNZAP_BONSAI_DIR"]
     cfg, quant, tie = ck.config_from_hf(d, max_context_length=1024)
     if quant != ck.QUANT_Q1:
         pytest.skip("the decoder model holds 1-bit projections")
     tok = Tokenizer.from_file(os.path.join(d, "tokenizer.json"))
-    enc = lambda s: tok.encode(s, add_special_tokens=False).ids
-    im_start, im_end = tok.token_to_id("<|im_start|>"), tok.token_to_id("<|im_end|>")
-    # applyChatTemplate (nnmetal/src/tokenizer.zig:330-367), piece by piece
-    ids = ([im_start] + enc("user\n") + enc(BONSAI_GOLDEN_PROMPT) + [im_end] + enc("\n")
-           + [im_start] + enc("assistant\n"))
+    ids = tok.apply_chat_template(BONSAI_GOLDEN_PROMPT)
     m = DecoderModel(mdev, cfg)
     try:
         m.load_weights(d, quant, tie)
-        toks, _, _ = m.generate(np.array(ids, dtype=np.uint32), len(BONSAI_GOLDEN_TOKENS))
+        m.set_eos(tok.stop_tokens())
+        toks, _, _ = m.generate(np.array(ids, dtype=np.uint32), 20)
     finally:
         m.close()
     assert list(map(int, toks)) == BONSAI_GOLDEN_TOKENS
@@ -245,3 +244,38 @@ def test_reference_model_shapes(mdev, shape):
         assert np.array_equal(toks, ref_toks), (toks, ref_toks)
     finally:
         m.close()
+
+
+def test_chat_end_to_end(mdev, tmp_path):
+    """The user's path end to end: a byte-level BPE tokenizer (trained here),
+    its chat template, an MLX checkpoint with a matching vocabulary, greedy
+    generate with the tokenizer's stop tokens, and the decoded reply; tokens
+    against the oracle decoder on the same checkpoint."""
+    tokenizers = pytest.importorskip("tokenizers")
+    from tokenizers import models, pre_tokenizers, trainers
+    from nnzap_amd import checkpoint as ck
+    from nnzap_amd.tokenizer import Tokenizer
+    from ckpt_util import write_mlx_checkpoint
+    hf = tokenizers.Tokenizer(models.BPE())
+    hf.pre_tokenizer = pre_tokenizers.ByteLevel(add_prefix_space=False)
+    text = ["The capital of France is Paris. The capital of Italy is Rome."] * 50
+    hf.train_from_iterator(text, trainers.BpeTrainer(
+        vocab_size=384, show_progress=False, initial_alphabet=pre_tokenizers.ByteLevel.alphabet(),
+        special_tokens=["<|endoftext|>", "<|im_start|>", "<|im_end|>"]))
+    tok = Tokenizer.from_json(hf.to_str())
+    V = tok.vocab_size
+    cfg = cf.DecoderConfig(**{**CKPT_CFG.__dict__, "vocab_size": V})
+    write_mlx_checkpoint(tmp_path, cfg, bits=1, tie=True)
+    ids = np.array(tok.apply_chat_template("The capital of France is"), dtype=np.uint32)
+    w = ck.load_checkpoint(tmp_path, cfg)
+    ref_toks, _ = OracleDecoder(w).generate(ids, 16, eos=tuple(tok.stop_tokens()))
+    m = DecoderModel(mdev, cfg)
+    try:
+        m.load_weights(tmp_path)
+        m.set_eos(tok.stop_tokens())
+        toks, _, _ = m.generate(ids, 16)
+    finally:
+        m.close()
+    assert np.array_equal(toks, ref_toks), (toks, ref_toks)
+    reply = tok.decode(toks)
+    assert reply == tok.decode(ref_toks) and len(toks) <= 16

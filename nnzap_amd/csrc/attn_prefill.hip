@@ -1,0 +1,276 @@
+// Causal GQA attention of a prefill batch on the matrix cores.
+//
+// Replaces, for the batched prefill, the reference's token-by-token
+// attention (gqa_attention_fused_f16io_tg per prompt token,
+// transformer.metal:1438-1695, driven by chunkedPrefill,
+// transformer.zig:4032-4068) with one flash-attention launch per layer:
+// queries n tokens at positions start.., keys/values from the layer's f16
+// KV cache (K [Hkv][max_ctx][D], V transposed [Hkv][D][max_ctx]) after the
+// prep kernel appended the batch's own keys and values.
+//
+// Layout on the MFMA (v_mfma_f32_16x16x32_f16, fp32 accumulate):
+//   * a wave owns 16 queries of one query head; a block holds the G query
+//     heads of one KV head, so the K/V tiles staged in LDS serve all of them;
+//   * scores are computed transposed, S^T[key][q] = K . Q^T: A = 16 keys x
+//     32 dims of K from LDS, B = Q^T from registers.  The accumulator puts
+//     keys 4g..4g+3 of a 16-key block in lane group g's four registers, all
+//     for the lane's own query q = lane % 16;
+//   * O^T[d][q] += V^T . P^T takes B = P^T straight from those registers:
+//     for a 32-key step, B slot 8g + 4s + r is key 16(2k+s) + 4g + r, and
+//     the A operand (V^T from LDS) reads V in the same key order, so no
+//     data moves between lanes;
+//   * the online softmax of query q runs in its own lanes (max/sum over the
+//     lane's 16 keys, then over the 4 lane groups).
+// Precision: the queries are kept unrounded (float32, as the reference
+// keeps q), so each MFMA operand that is not already f16 is split into an
+// f16 high part and an f16 remainder -- q and the probabilities p -- and
+// both products are accumulated: the scores and P.V carry ~2^-22 relative
+// error, the same as float32 arithmetic on these f16 keys and values.
+#include "internal.h"
+
+namespace {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+constexpr int KT = 64;  // keys per LDS tile
+
+struct PrefillArgs {
+    const float *q;      // [n][hq][D] f32
+    const f16_t *kc;     // [hkv][max_ctx][D]
+    const f16_t *vc;     // [hkv][D][max_ctx]
+    f16_t *out;          // [n][hq][D]
+    uint32_t start, n, hq, max_ctx;
+    float scale;
+};
+
+__device__ __forceinline__ void split_f16(float v, _Float16 &hi, _Float16 &lo) {
+    hi = (_Float16)v;
+    lo = (_Float16)(v - (float)hi);
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(64 * G) void attn_prefill_kernel(PrefillArgs a) {
+    constexpr int NT = 64 * G;
+    constexpr int NKS = D / 32;  // 32-dim steps of the score MFMAs
+    constexpr int NDT = D / 16;  // 16-dim tiles of O^T
+    constexpr int KP = D + 8;    // LDS pitch (halves) of a K row
+    constexpr int VP = KT + 8;   // LDS pitch (halves) of a V^T row
+    __shared__ __align__(16) _Float16 Ks[KT * KP];
+    __shared__ __align__(16) _Float16 Vs[D * VP];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const uint32_t hkv = blockIdx.y;
+    const uint32_t h = hkv * G + (uint32_t)w;
+    const uint32_t q0 = blockIdx.x * 16u;
+    const uint32_t qi = q0 + (uint32_t)c;
+    const bool qvalid = qi < a.n;
+    const uint32_t qpos = a.start + qi;
+    const uint32_t seq_end = a.start + a.n;
+    const uint32_t qlast = (q0 + 15u < a.n ? q0 + 15u : a.n - 1u) + a.start;
+    const uint32_t ntiles = qlast / KT + 1u;
+
+    // Q^T fragments: lane (g, c) holds dims 32 ks + 8 g .. +8 of query c
+    half8 qh[NKS], ql[NKS];
+    {
+        const float *qp = a.q + ((size_t)(qvalid ? qi : 0u) * a.hq + h) * D;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+            const float4 v0 = *(const float4 *)(qp + 32 * ks + 8 * g);
+            const float4 v1 = *(const float4 *)(qp + 32 * ks + 8 * g + 4);
+            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                _Float16 hi, lo;
+                split_f16(qvalid ? v[e] : 0.f, hi, lo);
+                qh[ks][e] = hi;
+                ql[ks][e] = lo;
+            }
+        }
+    }
+    float4v o[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) o[dt] = (float4v){0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.f;
+
+    const f16_t *kbase = a.kc + (size_t)hkv * a.max_ctx * D;
+    const f16_t *vbase = a.vc + (size_t)hkv * D * a.max_ctx;
+    // Tiles are staged through registers, one ahead: the next tile's loads
+    // are in flight while the current one is computed.  The loads are never
+    // branched around: addresses are clamped into the cache and keys past
+    // the sequence are zeroed by selects (8-key V pieces never cross
+    // max_ctx: max_ctx % 8 == 0).
+    constexpr int KPT = KT * D / 8 / NT, VPT = D * KT / 8 / NT;
+    uint4 kr[KPT], vr[VPT];
+    auto load_tile = [&](uint32_t k0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int p = tid + i * NT;
+            const uint32_t key = k0 + (uint32_t)(p / (D / 8));
+            const uint32_t kc = key < seq_end ? key : 0u;
+            const uint4 v = *(const uint4 *)(kbase + (size_t)kc * D + (p % (D / 8)) * 8);
+            kr[i] = key < seq_end ? v : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int p = tid + i * NT;
+            const uint32_t key = k0 + (uint32_t)(p % (KT / 8)) * 8u;
+            const uint32_t kc = key < seq_end ? key : 0u;
+            uint4 v = *(const uint4 *)(vbase + (size_t)(p / (KT / 8)) * a.max_ctx + kc);
+            // halves e with key + e >= seq_end become 0
+            const int keep = key >= seq_end ? 0 : (int)(seq_end - key < 8u ? seq_end - key : 8u);
+            const uint32_t m[4] = {keep >= 2 ? ~0u : (keep >= 1 ? 0xFFFFu : 0u),
+                                   keep >= 4 ? ~0u : (keep >= 3 ? 0xFFFFu : 0u),
+                                   keep >= 6 ? ~0u : (keep >= 5 ? 0xFFFFu : 0u),
+                                   keep >= 8 ? ~0u : (keep >= 7 ? 0xFFFFu : 0u)};
+            v.x &= m[0];
+            v.y &= m[1];
+            v.z &= m[2];
+            v.w &= m[3];
+            vr[i] = v;
+        }
+    };
+    auto store_tile = [&]() __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+            const int p = tid + i * NT;
+            *(uint4 *)(Ks + (p / (D / 8)) * KP + (p % (D / 8)) * 8) = kr[i];
+        }
+#pragma unroll
+        for (int i = 0; i < VPT; ++i) {
+            const int p = tid + i * NT;
+            *(uint4 *)(Vs + (p / (KT / 8)) * VP + (p % (KT / 8)) * 8) = vr[i];
+        }
+    };
+    load_tile(0);
+    for (uint32_t t = 0; t < ntiles; ++t) {
+        const uint32_t k0 = t * KT;
+        store_tile();
+        __syncthreads();
+        load_tile((t + 1 < ntiles ? t + 1 : t) * KT);
+
+        // S^T = K . Q^T, 4 blocks of 16 keys
+        float4v s[KT / 16];
+#pragma unroll
+        for (int st = 0; st < KT / 16; ++st) {
+            s[st] = (float4v){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < NKS; ++ks) {
+                const half8 ka = *(const half8 *)(Ks + (st * 16 + c) * KP + 32 * ks + 8 * g);
+                s[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[ks], s[st], 0, 0, 0);
+                s[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[ks], s[st], 0, 0, 0);
+            }
+        }
+        // scale, causal mask, online softmax of query c
+        float mx = -INFINITY;
+#pragma unroll
+        for (int st = 0; st < KT / 16; ++st)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t key = k0 + (uint32_t)(st * 16 + 4 * g + r);
+                const float v = (qvalid && key <= qpos) ? s[st][r] * a.scale : -INFINITY;
+                s[st][r] = v;
+                mx = fmaxf(mx, v);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = m_new == -INFINITY ? 1.f : expf(m_run - m_new);
+        float ls = 0.f;
+#pragma unroll
+        for (int st = 0; st < KT / 16; ++st)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float p = s[st][r] == -INFINITY ? 0.f : expf(s[st][r] - m_new);
+                s[st][r] = p;
+                ls += p;
+            }
+        ls += __shfl_xor(ls, 16);
+        ls += __shfl_xor(ls, 32);
+        l_run = l_run * alpha + ls;
+        m_run = m_new;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
+
+        // P^T as B operands: slot 8g + 4 sb + r = key 16 (2 kk + sb) + 4 g + r
+        half8 ph[KT / 32], pl[KT / 32];
+#pragma unroll
+        for (int kk = 0; kk < KT / 32; ++kk)
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    _Float16 hi, lo;
+                    split_f16(s[2 * kk + sb][r], hi, lo);
+                    ph[kk][4 * sb + r] = hi;
+                    pl[kk][4 * sb + r] = lo;
+                }
+        // O^T += V^T . P^T
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+            const _Float16 *vrow = Vs + (16 * dt + c) * VP + 4 * g;
+#pragma unroll
+            for (int kk = 0; kk < KT / 32; ++kk) {
+                const uint2 lo4 = *(const uint2 *)(vrow + (2 * kk) * 16);
+                const uint2 hi4 = *(const uint2 *)(vrow + (2 * kk + 1) * 16);
+                const uint4 u = make_uint4(lo4.x, lo4.y, hi4.x, hi4.y);
+                const half8 va = __builtin_bit_cast(half8, u);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, ph[kk], o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[kk], o[dt], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+
+    if (qvalid) {
+        const float inv = 1.0f / l_run;
+        f16_t *op = a.out + ((size_t)qi * a.hq + h) * D;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+            const uint32_t d = 16u * dt + 4u * g;
+            const uint32_t p0 = (uint32_t)__builtin_bit_cast(uint16_t, (f16_t)(o[dt][0] * inv)) |
+                                (uint32_t)__builtin_bit_cast(uint16_t, (f16_t)(o[dt][1] * inv)) << 16;
+            const uint32_t p1 = (uint32_t)__builtin_bit_cast(uint16_t, (f16_t)(o[dt][2] * inv)) |
+                                (uint32_t)__builtin_bit_cast(uint16_t, (f16_t)(o[dt][3] * inv)) << 16;
+            *(uint2 *)(op + d) = make_uint2(p0, p1);
+        }
+    }
+}
+
+template <int D>
+int launch_d(nnz_ctx *ctx, const PrefillArgs &a, uint32_t hkv, uint32_t G) {
+    const dim3 grid((a.n + 15) / 16, hkv);
+    switch (G) {
+    case 2: attn_prefill_kernel<D, 2><<<grid, 128, 0, ctx->stream>>>(a); break;
+    case 4: attn_prefill_kernel<D, 4><<<grid, 256, 0, ctx->stream>>>(a); break;
+    default: attn_prefill_kernel<D, 8><<<grid, 512, 0, ctx->stream>>>(a); break;
+    }
+    NNZ_LAUNCHED(ctx);
+    return NNZ_OK;
+}
+
+}  // namespace
+
+bool nnz_attn_prefill_supported(uint32_t head_dim, uint32_t hq, uint32_t hkv, uint32_t max_ctx) {
+    if (head_dim != 64 && head_dim != 128) return false;
+    if (hkv == 0 || hq % hkv) return false;
+    const uint32_t G = hq / hkv;   // blocks of G waves stage the tiles: G >= 2
+    return (G == 2 || G == 4 || G == 8) && max_ctx % 8 == 0;
+}
+
+int nnz_attn_prefill_launch(nnz_ctx *ctx, const float *q, const void *kc, const void *vc, void *out,
+                            uint32_t start, uint32_t n, uint32_t hq, uint32_t hkv,
+                            uint32_t head_dim, uint32_t max_ctx) {
+    NNZ_REQUIRE(ctx, q && kc && vc && out && n > 0, NNZ_EINVAL, "attn_prefill: bad arguments");
+    NNZ_REQUIRE(ctx, nnz_attn_prefill_supported(head_dim, hq, hkv, max_ctx), NNZ_EUNSUPPORTED,
+                "attn_prefill: head_dim %u, %u/%u heads, max_ctx %u not supported", head_dim, hq,
+                hkv, max_ctx);
+    NNZ_REQUIRE(ctx, (uint64_t)start + n <= max_ctx, NNZ_EINVAL,
+                "attn_prefill: positions %u..%u beyond max_ctx %u", start, start + n - 1, max_ctx);
+    NNZ_REQUIRE(ctx, (((uintptr_t)q | (uintptr_t)kc | (uintptr_t)vc | (uintptr_t)out) & 15) == 0,
+                NNZ_EINVAL, "attn_prefill: buffers must be 16-byte aligned");
+    PrefillArgs a{(const float *)q, (const f16_t *)kc, (const f16_t *)vc, (f16_t *)out,
+                  start, n, hq, max_ctx, 1.0f / sqrtf((float)head_dim)};
+    return head_dim == 128 ? launch_d<128>(ctx, a, hkv, hq / hkv) : launch_d<64>(ctx, a, hkv, hq / hkv);
+}

@@ -99,3 +99,17 @@ size_t nnz_sample_ws_bytes(uint32_t n);
 int nnz_sample_launch(nnz_ctx *ctx, const float *logits, uint32_t n, const nnz_sampling_params &p,
                       uint64_t *rng, void *ws, uint32_t *out_index, float *out_prob,
                       const NnzPick *pick);
+
+// Causal GQA attention of a prefill batch on MFMA (attn_prefill.hip): f32
+// queries [n][hq][D], f16 KV cache (V transposed), f16 output [n][hq][D].
+bool nnz_attn_prefill_supported(uint32_t head_dim, uint32_t hq, uint32_t hkv, uint32_t max_ctx);
+int nnz_attn_prefill_launch(nnz_ctx *ctx, const float *q, const void *kc, const void *vc, void *out,
+                            uint32_t start, uint32_t n, uint32_t hq, uint32_t hkv,
+                            uint32_t head_dim, uint32_t max_ctx);
+
+// Per-head q/k RMSNorm + RoPE and the KV append of a prefill batch, one wave
+// per (head, token) (transformer.hip); frequencies from a [head_dim/2] table.
+int nnz_attn_prep_waves_launch(nnz_ctx *ctx, const void *q, const void *kr, const void *vr,
+                               const float *qn, const float *kn, float *qout, void *kc, void *vc,
+                               const float *inv_freq, uint32_t hq, uint32_t hkv, uint32_t head_dim,
+                               uint32_t pos0, uint32_t nq, uint32_t max_ctx, float eps);

@@ -629,9 +629,15 @@ int nnz_model_prefill(nnz_model *m, const uint32_t *tokens_host, uint32_t n, uin
         RC(nnz_gemm_launch(ctx, &Ly.q.w, nullptr, m->p_xn, n, m->p_q, NNZ_GEMM_STORE_F16, dims_of(m, Ly.q)));
         RC(nnz_gemm_launch(ctx, &Ly.k.w, nullptr, m->p_xn, n, m->p_k, NNZ_GEMM_STORE_F16, dims_of(m, Ly.k)));
         RC(nnz_gemm_launch(ctx, &Ly.v.w, nullptr, m->p_xn, n, m->p_v, NNZ_GEMM_STORE_F16, dims_of(m, Ly.v)));
-        RC(nnz_attn_prep_launch(ctx, m->p_q, m->p_k, m->p_v, Ly.q_norm, Ly.k_norm, m->p_qf, Ly.kc,
-                                Ly.vc, c.num_query_heads, c.num_kv_heads, c.head_dim, start, nullptr,
-                                n, c.max_context_length, c.rms_eps, c.rope_theta));
+        RC(nnz_attn_prep_waves_launch(ctx, m->p_q, m->p_k, m->p_v, Ly.q_norm, Ly.k_norm, m->p_qf,
+                                      Ly.kc, Ly.vc, m->rope_inv, c.num_query_heads, c.num_kv_heads,
+                                      c.head_dim, start, n, c.max_context_length, c.rms_eps));
+        if (nnz_attn_prefill_supported(c.head_dim, c.num_query_heads, c.num_kv_heads,
+                                       c.max_context_length)) {
+            RC(nnz_attn_prefill_launch(ctx, m->p_qf, Ly.kc, Ly.vc, m->p_att, start, n,
+                                       c.num_query_heads, c.num_kv_heads, c.head_dim,
+                                       c.max_context_length));
+        } else {
         NnzAttnCall ac{};
         ac.q = m->p_qf;
         ac.qdt = NNZ_F32;
@@ -648,6 +654,7 @@ int nnz_model_prefill(nnz_model *m, const uint32_t *tokens_host, uint32_t n, uin
         ac.nq = n;
         ac.dims = gqa_dims(m, start + 1);
         RC(nnz_attn_launch_ex(ctx, ac));
+        }
         RC(nnz_gemm_launch(ctx, &Ly.o.w, nullptr, m->p_att, n, m->p_res, NNZ_GEMM_RESADD, dims_of(m, Ly.o)));
         RC(nnz_dispatch_rms_norm(ctx, m->p_res, Ly.ffn_norm, m->p_xn, NNZ_F16, 0, {H, n, c.rms_eps}));
         RC(nnz_gemm_launch(ctx, &Ly.gate.w, &Ly.up.w, m->p_xn, n, m->p_h, NNZ_GEMM_SILU_PAIR,

@@ -214,6 +214,50 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(
     }
 }
 
+// The same prologue for a prefill batch: one wave per (head, token), lane p
+// holding the rotation pair (2p, 2p+1), so the norm is one wave reduction
+// and the rotation needs no shuffle; frequencies from the model's table.
+__global__ __launch_bounds__(256) void attn_prep_waves_kernel(
+    const f16_t *q, const f16_t *kr, const f16_t *vr, const float *qn, const float *kn,
+    float *qout, f16_t *kc, f16_t *vc, const float *inv_freq, uint32_t hq, uint32_t hkv,
+    uint32_t head_dim, uint32_t pos0, uint32_t nq, uint32_t max_ctx, float eps) {
+    const uint32_t heads = hq + hkv;
+    const uint32_t u = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (u >= heads * nq) return;   // whole waves only
+    const uint32_t z = u / heads, b = u % heads, p = threadIdx.x & 63u;
+    const uint32_t pos = pos0 + z;
+    const bool on = 2u * p < head_dim;
+    const bool isq = b < hq;
+    const uint32_t h = isq ? b : b - hq;
+    const f16_t *src = isq ? q + ((size_t)z * hq + h) * head_dim : kr + ((size_t)z * hkv + h) * head_dim;
+    float x0 = 0.f, x1 = 0.f;
+    if (on) {
+        const uint32_t w = *(const uint32_t *)(src + 2u * p);
+        x0 = (float)__builtin_bit_cast(f16_t, (uint16_t)(w & 0xFFFFu));
+        x1 = (float)__builtin_bit_cast(f16_t, (uint16_t)(w >> 16));
+    }
+    const float ss = wave_sum(x0 * x0 + x1 * x1);
+    const float rms = rsqrtf(ss / (float)head_dim + eps);
+    const float *sc = isq ? qn : kn;
+    if (!on) return;
+    const float v0 = x0 * rms * sc[2u * p], v1 = x1 * rms * sc[2u * p + 1u];
+    const float ang = (float)pos * inv_freq[p];
+    float sn, cs;
+    sincosf(ang, &sn, &cs);
+    const float r0 = fmaf(v0, cs, -v1 * sn), r1 = fmaf(v0, sn, v1 * cs);
+    if (isq) {
+        *(float2 *)(qout + ((size_t)z * hq + h) * head_dim + 2u * p) = make_float2(r0, r1);
+    } else {
+        const size_t stride = (size_t)max_ctx * head_dim;
+        const uint32_t kw = (uint32_t)__builtin_bit_cast(uint16_t, (f16_t)r0) |
+                            (uint32_t)__builtin_bit_cast(uint16_t, (f16_t)r1) << 16;
+        *(uint32_t *)(kc + h * stride + (size_t)pos * head_dim + 2u * p) = kw;
+        const f16_t *vs = vr + ((size_t)z * hkv + h) * head_dim + 2u * p;
+        vc[h * stride + (size_t)(2u * p) * max_ctx + pos] = vs[0];
+        vc[h * stride + (size_t)(2u * p + 1u) * max_ctx + pos] = vs[1];
+    }
+}
+
 // ------------------------------------------------------ decode attention ---
 // Split-sequence GQA decode.  Grid (num_chunks, Hkv); block 256 threads.
 // Each block serves the G query heads of one KV head over one chunk of
@@ -1539,6 +1583,20 @@ int nnz_attn_prep_launch(nnz_ctx *ctx, const void *q, const void *kr, const void
     attn_prep_kernel<<<dim3(hq + hkv, nq), 256, 0, ctx->stream>>>(
         (const f16_t *)q, (const f16_t *)kr, (const f16_t *)vr, qn, kn, qout, (f16_t *)kc,
         (f16_t *)vc, hq, hkv, head_dim, pos, d_pos, max_ctx, eps, theta);
+    NNZ_LAUNCHED(ctx);
+    return NNZ_OK;
+}
+
+int nnz_attn_prep_waves_launch(nnz_ctx *ctx, const void *q, const void *kr, const void *vr,
+                               const float *qn, const float *kn, float *qout, void *kc, void *vc,
+                               const float *inv_freq, uint32_t hq, uint32_t hkv, uint32_t head_dim,
+                               uint32_t pos0, uint32_t nq, uint32_t max_ctx, float eps) {
+    NNZ_REQUIRE(ctx, head_dim % 2 == 0 && head_dim <= 128, NNZ_EUNSUPPORTED,
+                "attn_prep: head_dim %u (even, <= 128)", head_dim);
+    const uint32_t units = (hq + hkv) * nq;
+    attn_prep_waves_kernel<<<ceil_div(units, 4u), 256, 0, ctx->stream>>>(
+        (const f16_t *)q, (const f16_t *)kr, (const f16_t *)vr, qn, kn, qout, (f16_t *)kc,
+        (f16_t *)vc, inv_freq, hq, hkv, head_dim, pos0, nq, max_ctx, eps);
     NNZ_LAUNCHED(ctx);
     return NNZ_OK;
 }

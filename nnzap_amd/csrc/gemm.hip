@@ -41,13 +41,23 @@ __device__ __forceinline__ void step_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// Rows [0, rows0) of the launch come from matrix 0 (the kernel's codes0 /
+// scales0 / out), [rows0, rows0 + rows1) from matrix 1, the rest from
+// matrix 2; each writes its own output [P][rows].  n <= 1: one matrix.
+struct GemmSegs {
+    uint32_t n, rows0, rows1;
+    const uint32_t *codes1, *codes2;
+    const uint16_t *scales1, *scales2;
+    void *out1, *out2;
+};
+
 template <int MODE, int NMAT>
 __global__ __launch_bounds__(512) void dq_gemm_kernel(const f16_t *A, const uint32_t *codes0,
                                                       const uint16_t *scales0,
                                                       const uint32_t *codes1,
                                                       const uint16_t *scales1, void *out,
                                                       uint32_t P, uint32_t M, uint32_t K,
-                                                      uint32_t gs_log2) {
+                                                      uint32_t gs_log2, GemmSegs sg) {
     // A tile of a K-step: 64 rows x 128 bytes, the eight 16-byte pieces of
     // row r stored at slot (piece ^ (r & 7)) so the MFMA fragment reads (16
     // rows, one piece each) spread over the banks.  B: dequantised W rows,
@@ -61,7 +71,25 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const f16_t *A, const uint
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 2, wn = wave & 3;   // 8 waves: 2 x 4, each 32 rows x 16 columns
-    const uint32_t p0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const uint32_t p0 = blockIdx.y * BM;
+    uint32_t n0 = blockIdx.x * BN;
+    if (sg.n > 1) {   // row segments of up to three matrices, each with its own output
+        if (n0 < sg.rows0) {
+            M = sg.rows0;
+        } else if (n0 < sg.rows0 + sg.rows1 || sg.n == 2) {
+            n0 -= sg.rows0;
+            codes0 = sg.codes1;
+            scales0 = sg.scales1;
+            out = sg.out1;
+            M = sg.rows1;
+        } else {
+            n0 -= sg.rows0 + sg.rows1;
+            codes0 = sg.codes2;
+            scales0 = sg.scales2;
+            out = sg.out2;
+            M = M - sg.rows0 - sg.rows1;
+        }
+    }
     const uint32_t words_per_row = K / 32, groups_per_row = K >> gs_log2;
     const uint32_t nk = K / BK;
     if (tid < 256) {
@@ -233,21 +261,53 @@ int nnz_gemm_launch(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, 
     const uint16_t *s0 = (const uint16_t *)wa->scales;
     switch (mode) {
     case NNZ_GEMM_STORE_F16:
-        dq_gemm_kernel<NNZ_GEMM_STORE_F16, 1><<<grid, 512, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl);
+        dq_gemm_kernel<NNZ_GEMM_STORE_F16, 1><<<grid, 512, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl, GemmSegs{});
         break;
     case NNZ_GEMM_STORE_F32:
-        dq_gemm_kernel<NNZ_GEMM_STORE_F32, 1><<<grid, 512, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl);
+        dq_gemm_kernel<NNZ_GEMM_STORE_F32, 1><<<grid, 512, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl, GemmSegs{});
         break;
     case NNZ_GEMM_RESADD:
-        dq_gemm_kernel<NNZ_GEMM_RESADD, 1><<<grid, 512, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl);
+        dq_gemm_kernel<NNZ_GEMM_RESADD, 1><<<grid, 512, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl, GemmSegs{});
         break;
     case NNZ_GEMM_SILU_PAIR:
         dq_gemm_kernel<NNZ_GEMM_SILU_PAIR, 2><<<grid, 512, 0, ctx->stream>>>(
-            A, c0, s0, (const uint32_t *)wb->codes, (const uint16_t *)wb->scales, out, P, d.M, d.K, gl);
+            A, c0, s0, (const uint32_t *)wb->codes, (const uint16_t *)wb->scales, out, P, d.M, d.K, gl, GemmSegs{});
         break;
     default:
         return nnz_fail(ctx, NNZ_EINVAL, "dequant_gemm: unknown mode %d", mode);
     }
+    NNZ_LAUNCHED(ctx);
+    return NNZ_OK;
+}
+
+// One launch for up to three matrices sharing K and the A operand (the
+// prefill's Q, K and V projections), f16 outputs of their own.
+int nnz_gemm_segments_launch(nnz_ctx *ctx, const nnz_qweight *const *w, void *const *out, int nw,
+                             const void *a, uint32_t P, uint32_t K, uint32_t group_size) {
+    NNZ_REQUIRE(ctx, nw >= 1 && nw <= 3 && a && P > 0, NNZ_EINVAL, "gemm_segments: bad arguments");
+    NNZ_REQUIRE(ctx, K % BK == 0 && group_size % BK == 0 && K % group_size == 0 &&
+                         (group_size & (group_size - 1)) == 0,
+                NNZ_EUNSUPPORTED, "gemm_segments: need K %% 64 == 0, power-of-two group size %% 64 == 0");
+    NNZ_REQUIRE(ctx, ((uintptr_t)a & 15) == 0, NNZ_EINVAL, "gemm_segments: A must be 16-byte aligned");
+    uint32_t rows[3] = {0, 0, 0}, M = 0;
+    for (int i = 0; i < nw; ++i) {
+        NNZ_REQUIRE(ctx, w[i] && out[i] && w[i]->bits == 1 && w[i]->codes && w[i]->scales &&
+                             w[i]->group_size == group_size && w[i]->packed_count % K == 0,
+                    NNZ_EINVAL, "gemm_segments: bad weight %d", i);
+        rows[i] = w[i]->packed_count / K;
+        NNZ_REQUIRE(ctx, rows[i] % BN == 0, NNZ_EUNSUPPORTED, "gemm_segments: rows %% 64 != 0");
+        M += rows[i];
+    }
+    GemmSegs sg{(uint32_t)nw, rows[0], rows[1],
+                nw > 1 ? (const uint32_t *)w[1]->codes : nullptr,
+                nw > 2 ? (const uint32_t *)w[2]->codes : nullptr,
+                nw > 1 ? (const uint16_t *)w[1]->scales : nullptr,
+                nw > 2 ? (const uint16_t *)w[2]->scales : nullptr,
+                nw > 1 ? out[1] : nullptr, nw > 2 ? out[2] : nullptr};
+    dim3 grid(M / BN, ceil_div(P, BM));
+    dq_gemm_kernel<NNZ_GEMM_STORE_F16, 1><<<grid, 512, 0, ctx->stream>>>(
+        (const f16_t *)a, (const uint32_t *)w[0]->codes, (const uint16_t *)w[0]->scales, nullptr,
+        nullptr, out[0], P, M, K, (uint32_t)__builtin_ctz(group_size), sg);
     NNZ_LAUNCHED(ctx);
     return NNZ_OK;
 }

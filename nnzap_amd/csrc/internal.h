@@ -113,3 +113,8 @@ int nnz_attn_prep_waves_launch(nnz_ctx *ctx, const void *q, const void *kr, cons
                                const float *qn, const float *kn, float *qout, void *kc, void *vc,
                                const float *inv_freq, uint32_t hq, uint32_t hkv, uint32_t head_dim,
                                uint32_t pos0, uint32_t nq, uint32_t max_ctx, float eps);
+
+// One prefill GEMM launch over up to three 1-bit matrices that share K and
+// the f16 A operand, each written to its own f16 output [P][rows] (gemm.hip).
+int nnz_gemm_segments_launch(nnz_ctx *ctx, const nnz_qweight *const *w, void *const *out, int nw,
+                             const void *a, uint32_t P, uint32_t K, uint32_t group_size);

@@ -626,9 +626,11 @@ int nnz_model_prefill(nnz_model *m, const uint32_t *tokens_host, uint32_t n, uin
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         Layer &Ly = m->L[l];
         RC(nnz_dispatch_rms_norm(ctx, m->p_res, Ly.attn_norm, m->p_xn, NNZ_F16, 0, {H, n, c.rms_eps}));
-        RC(nnz_gemm_launch(ctx, &Ly.q.w, nullptr, m->p_xn, n, m->p_q, NNZ_GEMM_STORE_F16, dims_of(m, Ly.q)));
-        RC(nnz_gemm_launch(ctx, &Ly.k.w, nullptr, m->p_xn, n, m->p_k, NNZ_GEMM_STORE_F16, dims_of(m, Ly.k)));
-        RC(nnz_gemm_launch(ctx, &Ly.v.w, nullptr, m->p_xn, n, m->p_v, NNZ_GEMM_STORE_F16, dims_of(m, Ly.v)));
+        {   // Q, K and V in one launch (row segments of one grid)
+            const nnz_qweight *ws[3] = {&Ly.q.w, &Ly.k.w, &Ly.v.w};
+            void *outs[3] = {m->p_q, m->p_k, m->p_v};
+            RC(nnz_gemm_segments_launch(ctx, ws, outs, 3, m->p_xn, n, H, c.group_size));
+        }
         RC(nnz_attn_prep_waves_launch(ctx, m->p_q, m->p_k, m->p_v, Ly.q_norm, Ly.k_norm, m->p_qf,
                                       Ly.kc, Ly.vc, m->rope_inv, c.num_query_heads, c.num_kv_heads,
                                       c.head_dim, start, n, c.max_context_length, c.rms_eps));

@@ -6,14 +6,24 @@
 // steps (nnmetal/src/transformer.zig:4032-4068), and its only dequant-matmul
 // (`qmm`, compute.metal:2975-3083) stores W as [K x N] for the MNIST network.
 //
-// Design:
-//   * 64x64 output tile per 256-thread block, 4 waves in a 2x2 layout, each
-//     wave 32x32 = 2x2 MFMA tiles of v_mfma_f32_16x16x32_f16 (fp32 accumulate).
-//   * Per 64-wide K step the block stages A (f16, straight copy) and the
-//     dequantised W tile (+-s written as f16; exact because s is an f16
-//     scale) in LDS, rows padded by 16 bytes to spread LDS banks.
-//   * Products of f16 activations and f16 +-s are exact in the MFMA, so the
-//     result differs from the decode QMV only in fp32 summation order.
+// Design (v_mfma_f32_16x16x32_f16, fp32 accumulate):
+//   * One 64 (tokens) x 64 (W rows) output tile per 512-thread block.  The 8
+//     waves are 2 W-row halves x 4 k-phases: wave (wn, kq) computes a 64 x 32
+//     tile over the k-steps (64 k each) with index = kq mod 4, so a W
+//     fragment expanded in registers feeds 4 MFMAs, an A fragment read from
+//     LDS feeds 2, and the four partial tiles are summed through LDS at the
+//     end.
+//   * A is staged in LDS 4 k-steps (256 k) at a time, double-buffered, with
+//     one barrier per stage; the 16-byte piece p of row r sits at slot
+//     p ^ (r & 15), so the 16 rows of an MFMA fragment read hit distinct banks.
+//   * W is staged as packed bits (a 16-byte entry per row and k-step: two
+//     code words and the group scale); each lane reads the 8 bits of its B
+//     fragment and expands them in registers to f16 +-s (two ALU operations
+//     per pair of weights).  +-s times an f16
+//     activation is exact in the MFMA, so the result differs from the decode
+//     QMV only in fp32 summation order.
+//   * Blocks are numbered so that those resident on one XCD share their
+//     64-token A tile (the XCD's L2 keeps it) when the token tiles divide by 8.
 //   * Epilogues match the decode kernels: f16 store (Q/K/V), residual += (O,
 //     down), silu(a)*b of a gate/up pair stored as f16.
 #include "internal.h"
@@ -23,22 +33,45 @@ namespace {
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // register arrays of 16-byte pieces
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int BM = 64, BN = 64, BK = 64, LDS_STRIDE = BK + 8;  // halfs per B LDS row
-constexpr int GROUP = 4;  // K-steps whose global loads are issued together, one group ahead
+constexpr int BM = 64, BN = 64, BK = 64;
+constexpr int KQ = 4;                      // k-phases (waves along k)
+constexpr int SK = BK * KQ;                // k per LDS stage
+constexpr int PIECES = SK / 8;             // 16-byte pieces per A row and stage (32)
+constexpr int A_LOADS = BM * PIECES / 512; // pieces per thread and stage (4)
+constexpr int WROW = KQ + 1;               // W entries per LDS row (one of padding)
 
 // waitcnt immediate for gfx9: lgkmcnt = 0 only (the wave's LDS stores done)
 constexpr int LGKM0_IMM = 15 | (3 << 14) | (7 << 4);
 
 // Workgroup barrier for the pipelined loop: the wave's own LDS stores are
 // waited for, then s_barrier.  __syncthreads() would add a release fence,
-// which also waits for the next group's global loads still in flight.  The
+// which also waits for the next stage's global loads still in flight.  The
 // empty asm statements keep the compiler from moving LDS accesses across.
 __device__ __forceinline__ void step_barrier() {
     __builtin_amdgcn_s_waitcnt(LGKM0_IMM);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+}
+
+// Eight weight bits (k ascending from bit 0) -> the B fragment's eight f16
+// values: +s where the bit is set, -s where it is clear.  ns2 holds (-s, -s).
+// z2 = z | z << 15 carries the byte twice, so one shift by 15 - 2q brings bit
+// 2q to position 15 (low half's sign) and bit 2q+1 to position 31.
+__device__ __forceinline__ half8 expand_bits(uint32_t z, uint32_t ns2) {
+    // z2 is formed in asm so that the compiler does not fold the shifts below
+    // into 32-bit multiplies (quarter rate); each dword is then one shift and
+    // one three-input bit operation.
+    uint32_t z2;
+    asm("v_lshl_or_b32 %0, %1, 15, %1" : "=v"(z2) : "v"(z));
+    u32x4 e;
+    e[0] = ((z2 << 15) & 0x80008000u) ^ ns2;
+    e[1] = ((z2 << 13) & 0x80008000u) ^ ns2;
+    e[2] = ((z2 << 11) & 0x80008000u) ^ ns2;
+    e[3] = ((z2 << 9) & 0x80008000u) ^ ns2;
+    return __builtin_bit_cast(half8, e);
 }
 
 // Rows [0, rows0) of the launch come from matrix 0 (the kernel's codes0 /
@@ -58,21 +91,33 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const f16_t *A, const uint
                                                       const uint16_t *scales1, void *out,
                                                       uint32_t P, uint32_t M, uint32_t K,
                                                       uint32_t gs_log2, GemmSegs sg) {
-    // A tile of a K-step: 64 rows x 128 bytes, the eight 16-byte pieces of
-    // row r stored at slot (piece ^ (r & 7)) so the MFMA fragment reads (16
-    // rows, one piece each) spread over the banks.  B: dequantised W rows,
-    // padded by 16 bytes.  Both double-buffered by step parity.
-    __shared__ __attribute__((aligned(16))) f16_t As[2][BM * BK];
-    __shared__ __attribute__((aligned(16))) f16_t Bs[2][NMAT][BN * LDS_STRIDE];
-    // sign table: for a byte of weight bits, four words whose halves carry
-    // 0x8000 where the bit is clear -- XORed into (s, s) they give +-s
-    __shared__ __attribute__((aligned(16))) u32x4 sgn[256];
+    // Two A stages (64 rows x 256 k of f16 each); reused for the k-phase
+    // reduction after the main loop.
+    __shared__ __attribute__((aligned(16))) f16_t As[2][BM * SK];
+    // W per stage: for each matrix and row, one 16-byte entry per k-step
+    // (code words of its 64 k, scale), rows padded to WROW entries so the 16
+    // rows of a fragment read hit distinct banks.
+    __shared__ u32x4 Ws[2][NMAT][BN * WROW];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 2, wn = wave & 3;   // 8 waves: 2 x 4, each 32 rows x 16 columns
-    const uint32_t p0 = blockIdx.y * BM;
-    uint32_t n0 = blockIdx.x * BN;
+    const int wn = wave & 1, kq = wave >> 1;
+
+    // Block -> (W tile x, token tile y).  Workgroups are dispatched to the 8
+    // XCDs round-robin, so block L runs on XCD L % 8; with the token tiles a
+    // multiple of 8, XCD j gets token tiles j, j + 8, ... and all W tiles.
+    const uint32_t nx = M / BN, ny = ceil_div(P, BM), L = blockIdx.x;
+    uint32_t bx, by;
+    if ((ny & 7) == 0) {
+        const uint32_t slot = L >> 3;
+        by = 8 * (slot / nx) + (L & 7);
+        bx = slot % nx;
+    } else {
+        bx = L % nx;
+        by = L / nx;
+    }
+    const uint32_t p0 = by * BM;
+    uint32_t n0 = bx * BN;
     if (sg.n > 1) {   // row segments of up to three matrices, each with its own output
         if (n0 < sg.rows0) {
             M = sg.rows0;
@@ -91,143 +136,155 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const f16_t *A, const uint
         }
     }
     const uint32_t words_per_row = K / 32, groups_per_row = K >> gs_log2;
-    const uint32_t nk = K / BK;
-    if (tid < 256) {
-        const uint32_t b = tid;
-        u32x4 e;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            e[q] = (((b >> (2 * q)) & 1u) ? 0u : 0x8000u) | (((b >> (2 * q + 1)) & 1u) ? 0u : 0x80000000u);
-        sgn[b] = e;
-    }
+    const uint32_t nk = K / BK, nst = ceil_div(nk, (uint32_t)KQ);
 
-    float4v acc[NMAT][2];
+    float4v acc[NMAT][4][2];
 #pragma unroll
     for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-        for (int i = 0; i < 2; ++i) acc[m][i] = (float4v){0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[m][i][j] = (float4v){0.f, 0.f, 0.f, 0.f};
 
-    // Loader roles (per step): thread -> row tid/8 and piece tid%8: A's
-    // 16-byte piece (rows past P re-read row P-1, discarded at the store),
-    // W's 8 columns at 8*(tid%8).
-    const int lr = tid >> 3, lq = tid & 7, lc = lq * 8;
-    const f16_t *arow = A + (size_t)min(p0 + (uint32_t)lr, P - 1) * K + lc;
-    const uint32_t *wrow0 = codes0 + (size_t)(n0 + lr) * words_per_row;
-    const uint32_t *wrow1 = NMAT == 2 ? codes1 + (size_t)(n0 + lr) * words_per_row : wrow0;
-    const uint16_t *srow0 = scales0 + (size_t)(n0 + lr) * groups_per_row;
-    const uint16_t *srow1 = NMAT == 2 ? scales1 + (size_t)(n0 + lr) * groups_per_row : srow0;
-    const uint32_t ngroups = ceil_div(nk, (uint32_t)GROUP);
+    // A loader: piece (tid % 32) of rows tid / 32 + 16 u, u < 4 (rows past P
+    // re-read row P - 1, discarded at the store; k-steps past the end re-read
+    // the last one, never used).
+    const int lp = tid & (PIECES - 1), lr = tid / PIECES;
+    const f16_t *arow[A_LOADS];
+#pragma unroll
+    for (int u = 0; u < A_LOADS; ++u)
+        arow[u] = A + (size_t)min(p0 + (uint32_t)(lr + 16 * u), P - 1) * K + (lp & 7) * 8;
+    // W loader: thread t < 256 NMAT loads k-step t % 4 of the stage for row
+    // (t / 4) % 64 of matrix t / 256: the step's two code words and its scale.
+    const int wl_m = tid >> 8, wl_row = (tid >> 2) & 63, wl_q = tid & 3;
+    const bool wl = wl_m < NMAT;
+    const uint32_t *wl_codes = (NMAT == 2 && wl_m == 1 ? codes1 : codes0) +
+                               (size_t)(n0 + wl_row) * words_per_row;
+    const uint16_t *wl_scales = (NMAT == 2 && wl_m == 1 ? scales1 : scales0) +
+                                (size_t)(n0 + wl_row) * groups_per_row;
+    const int bsh = 8 * (lane >> 4);   // the lane's byte within a 32-k word
 
-    // One group's registers: A pieces, W words, scales (two sets, used in
-    // turn, so no register is copied).
-    u32x4 aA[GROUP], aB[GROUP];
-    uint32_t wA[GROUP][NMAT], wB[GROUP][NMAT];
-    uint32_t sA[GROUP][NMAT], sB[GROUP][NMAT];
-    auto issue = [&](u32x4 (&a)[GROUP], uint32_t (&w)[GROUP][NMAT], uint32_t (&sc)[GROUP][NMAT],
-                     uint32_t g) __attribute__((always_inline)) {
-        // steps past the last one re-read the last step (loads are never
-        // branched around; those steps are skipped in run_group)
+    // One stage in flight: A pieces and this thread's W entry, loaded at the
+    // start of the previous stage and stored to LDS at its end.
+    u32x4 areg[A_LOADS];
+    u32x2 wreg = {0u, 0u};
+    uint32_t sreg = 0;
+    auto issue = [&](uint32_t st) __attribute__((always_inline)) {
+        const uint32_t ka = min(st * KQ + (uint32_t)(lp >> 3), nk - 1) * BK;
 #pragma unroll
-        for (int t = 0; t < GROUP; ++t) a[t] = *(const u32x4 *)(arow + min(g * GROUP + t, nk - 1) * BK);
-#pragma unroll
-        for (int t = 0; t < GROUP; ++t) {
-            const uint32_t col = min(g * GROUP + t, nk - 1) * BK + lc;
-            w[t][0] = wrow0[col / 32];
-            sc[t][0] = srow0[col >> gs_log2];
-            if constexpr (NMAT == 2) {
-                w[t][1] = wrow1[col / 32];
-                sc[t][1] = srow1[col >> gs_log2];
-            }
+        for (int u = 0; u < A_LOADS; ++u) areg[u] = *(const u32x4 *)(arow[u] + ka);
+        if (wl) {
+            const uint32_t ks = min(st * KQ + (uint32_t)wl_q, nk - 1);
+            wreg = *(const u32x2 *)(wl_codes + 2 * ks);
+            sreg = wl_scales[(ks * BK) >> gs_log2];
         }
     };
-    // Stage step ks (registers -> LDS buffer ks & 1): the A piece swizzled,
-    // the byte of W bits expanded to +-s through the sign table.
-    auto stage = [&](const u32x4 &a, const uint32_t (&w)[NMAT], const uint32_t (&sc)[NMAT],
-                     uint32_t ks) __attribute__((always_inline)) {
-        const int buf = ks & 1;
-        ((u32x4 *)(As[buf] + lr * BK))[lq ^ (lr & 7)] = a;
+    auto stage = [&](uint32_t st) __attribute__((always_inline)) {
+        f16_t *buf = As[st & 1];
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m) {
-            const uint32_t byte = (w[m] >> (lc & 31)) & 0xFFu;
-            const uint32_t s2 = sc[m] | (sc[m] << 16);
-            *(u32x4 *)(Bs[buf][m] + lr * LDS_STRIDE + lc) = sgn[byte] ^ s2;
+        for (int u = 0; u < A_LOADS; ++u) {
+            const int r = lr + 16 * u;
+            ((u32x4 *)(buf + r * SK))[lp ^ (r & 15)] = areg[u];
         }
+        if (wl) Ws[st & 1][wl_m][wl_row * WROW + wl_q] = (u32x4){wreg[0], wreg[1], sreg, 0u};
     };
-    auto compute = [&](uint32_t ks) __attribute__((always_inline)) {
-        const int buf = ks & 1;
+    auto compute = [&](uint32_t st) __attribute__((always_inline)) {
+        if (st * KQ + kq >= nk) return;   // wave-uniform
+        const f16_t *buf = As[st & 1];
+        uint32_t w[NMAT][2][2], ns2[NMAT][2];
 #pragma unroll
-        for (int kk = 0; kk < BK; kk += 32) {
-            const int piece = kk / 8 + (lane >> 4);
-            half8 af[2];
+        for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int r = wm * 32 + i * 16 + (lane & 15);
-                af[i] = *(const half8 *)(As[buf] + r * BK + 8 * (piece ^ (r & 7)));
+            for (int j = 0; j < 2; ++j) {
+                const u32x4 e = Ws[st & 1][m][(32 * wn + 16 * j + (lane & 15)) * WROW + kq];
+                w[m][j][0] = e[0];
+                w[m][j][1] = e[1];
+                ns2[m][j] = (e[2] | (e[2] << 16)) ^ 0x80008000u;
             }
 #pragma unroll
-            for (int m = 0; m < NMAT; ++m) {
-                const half8 bf = *(const half8 *)(Bs[buf][m] + (wn * 16 + (lane & 15)) * LDS_STRIDE +
-                                                  kk + 8 * (lane >> 4));
+        for (int kk = 0; kk < 2; ++kk) {
+            const int piece = kq * 8 + kk * 4 + (lane >> 4);
+            half8 af[4];
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
-                    acc[m][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf, acc[m][i], 0, 0, 0);
+            for (int i = 0; i < 4; ++i) {
+                const int r = i * 16 + (lane & 15);
+                af[i] = *(const half8 *)(buf + r * SK + 8 * (piece ^ (r & 15)));
             }
-        }
-    };
-    // Steps 4g..4g+3 of group g (registers `cur`): each iteration stages
-    // the NEXT step (from `cur`, or for the last one from `nxt`, the next
-    // group's set) while the MFMAs of the current step run, then one
-    // barrier.  The buffer a step stages into was last read two steps
-    // earlier, before the previous barrier.  Steps past the end are skipped
-    // (block-uniform).
-    auto run_group = [&](const u32x4 (&ca)[GROUP], const uint32_t (&cw)[GROUP][NMAT],
-                         const uint32_t (&cs)[GROUP][NMAT], const u32x4 (&na)[GROUP],
-                         const uint32_t (&nw)[GROUP][NMAT], const uint32_t (&ns)[GROUP][NMAT],
-                         uint32_t g) __attribute__((always_inline)) {
 #pragma unroll
-        for (int t = 0; t < GROUP; ++t) {
-            const uint32_t ks = g * GROUP + t;
-            if (ks >= nk) break;   // block-uniform
-            if (ks + 1 < nk) {
-                if (t + 1 < GROUP) stage(ca[t + 1], cw[t + 1], cs[t + 1], ks + 1);
-                else stage(na[0], nw[0], ns[0], ks + 1);
-            }
-            compute(ks);
-            step_barrier();
+            for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const half8 bf = expand_bits((w[m][j][kk] >> bsh) & 0xFFu, ns2[m][j]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        acc[m][i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf, acc[m][i][j], 0, 0, 0);
+                }
         }
     };
 
-    // Group pipeline: the loads of group g+1 are issued before group g's
-    // steps run, so they have a group's worth of compute to arrive.  Two
-    // groups per pass, the register sets in turn.
-    static_assert(GROUP % 2 == 0, "step parity across groups");
-    issue(aA, wA, sA, 0);
-    step_barrier();   // the sign table
-    stage(aA[0], wA[0], sA[0], 0);
+    // Stage pipeline: stage st + 1's loads are issued before stage st is
+    // computed and stored to the other LDS buffers after it (those were last
+    // read in stage st - 1, before the previous barrier).
+    issue(0);
+    stage(0);
     step_barrier();
-    for (uint32_t g = 0; g < ngroups; g += 2) {
-        issue(aB, wB, sB, g + 1);
-        run_group(aA, wA, sA, aB, wB, sB, g);
-        issue(aA, wA, sA, g + 2);
-        run_group(aB, wB, sB, aA, wA, sA, g + 1);
+    for (uint32_t st = 0; st < nst; ++st) {
+        if (st + 1 < nst) issue(st + 1);   // block-uniform
+        compute(st);
+        if (st + 1 < nst) stage(st + 1);
+        step_barrier();
     }
+
+    // k-phase reduction through LDS (the stage buffers are free): phases 2, 3
+    // hand their tiles to 0, 1, then phase 1 to phase 0.  Slot layout: one
+    // float4 per (fragment, lane), lanes adjacent.
+    constexpr int NF = NMAT * 8;
+    float4v *red = (float4v *)&As[0][0];
+    auto put = [&](int slot) __attribute__((always_inline)) {
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) red[(slot * NF + (m * 8 + i * 2 + j)) * 64 + lane] = acc[m][i][j];
+    };
+    auto add = [&](int slot) __attribute__((always_inline)) {
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[m][i][j] += red[(slot * NF + (m * 8 + i * 2 + j)) * 64 + lane];
+    };
+    static_assert(4 * NF * 64 * 16 <= (int)sizeof(As), "reduction slots fit the stage buffers");
+    if (kq >= 2) put((kq - 2) * 2 + wn);
+    __syncthreads();
+    if (kq < 2) add(kq * 2 + wn);
+    __syncthreads();
+    if (kq == 1) put(wn);
+    __syncthreads();
+    if (kq != 0) return;   // after the last barrier
+    add(wn);
 
     // D layout: lane holds rows 4*(lane/16)+r, column lane%16 of each 16x16 tile.
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const uint32_t p = p0 + wm * 32 + i * 16 + 4 * (lane >> 4) + r;
-            const uint32_t n = n0 + wn * 16 + (lane & 15);
+            const uint32_t p = p0 + i * 16 + 4 * (lane >> 4) + r;
             if (p >= P) continue;
-            const size_t o = (size_t)p * M + n;
-            const float c = acc[0][i][r];
-            if constexpr (MODE == NNZ_GEMM_STORE_F16) ((f16_t *)out)[o] = (f16_t)c;
-            else if constexpr (MODE == NNZ_GEMM_STORE_F32) ((float *)out)[o] = c;
-            else if constexpr (MODE == NNZ_GEMM_RESADD) ((float *)out)[o] += c;
-            else {
-                const float u = acc[NMAT - 1][i][r];
-                ((f16_t *)out)[o] = (f16_t)(c / (1.f + expf(-c)) * u);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t n = n0 + 32 * wn + 16 * j + (lane & 15);
+                const size_t o = (size_t)p * M + n;
+                const float c = acc[0][i][j][r];
+                if constexpr (MODE == NNZ_GEMM_STORE_F16) ((f16_t *)out)[o] = (f16_t)c;
+                else if constexpr (MODE == NNZ_GEMM_STORE_F32) ((float *)out)[o] = c;
+                else if constexpr (MODE == NNZ_GEMM_RESADD) ((float *)out)[o] += c;
+                else {
+                    const float u = acc[NMAT - 1][i][j][r];
+                    ((f16_t *)out)[o] = (f16_t)(c / (1.f + expf(-c)) * u);
+                }
             }
         }
 }
@@ -245,6 +302,8 @@ int nnz_gemm_launch(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, 
                          d.K % d.group_size == 0,
                 NNZ_EUNSUPPORTED, "dequant_gemm: need M %% 64 == 0, K %% 64 == 0, group size %% 64 == 0");
     NNZ_REQUIRE(ctx, ((uintptr_t)a & 15) == 0, NNZ_EINVAL, "dequant_gemm: A must be 16-byte aligned");
+    NNZ_REQUIRE(ctx, ((uintptr_t)wa->codes & 7) == 0 && (!wb || ((uintptr_t)wb->codes & 7) == 0),
+                NNZ_EINVAL, "dequant_gemm: codes must be 8-byte aligned");
     const bool pair = mode == NNZ_GEMM_SILU_PAIR;
     if (pair) {
         NNZ_REQUIRE(ctx, wb && wb->bits == 1 && wb->codes && wb->scales &&
@@ -255,7 +314,7 @@ int nnz_gemm_launch(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, 
     NNZ_REQUIRE(ctx, (d.group_size & (d.group_size - 1)) == 0, NNZ_EUNSUPPORTED,
                 "dequant_gemm: group size must be a power of two");
     const uint32_t gl = (uint32_t)__builtin_ctz(d.group_size);
-    dim3 grid(d.M / BN, ceil_div(P, BM));
+    const uint32_t grid = d.M / BN * ceil_div(P, BM);
     const f16_t *A = (const f16_t *)a;
     const uint32_t *c0 = (const uint32_t *)wa->codes;
     const uint16_t *s0 = (const uint16_t *)wa->scales;
@@ -294,6 +353,8 @@ int nnz_gemm_segments_launch(nnz_ctx *ctx, const nnz_qweight *const *w, void *co
         NNZ_REQUIRE(ctx, w[i] && out[i] && w[i]->bits == 1 && w[i]->codes && w[i]->scales &&
                              w[i]->group_size == group_size && w[i]->packed_count % K == 0,
                     NNZ_EINVAL, "gemm_segments: bad weight %d", i);
+        NNZ_REQUIRE(ctx, ((uintptr_t)w[i]->codes & 7) == 0, NNZ_EINVAL,
+                    "gemm_segments: codes must be 8-byte aligned");
         rows[i] = w[i]->packed_count / K;
         NNZ_REQUIRE(ctx, rows[i] % BN == 0, NNZ_EUNSUPPORTED, "gemm_segments: rows %% 64 != 0");
         M += rows[i];
@@ -304,7 +365,7 @@ int nnz_gemm_segments_launch(nnz_ctx *ctx, const nnz_qweight *const *w, void *co
                 nw > 1 ? (const uint16_t *)w[1]->scales : nullptr,
                 nw > 2 ? (const uint16_t *)w[2]->scales : nullptr,
                 nw > 1 ? out[1] : nullptr, nw > 2 ? out[2] : nullptr};
-    dim3 grid(M / BN, ceil_div(P, BM));
+    const uint32_t grid = M / BN * ceil_div(P, BM);
     dq_gemm_kernel<NNZ_GEMM_STORE_F16, 1><<<grid, 512, 0, ctx->stream>>>(
         (const f16_t *)a, (const uint32_t *)w[0]->codes, (const uint16_t *)w[0]->scales, nullptr,
         nullptr, out[0], P, M, K, (uint32_t)__builtin_ctz(group_size), sg);

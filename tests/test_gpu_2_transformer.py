@@ -361,6 +361,25 @@ def test_dequant_gemm_modes(dev, P):
     assert_close(host(out16), O.f16(O.silu(ra) * rb), what="gemm silu pair")
 
 
+@pytest.mark.parametrize("P,M,K,gs", [(100, 192, 2112, 64), (512, 128, 6144, 128),
+                                       (64, 64, 192, 64), (1024, 64, 320, 64)])
+def test_dequant_gemm_shapes(dev, P, M, K, gs):
+    """K not a multiple of the 256-k stage (last stage partial), group size 64,
+    token tiles that do and do not divide by 8, and the silu pair."""
+    wa, wb = cf.q1_matrix(M, K, gs, 490, 491), cf.q1_matrix(M, K, gs, 492, 493)
+    a16 = (0.5 * S.normal(494, P * K)).astype(np.float16).reshape(P, K)
+    A = a16.astype(np.float64)
+    da, db = ops.DeviceQWeight(dev, wa), ops.DeviceQWeight(dev, wb)
+    ra, rb = A @ O.dequant(wa).T, A @ O.dequant(wb).T
+    out32 = torch.empty(P, M, dtype=torch.float32, device="cuda")
+    ops.dispatch_dequant_gemm(dev, da, tdev(a16), out32, L.GEMM_STORE_F32)
+    out16 = torch.empty(P, M, dtype=torch.float16, device="cuda")
+    ops.dispatch_dequant_gemm(dev, da, tdev(a16), out16, L.GEMM_SILU_PAIR, wb=db)
+    dev.sync()
+    assert_close(host(out32), ra, what="gemm f32")
+    assert_close(host(out16), O.f16(O.silu(ra) * rb), what="gemm silu pair")
+
+
 def test_gemm_row_equals_decode_qmv(dev):
     """Per-token equivalence: GEMM row p equals the decode QMV of token p."""
     M, K, P = 512, 2048, 8

@@ -80,6 +80,63 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float *in, const fl
     }
 }
 
+// Rows of 256 V floats (hidden 256 .. 4096): one wave per row holding the row
+// in registers (V float4 per lane, adjacent lanes on adjacent 16-byte pieces),
+// the sum of squares reduced across the wave without LDS or barriers.  Same
+// expression as rms_norm_kernel; only the fp32 summation order differs.
+template <int ODT, bool TRUNC, int V>
+__global__ __launch_bounds__(64) void rms_norm_rows_kernel(const float *in, const float *scale,
+                                                            void *out, uint32_t rows, float eps) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    constexpr uint32_t n = 256 * V;
+    const uint32_t row = blockIdx.x, lane = threadIdx.x;
+    const f4 *x = (const f4 *)(in + (size_t)row * n) + lane;
+    const f4 *sc = (const f4 *)scale + lane;
+    f4 v[V], w[V];   // the norm weights are loaded with the row, not after the reduction
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) v[i] = x[64 * i];
+#pragma unroll
+    for (int i = 0; i < V; ++i) w[i] = sc[64 * i];
+#pragma unroll
+    for (int i = 0; i < V; ++i) ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+    const float rms = rsqrtf(wave_sum(ss) / (float)n + eps);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+        f4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float t = v[i][e] * rms * w[i][e];
+            if constexpr (TRUNC) t = bf16_trunc(t);
+            y[e] = t;
+        }
+        const size_t o = (size_t)row * n / 4 + lane + 64 * i;   // in 4-element units
+        if constexpr (ODT == NNZ_F32) ((f4 *)out)[o] = y;
+        else ((h4 *)out)[o] = (h4){(_Float16)y[0], (_Float16)y[1], (_Float16)y[2], (_Float16)y[3]};
+    }
+}
+
+template <int ODT, bool TRUNC>
+void launch_rms_norm(nnz_ctx *ctx, const float *in, const float *scale, void *out, uint32_t n,
+                     uint32_t rows, float eps) {
+    const bool vec = n % 256 == 0 && n <= 4096 && ((uintptr_t)in & 15) == 0 &&
+                     ((uintptr_t)scale & 15) == 0 && ((uintptr_t)out & 15) == 0;
+    if (!vec) {
+        rms_norm_kernel<ODT, TRUNC><<<rows, 256, 0, ctx->stream>>>(in, scale, out, n, eps);
+        return;
+    }
+    const uint32_t g = rows;   // one single-wave workgroup per row, spread over every CU
+    switch (n / 256) {
+#define NNZ_RMS_CASE(V) \
+    case V: rms_norm_rows_kernel<ODT, TRUNC, V><<<g, 64, 0, ctx->stream>>>(in, scale, out, rows, eps); break;
+        NNZ_RMS_CASE(1) NNZ_RMS_CASE(2) NNZ_RMS_CASE(3) NNZ_RMS_CASE(4) NNZ_RMS_CASE(5) NNZ_RMS_CASE(6)
+        NNZ_RMS_CASE(7) NNZ_RMS_CASE(8) NNZ_RMS_CASE(9) NNZ_RMS_CASE(10) NNZ_RMS_CASE(11) NNZ_RMS_CASE(12)
+        NNZ_RMS_CASE(13) NNZ_RMS_CASE(14) NNZ_RMS_CASE(15) NNZ_RMS_CASE(16)
+#undef NNZ_RMS_CASE
+    }
+}
+
 // ------------------------------------------------------------------- SiLU --
 __global__ void silu_kernel(const float *in, float *out, uint32_t n) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -1614,13 +1671,12 @@ int nnz_dispatch_rms_norm(nnz_ctx *ctx, const float *input, const float *scale, 
     NNZ_CHECK_CTX(ctx);
     NNZ_REQUIRE(ctx, input && scale && output, NNZ_EINVAL, "rms_norm: null buffer");
     NNZ_REQUIRE(ctx, d.hidden_size > 0 && d.num_tokens > 0, NNZ_EINVAL, "rms_norm: zero dims");
-    dim3 g(d.num_tokens);
     if (out_dtype == NNZ_F32 && !trunc)
-        rms_norm_kernel<NNZ_F32, false><<<g, 256, 0, ctx->stream>>>(input, scale, output, d.hidden_size, d.eps);
+        launch_rms_norm<NNZ_F32, false>(ctx, input, scale, output, d.hidden_size, d.num_tokens, d.eps);
     else if (out_dtype == NNZ_F16 && !trunc)
-        rms_norm_kernel<NNZ_F16, false><<<g, 256, 0, ctx->stream>>>(input, scale, output, d.hidden_size, d.eps);
+        launch_rms_norm<NNZ_F16, false>(ctx, input, scale, output, d.hidden_size, d.num_tokens, d.eps);
     else if (out_dtype == NNZ_F16 && trunc)
-        rms_norm_kernel<NNZ_F16, true><<<g, 256, 0, ctx->stream>>>(input, scale, output, d.hidden_size, d.eps);
+        launch_rms_norm<NNZ_F16, true>(ctx, input, scale, output, d.hidden_size, d.num_tokens, d.eps);
     else
         return nnz_fail(ctx, NNZ_EINVAL, "rms_norm: unsupported output variant");
     NNZ_LAUNCHED(ctx);

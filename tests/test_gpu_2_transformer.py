@@ -202,8 +202,10 @@ def test_attention_partials_merged_o_projection(dev, pos, freq_table):
 
 # ------------------------------------------------------------------ norms ---
 @pytest.mark.parametrize("variant", ["f32", "f16", "bf16_f16"])
-def test_rms_norm_variants(dev, variant):
-    H, T = 2048, 3
+@pytest.mark.parametrize("H,T", [(2048, 3), (2560, 5), (4096, 9), (200, 2), (512, 513)])
+def test_rms_norm_variants(dev, variant, H, T):
+    """Wave-per-row path (hidden a multiple of 256 up to 4096, any row count)
+    and the block-per-row path (hidden 200)."""
     x = S.normal(420, H * T).astype(np.float32)
     w = (1 + 0.1 * S.normal(421, H)).astype(np.float32)
     odt = torch.float32 if variant == "f32" else torch.float16

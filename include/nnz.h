@@ -422,13 +422,23 @@ typedef struct {
     uint32_t num_query_heads, num_kv_heads, head_dim, max_context_length;
     uint32_t max_prefill_length, group_size;
     float rope_theta, rms_eps;
-    uint32_t embed_kind;   /* NNZ_EMBED_Q1 or NNZ_EMBED_BF16 */
-    uint32_t lm_head_kind; /* NNZ_LMHEAD_Q1 (own 1-bit matrix) or NNZ_LMHEAD_TIED_BF16 */
+    uint32_t embed_kind;   /* NNZ_EMBED_Q1, NNZ_EMBED_BF16 or NNZ_EMBED_Q4 */
+    uint32_t lm_head_kind; /* NNZ_LMHEAD_Q1 (own 1-bit matrix), NNZ_LMHEAD_TIED_BF16 or NNZ_LMHEAD_Q4 */
+    /* transformer.zig:35-55 QuantFormat: NNZ_QUANT_Q1 (q1_0: 1-bit, f16
+     * scales) or NNZ_QUANT_Q4 (q4_mlx: 4-bit affine, raw bf16 scales and
+     * biases; the reference's BF16-faithful rounding points, transformer.zig
+     * :2646, :2743, :2977, :3100).  Q4 models take NNZ_EMBED_Q4 and
+     * NNZ_LMHEAD_Q4 (a tied checkpoint uploads its embedding into the head). */
+    uint32_t quant_format;
 } nnz_model_config;
 #define NNZ_EMBED_Q1 0
 #define NNZ_EMBED_BF16 1
+#define NNZ_EMBED_Q4 2
 #define NNZ_LMHEAD_Q1 0
 #define NNZ_LMHEAD_TIED_BF16 1
+#define NNZ_LMHEAD_Q4 2
+#define NNZ_QUANT_Q1 0
+#define NNZ_QUANT_Q4 1
 
 /* Tensor ids for nnz_model_tensor (per-layer ids take `layer`). */
 #define NNZ_T_EMBED_CODES 0   /* Q1: uint32 codes; BF16: the bf16 table       */
@@ -436,6 +446,8 @@ typedef struct {
 #define NNZ_T_LM_CODES 2
 #define NNZ_T_LM_SCALES 3
 #define NNZ_T_FINAL_NORM 4    /* f32 [hidden]                                  */
+#define NNZ_T_EMBED_BIASES 5  /* Q4 only: bf16 (scales likewise bf16 for Q4)   */
+#define NNZ_T_LM_BIASES 6     /* Q4 only                                       */
 #define NNZ_T_Q_CODES 10
 #define NNZ_T_Q_SCALES 11
 #define NNZ_T_K_CODES 12
@@ -456,6 +468,13 @@ typedef struct {
 #define NNZ_T_K_NORM 27       /* f32 [head_dim] */
 #define NNZ_T_K_CACHE 30      /* f16 [Hkv][max_ctx][D]  */
 #define NNZ_T_V_CACHE 31      /* f16 [Hkv][D][max_ctx]  */
+#define NNZ_T_Q_BIASES 50     /* Q4 only: bf16 biases of each projection      */
+#define NNZ_T_K_BIASES 51
+#define NNZ_T_V_BIASES 52
+#define NNZ_T_O_BIASES 53
+#define NNZ_T_GATE_BIASES 54
+#define NNZ_T_UP_BIASES 55
+#define NNZ_T_DOWN_BIASES 56
 #define NNZ_T_LOGITS 40       /* f32 [vocab]            */
 #define NNZ_T_RESIDUAL 41     /* f32 [hidden]           */
 
@@ -473,7 +492,8 @@ int nnz_model_forward_decode(nnz_model *m, uint32_t token_id, uint32_t position)
 /* Batched prefill (new; the reference prefills token by token through
  * forwardDecode, transformer.zig:4032-4068): tokens[0..n) at positions
  * start..start+n-1 via the dequant-GEMM; leaves the last token's logits in
- * NNZ_T_LOGITS.  `tokens_host` is a host array. */
+ * NNZ_T_LOGITS.  `tokens_host` is a host array.  Q4 models run the prompt
+ * token by token through the decode step, as the reference does. */
 int nnz_model_prefill(nnz_model *m, const uint32_t *tokens_host, uint32_t n, uint32_t start);
 /* generate (transformer.zig:3942): prefill the prompt, then up to `n_new`
  * decode steps; each step is one replay of a captured hipGraph that picks

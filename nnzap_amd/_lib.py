@@ -16,8 +16,9 @@ HEADER = HERE.parent / "include" / "nnz.h"
 OK, EINVAL, EUNSUPPORTED, EHIP, ENOMEM, ETIMEOUT, ESTATE = 0, -1, -2, -3, -4, -5, -6
 F32, F16, BF16 = 0, 1, 2
 GEMM_STORE_F16, GEMM_STORE_F32, GEMM_RESADD, GEMM_SILU_PAIR = 0, 1, 2, 3
-EMBED_Q1, EMBED_BF16 = 0, 1
-LMHEAD_Q1, LMHEAD_TIED_BF16 = 0, 1
+EMBED_Q1, EMBED_BF16, EMBED_Q4 = 0, 1, 2
+LMHEAD_Q1, LMHEAD_TIED_BF16, LMHEAD_Q4 = 0, 1, 2
+QUANT_FORMAT_Q1, QUANT_FORMAT_Q4 = 0, 1
 
 u32, f32, vp, i32, sz = C.c_uint32, C.c_float, C.c_void_p, C.c_int32, C.c_size_t
 
@@ -86,7 +87,7 @@ class ModelConfig(C.Structure):
                 ("num_layers", u32), ("num_query_heads", u32), ("num_kv_heads", u32),
                 ("head_dim", u32), ("max_context_length", u32), ("max_prefill_length", u32),
                 ("group_size", u32), ("rope_theta", f32), ("rms_eps", f32),
-                ("embed_kind", u32), ("lm_head_kind", u32)]
+                ("embed_kind", u32), ("lm_head_kind", u32), ("quant_format", u32)]
 
 
 P = C.POINTER

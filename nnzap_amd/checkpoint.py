@@ -228,5 +228,6 @@ def config_from_hf(config: dict | str | os.PathLike, max_context_length: int = 3
         group_size=int(q.get("group_size", 128 if bits == 1 else 64)),
         rope_theta=float(config.get("rope_theta", 1e6)),
         rms_eps=float(config.get("rms_norm_eps", 1e-6)),
-        embed_kind=0, lm_head_kind=0)
+        embed_kind=0 if bits == 1 else 2, lm_head_kind=0 if bits == 1 else 2,
+        quant_format=0 if bits == 1 else 1)
     return cfg, (QUANT_Q1 if bits == 1 else QUANT_Q4), bool(config.get("tie_word_embeddings", True))

@@ -91,8 +91,9 @@ class DecoderConfig:
     group_size: int = 128
     rope_theta: float = 1_000_000.0
     rms_eps: float = 1e-6
-    embed_kind: int = 1      # EMBED_BF16
-    lm_head_kind: int = 0    # LMHEAD_Q1 (own 1-bit matrix); 1 = tied bf16 table
+    embed_kind: int = 1      # EMBED_BF16; 0 = EMBED_Q1, 2 = EMBED_Q4
+    lm_head_kind: int = 0    # LMHEAD_Q1 (own 1-bit matrix); 1 = tied bf16 table; 2 = LMHEAD_Q4
+    quant_format: int = 0    # 0 = q1_0 (1-bit), 1 = q4_mlx (4-bit affine, bf16 scales/biases)
 
     @property
     def qdim(self):
@@ -109,6 +110,13 @@ BONSAI_1_7B = DecoderConfig()
 TINY = DecoderConfig(vocab_size=512, hidden_size=256, intermediate_size=512, num_layers=2,
                      num_query_heads=4, num_kv_heads=2, head_dim=64, max_context_length=256,
                      max_prefill_length=64, group_size=128, rope_theta=10000.0)
+
+# The same tiny shape as a q4_mlx model (Bonsai*_Q4 presets,
+# transformer.zig:336-382: group size 64, Q4 embedding tied to the LM head).
+TINY_Q4 = DecoderConfig(vocab_size=512, hidden_size=256, intermediate_size=512, num_layers=2,
+                        num_query_heads=4, num_kv_heads=2, head_dim=64, max_context_length=256,
+                        max_prefill_length=64, group_size=64, rope_theta=10000.0,
+                        embed_kind=2, lm_head_kind=2, quant_format=1)
 
 PROJS = ("q", "k", "v", "o", "gate", "up", "down")
 
@@ -128,7 +136,7 @@ def tensor_seed(layer: int, slot: int) -> int:
 class DecoderWeights:
     cfg: DecoderConfig
     embed_bf16: np.ndarray | None = None      # uint16 [V, H]
-    embed_q1: QWeight | None = None
+    embed_q1: QWeight | None = None           # quantised table (1-bit, or 4-bit for q4_mlx)
     lm_head: QWeight | None = None
     final_norm: np.ndarray | None = None      # f32 [H]
     layers: list = field(default_factory=list)  # dicts: q..down (QWeight), norms (f32)
@@ -150,6 +158,8 @@ def decoder_weights(cfg: DecoderConfig, norm_mode: str = "small",
     stream, nnz_synth_normal_bf16; the oracle regenerates single rows)."""
     dw = DecoderWeights(cfg)
     V, H = cfg.vocab_size, cfg.hidden_size
+    if cfg.quant_format == 1:
+        return _decoder_weights_q4(cfg, norm_mode)
     if host_embed or cfg.lm_head_kind == 1:
         dw.embed_bf16 = S.f64_to_bf16_bits(0.02 * S.normal(S.SEED_MODEL_BASE + 0, V * H)).reshape(V, H)
     if cfg.lm_head_kind == 0:
@@ -165,6 +175,29 @@ def decoder_weights(cfg: DecoderConfig, norm_mode: str = "small",
         layer["ffn_norm"] = norm_weights(tensor_seed(l, 21), H, norm_mode)
         layer["q_norm"] = norm_weights(tensor_seed(l, 22), cfg.head_dim, norm_mode)
         layer["k_norm"] = norm_weights(tensor_seed(l, 23), cfg.head_dim, norm_mode)
+        dw.layers.append(layer)
+    return dw
+
+
+def _decoder_weights_q4(cfg: DecoderConfig, norm_mode: str) -> DecoderWeights:
+    """Synthetic q4_mlx decoder: every projection and the (tied) embedding a
+    4-bit affine matrix with raw bf16 scales and biases."""
+    dw = DecoderWeights(cfg)
+    V, H, gs = cfg.vocab_size, cfg.hidden_size, cfg.group_size
+    dw.embed_q1 = q4_matrix(V, H, gs, S.SEED_MODEL_BASE + 0, S.SEED_MODEL_BASE + 1,
+                            S.SEED_MODEL_BASE + 2, scale_dtype=DT_BF16)
+    dw.lm_head = dw.embed_q1
+    dw.final_norm = norm_weights(S.SEED_MODEL_BASE + 3, H, norm_mode)
+    for l in range(cfg.num_layers):
+        layer = {}
+        for i, name in enumerate(PROJS):
+            M, K = proj_shape(cfg, name)
+            layer[name] = q4_matrix(M, K, gs, tensor_seed(l, 3 * i), tensor_seed(l, 3 * i + 1),
+                                    tensor_seed(l, 3 * i + 2), scale_dtype=DT_BF16)
+        layer["attn_norm"] = norm_weights(tensor_seed(l, 40), H, norm_mode)
+        layer["ffn_norm"] = norm_weights(tensor_seed(l, 41), H, norm_mode)
+        layer["q_norm"] = norm_weights(tensor_seed(l, 42), cfg.head_dim, norm_mode)
+        layer["k_norm"] = norm_weights(tensor_seed(l, 43), cfg.head_dim, norm_mode)
         dw.layers.append(layer)
     return dw
 

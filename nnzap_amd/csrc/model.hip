@@ -67,6 +67,15 @@ __global__ void embed_state_bf16_kernel(const uint32_t *state, const uint16_t *t
     out[d] = bf16_to_f32(table[(size_t)row * hidden + d]);
 }
 
+// State block for prompt token t of a token-by-token prefill.
+__global__ void prefill_state_kernel(uint32_t *state, const uint32_t *ids, uint32_t t, uint32_t start) {
+    state[ST_TOKEN] = ids[t];
+    state[ST_POS] = start + t;
+    state[ST_SEQ] = start + t + 1;
+    state[ST_STEP] = 0;
+    state[ST_DONE] = 0;
+}
+
 __global__ void embed_ids_q1_kernel(const uint32_t *ids, const uint8_t *bits, const uint16_t *scales,
                                     float *out, uint32_t hidden, uint32_t ntok, uint32_t gs,
                                     uint32_t vocab) {
@@ -188,7 +197,7 @@ __global__ __launch_bounds__(256) void argmax_final_advance_kernel(const Top2 *p
 }
 
 struct Proj {
-    void *codes = nullptr, *scales = nullptr;
+    void *codes = nullptr, *scales = nullptr, *biases = nullptr;
     uint32_t M = 0, K = 0;
     nnz_qweight w{};
 };
@@ -206,7 +215,7 @@ struct nnz_model {
     nnz_model_config c{};
     uint32_t qdim = 0, kvdim = 0, G = 0;
     std::vector<Layer> L;
-    void *emb = nullptr, *emb_scales = nullptr;
+    void *emb = nullptr, *emb_scales = nullptr, *emb_biases = nullptr;
     Proj lm;
     float *final_norm = nullptr;
     // decode activations
@@ -259,18 +268,26 @@ int model_alloc(nnz_model *m, size_t bytes, void **out) {
         (ptr) = (decltype(ptr))p_;                                           \
     } while (0)
 
+bool is_q4(const nnz_model *m) { return m->c.quant_format == NNZ_QUANT_Q4; }
+
+// Q1: bits + f16 scales.  Q4 (MLX affine): nibbles + raw bf16 scales and
+// biases (model.zig:962-1026 loadQ4Projection keeps them as BF16).
+size_t codes_bytes(const nnz_model *m, size_t n) { return is_q4(m) ? n / 2 : n / 8; }
+
 int alloc_proj(nnz_model *m, Proj &p, uint32_t M, uint32_t K) {
     p.M = M;
     p.K = K;
-    MALLOC(p.codes, (size_t)M * K / 8);
-    MALLOC(p.scales, (size_t)M * K / m->c.group_size * 2);
+    const size_t groups = (size_t)M * K / m->c.group_size;
+    MALLOC(p.codes, codes_bytes(m, (size_t)M * K));
+    MALLOC(p.scales, groups * 2);
+    if (is_q4(m)) MALLOC(p.biases, groups * 2);
     p.w.codes = p.codes;
     p.w.scales = p.scales;
-    p.w.biases = nullptr;
+    p.w.biases = p.biases;
     p.w.packed_count = M * K;
     p.w.group_size = m->c.group_size;
-    p.w.bits = 1;
-    p.w.scale_dtype = NNZ_F16;
+    p.w.bits = is_q4(m) ? 4 : 1;
+    p.w.scale_dtype = is_q4(m) ? NNZ_BF16 : NNZ_F16;
     return NNZ_OK;
 }
 
@@ -282,6 +299,8 @@ nnz_gqa_dims gqa_dims(const nnz_model *m, uint32_t seq) {
 }
 
 int lm_head(nnz_model *m, const f16_t *x, float *logits) {
+    if (m->c.lm_head_kind == NNZ_LMHEAD_Q4)
+        return nnz_dispatch_q4mv_f16in(m->ctx, &m->lm.w, x, logits, dims_of(m, m->lm));
     if (m->c.lm_head_kind == NNZ_LMHEAD_Q1)
         return nnz_dispatch_qmv_f16in(m->ctx, &m->lm.w, x, logits, dims_of(m, m->lm));
     const uint32_t K = m->c.hidden_size, units = K / 32;
@@ -319,14 +338,21 @@ int enqueue_decode_step(nnz_model *m, uint32_t max_seq) {
     nnz_ctx *ctx = m->ctx;
     const nnz_model_config &c = m->c;
     const uint32_t H = c.hidden_size;
-    if (c.embed_kind == NNZ_EMBED_Q1)
-        embed_state_q1_kernel<<<ceil_div(H, 256), 256, 0, ctx->stream>>>(
-            m->state, (const uint8_t *)m->emb, (const uint16_t *)m->emb_scales, m->residual, H,
-            c.group_size, c.vocab_size);
-    else
-        embed_state_bf16_kernel<<<ceil_div(H, 256), 256, 0, ctx->stream>>>(
-            m->state, (const uint16_t *)m->emb, m->residual, H, c.vocab_size);
-    NNZ_LAUNCHED(ctx);
+    if (c.embed_kind == NNZ_EMBED_Q4) {
+        // transformer.zig:2646-2668 (Q4 branch): embedding_lookup_q4
+        RC(nnz_dispatch_embedding_lookup_q4(ctx, m->state + ST_TOKEN, m->emb, m->emb_scales,
+                                            m->emb_biases, m->residual,
+                                            {c.vocab_size, H, 1, c.group_size}));
+    } else {
+        if (c.embed_kind == NNZ_EMBED_Q1)
+            embed_state_q1_kernel<<<ceil_div(H, 256), 256, 0, ctx->stream>>>(
+                m->state, (const uint8_t *)m->emb, (const uint16_t *)m->emb_scales, m->residual, H,
+                c.group_size, c.vocab_size);
+        else
+            embed_state_bf16_kernel<<<ceil_div(H, 256), 256, 0, ctx->stream>>>(
+                m->state, (const uint16_t *)m->emb, m->residual, H, c.vocab_size);
+        NNZ_LAUNCHED(ctx);
+    }
 
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         Layer &Ly = m->L[l];
@@ -348,16 +374,24 @@ int enqueue_decode_step(nnz_model *m, uint32_t max_seq) {
             RC(nnz_qmv_merge_resadd_launch(ctx, &Ly.o.w, m->part_o, m->part_ml, m->state + ST_SEQ,
                                            max_seq, nch, nnz_attn_fused_chunk(max_seq, c.num_kv_heads),
                                            c.head_dim, m->residual, dims_of(m, Ly.o)));
+        else if (is_q4(m))
+            RC(nnz_dispatch_q4mv_f16io_resadd(ctx, &Ly.o.w, m->att, m->residual, dims_of(m, Ly.o)));
         else
             RC(nnz_dispatch_qmv_f16io_resadd(ctx, &Ly.o.w, m->att, m->residual, dims_of(m, Ly.o)));
         // transformer.zig:3372-3646 encodeMLPHalf (fused norm + gate/up + SiLU, down += )
-        RC(nnz_dispatch_fused_norm_pair_silu_f16io(ctx, &Ly.gate.w, &Ly.up.w, m->residual, m->h,
-                                                   Ly.ffn_norm, dims_of(m, Ly.gate)));
-        RC(nnz_dispatch_qmv_f16io_resadd(ctx, &Ly.down.w, m->h, m->residual, dims_of(m, Ly.down)));
+        if (is_q4(m)) {
+            RC(nnz_dispatch_q4_fused_norm_pair_silu_f16io(ctx, &Ly.gate.w, &Ly.up.w, m->residual, m->h,
+                                                          Ly.ffn_norm, dims_of(m, Ly.gate)));
+            RC(nnz_dispatch_q4mv_f16io_resadd(ctx, &Ly.down.w, m->h, m->residual, dims_of(m, Ly.down)));
+        } else {
+            RC(nnz_dispatch_fused_norm_pair_silu_f16io(ctx, &Ly.gate.w, &Ly.up.w, m->residual, m->h,
+                                                       Ly.ffn_norm, dims_of(m, Ly.gate)));
+            RC(nnz_dispatch_qmv_f16io_resadd(ctx, &Ly.down.w, m->h, m->residual, dims_of(m, Ly.down)));
+        }
     }
     // transformer.zig:2730-2785 encodeFinalNormAndLMHead (norm fused into the
     // 1-bit LM head; the tied bf16 head keeps a separate norm)
-    if (c.lm_head_kind == NNZ_LMHEAD_Q1)
+    if (c.lm_head_kind == NNZ_LMHEAD_Q1 || c.lm_head_kind == NNZ_LMHEAD_Q4)
         return nnz_qmv_norm_f32out_launch(ctx, &m->lm.w, m->residual, m->final_norm, m->logits,
                                           dims_of(m, m->lm));
     RC(nnz_dispatch_rms_norm(ctx, m->residual, m->final_norm, m->xn, NNZ_F16, 0,
@@ -450,9 +484,14 @@ int nnz_model_create(nnz_ctx *ctx, const nnz_model_config *cfg, nnz_model **out)
                 "model_create: max_context_length must be a multiple of 8");
     NNZ_REQUIRE(ctx, (uint64_t)c.vocab_size * c.hidden_size < (1ull << 32), NNZ_EUNSUPPORTED,
                 "model_create: vocab*hidden must fit in 32 bits");
-    NNZ_REQUIRE(ctx, c.embed_kind <= NNZ_EMBED_BF16 && c.lm_head_kind <= NNZ_LMHEAD_TIED_BF16 &&
-                         !(c.lm_head_kind == NNZ_LMHEAD_TIED_BF16 && c.embed_kind != NNZ_EMBED_BF16),
-                NNZ_EINVAL, "model_create: bad embed/lm_head kind");
+    if (c.quant_format == NNZ_QUANT_Q4)
+        NNZ_REQUIRE(ctx, c.embed_kind == NNZ_EMBED_Q4 && c.lm_head_kind == NNZ_LMHEAD_Q4, NNZ_EINVAL,
+                    "model_create: Q4 models take NNZ_EMBED_Q4 and NNZ_LMHEAD_Q4");
+    else
+        NNZ_REQUIRE(ctx, c.quant_format == NNZ_QUANT_Q1 && c.embed_kind <= NNZ_EMBED_BF16 &&
+                             c.lm_head_kind <= NNZ_LMHEAD_TIED_BF16 &&
+                             !(c.lm_head_kind == NNZ_LMHEAD_TIED_BF16 && c.embed_kind != NNZ_EMBED_BF16),
+                    NNZ_EINVAL, "model_create: bad quant format or embed/lm_head kind");
 
     nnz_model *m = new nnz_model();
     m->ctx = ctx;
@@ -466,13 +505,15 @@ int nnz_model_create(nnz_ctx *ctx, const nnz_model_config *cfg, nnz_model **out)
     };
     auto body = [&]() -> int {
         const size_t VH = (size_t)c.vocab_size * c.hidden_size;
-        if (c.embed_kind == NNZ_EMBED_Q1) {
-            MALLOC(m->emb, VH / 8 + 4);
+        if (c.embed_kind == NNZ_EMBED_Q1 || c.embed_kind == NNZ_EMBED_Q4) {
+            MALLOC(m->emb, codes_bytes(m, VH) + 4);
             MALLOC(m->emb_scales, ceil_div((uint32_t)VH, c.group_size) * 2);
+            if (c.embed_kind == NNZ_EMBED_Q4) MALLOC(m->emb_biases, ceil_div((uint32_t)VH, c.group_size) * 2);
         } else {
             MALLOC(m->emb, VH * 2);
         }
-        if (c.lm_head_kind == NNZ_LMHEAD_Q1) RC(alloc_proj(m, m->lm, c.vocab_size, c.hidden_size));
+        if (c.lm_head_kind == NNZ_LMHEAD_Q1 || c.lm_head_kind == NNZ_LMHEAD_Q4)
+            RC(alloc_proj(m, m->lm, c.vocab_size, c.hidden_size));
         MALLOC(m->final_norm, c.hidden_size * 4);
         m->L.resize(c.num_layers);
         const size_t kv_bytes = (size_t)c.num_kv_heads * c.max_context_length * c.head_dim * 2;
@@ -543,14 +584,19 @@ int nnz_model_tensor(nnz_model *m, int id, uint32_t layer, void **ptr, size_t *b
         *bytes = b;
         return p ? NNZ_OK : nnz_fail(ctx, NNZ_ESTATE, "tensor %d not present in this config", id);
     };
-    if (id < 10 || id >= 40) {
+    const bool per_layer = (id >= 10 && id < 40) || (id >= NNZ_T_Q_BIASES && id <= NNZ_T_DOWN_BIASES);
+    if (!per_layer) {
+        const bool qemb = c.embed_kind == NNZ_EMBED_Q1 || c.embed_kind == NNZ_EMBED_Q4;
         switch (id) {
         case NNZ_T_EMBED_CODES:
-            return set(m->emb, c.embed_kind == NNZ_EMBED_Q1 ? VH / 8 : VH * 2);
+            return set(m->emb, qemb ? codes_bytes(m, VH) : VH * 2);
         case NNZ_T_EMBED_SCALES:
-            return set(m->emb_scales, c.embed_kind == NNZ_EMBED_Q1 ? ceil_div((uint32_t)VH, c.group_size) * 2 : 0);
-        case NNZ_T_LM_CODES: return set(m->lm.codes, VH / 8);
+            return set(m->emb_scales, qemb ? ceil_div((uint32_t)VH, c.group_size) * 2 : 0);
+        case NNZ_T_EMBED_BIASES:
+            return set(m->emb_biases, ceil_div((uint32_t)VH, c.group_size) * 2);
+        case NNZ_T_LM_CODES: return set(m->lm.codes, codes_bytes(m, VH));
         case NNZ_T_LM_SCALES: return set(m->lm.scales, VH / c.group_size * 2);
+        case NNZ_T_LM_BIASES: return set(m->lm.biases, VH / c.group_size * 2);
         case NNZ_T_FINAL_NORM: return set(m->final_norm, c.hidden_size * 4);
         case NNZ_T_LOGITS: return set(m->logits, (size_t)c.vocab_size * 4);
         case NNZ_T_RESIDUAL: return set(m->residual, c.hidden_size * 4);
@@ -560,8 +606,9 @@ int nnz_model_tensor(nnz_model *m, int id, uint32_t layer, void **ptr, size_t *b
     NNZ_REQUIRE(ctx, layer < c.num_layers, NNZ_EINVAL, "layer %u out of range", layer);
     Layer &Ly = m->L[layer];
     const size_t kv_bytes = (size_t)c.num_kv_heads * c.max_context_length * c.head_dim * 2;
-    auto codes = [&](Proj &p) { return set(p.codes, (size_t)p.M * p.K / 8); };
+    auto codes = [&](Proj &p) { return set(p.codes, codes_bytes(m, (size_t)p.M * p.K)); };
     auto scales = [&](Proj &p) { return set(p.scales, (size_t)p.M * p.K / c.group_size * 2); };
+    auto biases = [&](Proj &p) { return set(p.biases, (size_t)p.M * p.K / c.group_size * 2); };
     switch (id) {
     case NNZ_T_Q_CODES: return codes(Ly.q);
     case NNZ_T_Q_SCALES: return scales(Ly.q);
@@ -577,6 +624,13 @@ int nnz_model_tensor(nnz_model *m, int id, uint32_t layer, void **ptr, size_t *b
     case NNZ_T_UP_SCALES: return scales(Ly.up);
     case NNZ_T_DOWN_CODES: return codes(Ly.down);
     case NNZ_T_DOWN_SCALES: return scales(Ly.down);
+    case NNZ_T_Q_BIASES: return biases(Ly.q);
+    case NNZ_T_K_BIASES: return biases(Ly.k);
+    case NNZ_T_V_BIASES: return biases(Ly.v);
+    case NNZ_T_O_BIASES: return biases(Ly.o);
+    case NNZ_T_GATE_BIASES: return biases(Ly.gate);
+    case NNZ_T_UP_BIASES: return biases(Ly.up);
+    case NNZ_T_DOWN_BIASES: return biases(Ly.down);
     case NNZ_T_ATTN_NORM: return set(Ly.attn_norm, c.hidden_size * 4);
     case NNZ_T_FFN_NORM: return set(Ly.ffn_norm, c.hidden_size * 4);
     case NNZ_T_Q_NORM: return set(Ly.q_norm, c.head_dim * 4);
@@ -613,6 +667,16 @@ int nnz_model_prefill(nnz_model *m, const uint32_t *tokens_host, uint32_t n, uin
         NNZ_REQUIRE(ctx, tokens_host[i] < c.vocab_size, NNZ_EINVAL, "prefill: token id out of range");
     RC(ensure_prefill_buffers(m, n, start));
     NNZ_HIP(ctx, hipMemcpyAsync(m->p_ids, tokens_host, (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
+    if (is_q4(m)) {
+        // chunkedPrefill (transformer.zig:4032-4068): one decode step per
+        // prompt token; the last one leaves its logits.
+        for (uint32_t t = 0; t < n; ++t) {
+            prefill_state_kernel<<<1, 1, 0, ctx->stream>>>(m->state, m->p_ids, t, start);
+            NNZ_LAUNCHED(ctx);
+            RC(enqueue_decode_step(m, start + t + 1));
+        }
+        return NNZ_OK;
+    }
     const uint32_t H = c.hidden_size;
     if (c.embed_kind == NNZ_EMBED_Q1)
         embed_ids_q1_kernel<<<ceil_div(n * H, 256), 256, 0, ctx->stream>>>(

@@ -1010,6 +1010,11 @@ int launch_qmv(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, const
 // Internal fused launches used by the decoder (csrc/model.hip).
 // ---------------------------------------------------------------------------
 
+// The decoder's fused launches take the form of the weights: 1-bit (Q1) or
+// 4-bit with the reference's BF16-faithful rounding (Q4: fused-norm input
+// BF16-truncated before f16, results BF16-truncated before the store or +=,
+// q4mv_bf16_specialized.metal:52-57, :806).
+
 // RMSNorm prologue + Q, K and V projections in one launch (f16 outputs).
 int nnz_qmv_norm_qkv_launch(nnz_ctx *ctx, const nnz_qweight *wq, const nnz_qweight *wk,
                             const nnz_qweight *wv, const float *residual, const float *norm_w,
@@ -1018,15 +1023,24 @@ int nnz_qmv_norm_qkv_launch(nnz_ctx *ctx, const nnz_qweight *wq, const nnz_qweig
     const nnz_qweight *w[3] = {wq, wk, wv};
     void *out[3] = {q, k, v};
     const uint32_t rows[3] = {qrows, kvrows, kvrows};
+    NNZ_REQUIRE(ctx, wq != nullptr, NNZ_EINVAL, "norm_qkv: null weight");
+    if (wq->bits == 4)
+        return launch_qmv_ex<4, NNZ_F32, 1, true, EPI_STORE, NNZ_F16, true>(
+            ctx, w, rows, 3, residual, norm_w, out, {qrows + 2 * kvrows, K, gs}, "q4_norm_qkv");
     return launch_qmv_ex<1, NNZ_F32, 1, true, EPI_STORE, NNZ_F16, false>(
         ctx, w, rows, 3, residual, norm_w, out, {qrows + 2 * kvrows, K, gs}, "norm_qkv");
 }
 
-// RMSNorm prologue (x rounded to f16 like rms_norm_f16out) + 1-bit LM head,
-// f32 logits: the reference's final rms_norm_f16out + qmv_spec_f16in pair
+// RMSNorm prologue (x rounded to f16 like rms_norm_f16out, or BF16-truncated
+// first like rms_norm_bf16_f16out for Q4) + LM head, f32 logits: the
+// reference's final norm + qmv_spec_f16in / q4mv_spec_f16in pair
 // (transformer.zig:2730-2785) in one launch.
 int nnz_qmv_norm_f32out_launch(nnz_ctx *ctx, const nnz_qweight *w, const float *residual,
                                const float *norm_w, float *out, nnz_qmv_dims d) {
+    NNZ_REQUIRE(ctx, w != nullptr, NNZ_EINVAL, "norm_lm_head: null weight");
+    if (w->bits == 4)
+        return launch_qmv<4, NNZ_F32, 1, true, EPI_STORE, NNZ_F32, true>(
+            ctx, w, nullptr, residual, norm_w, out, nullptr, d, "q4_norm_lm_head");
     return launch_qmv<1, NNZ_F32, 1, true, EPI_STORE, NNZ_F32, false>(ctx, w, nullptr, residual,
                                                                        norm_w, out, nullptr, d,
                                                                        "norm_lm_head");
@@ -1043,6 +1057,10 @@ int nnz_qmv_merge_resadd_launch(nnz_ctx *ctx, const nnz_qweight *w, const float 
     const nnz_qweight *ws[1] = {w};
     void *out[1] = {residual};
     const uint32_t rows[1] = {d.M};
+    NNZ_REQUIRE(ctx, w != nullptr, NNZ_EINVAL, "merge_o_resadd: null weight");
+    if (w->bits == 4)
+        return launch_qmv_ex<4, NNZ_F16, 1, XIN_MERGE, EPI_RESADD, NNZ_F32, true>(
+            ctx, ws, rows, 1, nullptr, nullptr, out, d, "q4_merge_o_resadd", &mg);
     return launch_qmv_ex<1, NNZ_F16, 1, XIN_MERGE, EPI_RESADD, NNZ_F32, false>(
         ctx, ws, rows, 1, nullptr, nullptr, out, d, "merge_o_resadd", &mg);
 }
@@ -1055,6 +1073,7 @@ int nnz_dispatch_qmv_merge_f16io_resadd(nnz_ctx *ctx, const nnz_qweight *w, cons
                                         nnz_qmv_dims dims) {
     NNZ_CHECK_CTX(ctx);
     NNZ_REQUIRE(ctx, seq_len > 0 && head_dim > 0, NNZ_EINVAL, "merge_o_resadd: zero dims");
+    NNZ_REQUIRE(ctx, w && w->bits == 1, NNZ_EINVAL, "merge_o_resadd: 1-bit weights");
     const uint32_t chunk = nnz_attn_fused_chunk(seq_len, 1);
     return nnz_qmv_merge_resadd_launch(ctx, w, part_o, part_ml, d_seq_len, seq_len,
                                        ceil_div(seq_len, chunk), chunk, head_dim, residual, dims);
@@ -1138,11 +1157,14 @@ int nnz_dispatch_fused_norm_qkv_f16io(nnz_ctx *ctx, const nnz_qweight *wq, const
                                       nnz_qmv_dims q_dims, uint32_t kv_rows) {
     NNZ_CHECK_CTX(ctx);
     NNZ_REQUIRE(ctx, kv_rows > 0, NNZ_EINVAL, "fused_norm_qkv: kv_rows == 0");
+    NNZ_REQUIRE(ctx, wq && wq->bits == 1, NNZ_EINVAL, "fused_norm_qkv: 1-bit weights");
     return nnz_qmv_norm_qkv_launch(ctx, wq, wk, wv, residual, norm_scale, out_q, out_k, out_v,
                                    q_dims.M, kv_rows, q_dims.K, q_dims.group_size);
 }
 int nnz_dispatch_fused_norm_qmv_f16in(nnz_ctx *ctx, const nnz_qweight *w, const float *residual,
                                       float *output, const float *norm_scale, nnz_qmv_dims dims) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, w && w->bits == 1, NNZ_EINVAL, "fused_norm_qmv_f16in: 1-bit weights");
     return nnz_qmv_norm_f32out_launch(ctx, w, residual, norm_scale, output, dims);
 }
 

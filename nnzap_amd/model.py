@@ -20,6 +20,8 @@ _CODES = {"q": 10, "k": 12, "v": 14, "o": 16, "gate": 18, "up": 20, "down": 22}
 T_EMBED_CODES, T_EMBED_SCALES, T_LM_CODES, T_LM_SCALES, T_FINAL_NORM = 0, 1, 2, 3, 4
 T_ATTN_NORM, T_FFN_NORM, T_Q_NORM, T_K_NORM = 24, 25, 26, 27
 T_K_CACHE, T_V_CACHE, T_LOGITS, T_RESIDUAL = 30, 31, 40, 41
+T_EMBED_BIASES, T_LM_BIASES = 5, 6
+_BIASES = {"q": 50, "k": 51, "v": 52, "o": 53, "gate": 54, "up": 55, "down": 56}
 
 
 class DecoderModel:
@@ -30,7 +32,8 @@ class DecoderModel:
         c = L.ModelConfig(cfg.vocab_size, cfg.hidden_size, cfg.intermediate_size, cfg.num_layers,
                           cfg.num_query_heads, cfg.num_kv_heads, cfg.head_dim,
                           cfg.max_context_length, cfg.max_prefill_length, cfg.group_size,
-                          cfg.rope_theta, cfg.rms_eps, cfg.embed_kind, cfg.lm_head_kind)
+                          cfg.rope_theta, cfg.rms_eps, cfg.embed_kind, cfg.lm_head_kind,
+                          cfg.quant_format)
         h = C.c_void_p()
         dev.call("nnz_model_create", C.byref(c), C.byref(h))
         self.h = h
@@ -75,10 +78,11 @@ class DecoderModel:
         ``embed_on_device`` the bf16 embedding table is generated on the GPU
         from the same seeded stream instead of being uploaded."""
         cfg = self.cfg
+        bits = 4 if cfg.quant_format == L.QUANT_FORMAT_Q4 else 1
         for l, layer in enumerate(w.layers):
             for name in PROJS:
-                if layer[name].bits != 1:
-                    raise ValueError(f"layer {l} {name}: this decoder holds 1-bit projections, "
+                if layer[name].bits != bits:
+                    raise ValueError(f"layer {l} {name}: this decoder holds {bits}-bit projections, "
                                      f"got {layer[name].bits}-bit")
         if len(w.layers) != cfg.num_layers:
             raise ValueError(f"{len(w.layers)} layers given, config has {cfg.num_layers}")
@@ -90,24 +94,30 @@ class DecoderModel:
             else:
                 self.upload(T_EMBED_CODES, 0, w.embed_bf16)
         else:
-            if w.embed_q1 is None or w.embed_q1.bits != 1:
-                raise ValueError("config asks for a 1-bit embedding table")
-            self.upload(T_EMBED_CODES, 0, w.embed_q1.codes)
-            self.upload(T_EMBED_SCALES, 0, w.embed_q1.scales)
-        if cfg.lm_head_kind == L.LMHEAD_Q1:
-            self.upload(T_LM_CODES, 0, w.lm_head.codes)
-            self.upload(T_LM_SCALES, 0, w.lm_head.scales)
+            if w.embed_q1 is None or w.embed_q1.bits != bits:
+                raise ValueError(f"config asks for a {bits}-bit embedding table")
+            self._upload_q(T_EMBED_CODES, T_EMBED_SCALES, T_EMBED_BIASES, 0, w.embed_q1)
+        if cfg.lm_head_kind in (L.LMHEAD_Q1, L.LMHEAD_Q4):
+            if w.lm_head is None or w.lm_head.bits != bits:
+                raise ValueError(f"config asks for a {bits}-bit LM head")
+            self._upload_q(T_LM_CODES, T_LM_SCALES, T_LM_BIASES, 0, w.lm_head)
         self.upload(T_FINAL_NORM, 0, w.final_norm)
         for l, layer in enumerate(w.layers):
             for name in PROJS:
                 cid = _CODES[name]
-                self.upload(cid, l, layer[name].codes)
-                self.upload(cid + 1, l, layer[name].scales)
+                self._upload_q(cid, cid + 1, _BIASES[name], l, layer[name])
             self.upload(T_ATTN_NORM, l, layer["attn_norm"])
             self.upload(T_FFN_NORM, l, layer["ffn_norm"])
             self.upload(T_Q_NORM, l, layer["q_norm"])
             self.upload(T_K_NORM, l, layer["k_norm"])
         self.dev.sync()
+
+    def _upload_q(self, t_codes: int, t_scales: int, t_biases: int, layer: int, q) -> None:
+        """Codes and scales, plus the biases of a 4-bit (q4_mlx) matrix."""
+        self.upload(t_codes, layer, q.codes)
+        self.upload(t_scales, layer, q.scales)
+        if q.bits == 4:
+            self.upload(t_biases, layer, q.biases)
 
     def load_weights(self, paths, quant: str = "q1", tie_word_embeddings: bool = True,
                      strict: bool = True) -> None:
@@ -119,8 +129,13 @@ class DecoderModel:
         from . import checkpoint as ck
         from .safetensors import SafetensorsFile
         cfg = self.cfg
-        if cfg.embed_kind != L.EMBED_Q1 or cfg.lm_head_kind != L.LMHEAD_Q1:
-            raise ValueError("checkpoint models need embed_kind EMBED_Q1, lm_head_kind LMHEAD_Q1")
+        q4 = cfg.quant_format == L.QUANT_FORMAT_Q4
+        if q4 != (quant == ck.QUANT_Q4):
+            raise ValueError(f"quant {quant!r} does not match the model's quant_format")
+        want = (L.EMBED_Q4, L.LMHEAD_Q4) if q4 else (L.EMBED_Q1, L.LMHEAD_Q1)
+        if (cfg.embed_kind, cfg.lm_head_kind) != want:
+            raise ValueError("checkpoint models need a quantised embedding and LM head "
+                             "(EMBED_Q1/LMHEAD_Q1, or EMBED_Q4/LMHEAD_Q4 for q4_mlx)")
         if isinstance(paths, (str, os.PathLike)):
             paths = ck.find_shards(paths) if os.path.isdir(paths) else [paths]
         with ExitStack() as stack:

@@ -12,6 +12,13 @@ with the reference's storage rounding points:
   normalised/rotated k and v stored as float16 in the KV cache (:1583-1592);
 * logits: float32 (qmv_spec_f16in, qmv_specialized.metal:735).
 
+A q4_mlx model (``cfg.quant_format == 1``) takes the Q4 path's extra
+rounding points (transformer.zig:2646, :2743, :2977, :3100): the embedding
+row, every norm output before it is narrowed to float16, and every
+projection result (stored, added to the residual, or the SiLU*mul product,
+and the logits) are BF16-truncated (q4mv_bf16_specialized.metal:52-57, :806;
+transformer.metal:505-549, :610-677).
+
 Prefill is evaluated as a batch (all prompt tokens at once, causal mask):
 mathematically identical to the reference's token-by-token prefill
 (transformer.zig:4032-4068) because every token's computation only reads
@@ -35,6 +42,7 @@ class OracleDecoder:
     def __init__(self, w: DecoderWeights, max_ctx: int | None = None):
         cfg = w.cfg
         self.cfg, self.w = cfg, w
+        self.q4 = getattr(cfg, "quant_format", 0) == 1
         self.W = [{n: O.dequant(layer[n]) for n in PROJS} for layer in w.layers]
         self.lm = O.dequant(w.lm_head) if w.lm_head is not None else None
         T = max_ctx or cfg.max_context_length
@@ -47,6 +55,10 @@ class OracleDecoder:
         cfg = self.cfg
         ids = [int(i) for i in ids]
         e = self.w.embed_q1
+        if e is not None and e.bits == 4:
+            # embedding_lookup_q4 (transformer.metal:505-549)
+            return O.embed_q4(ids, e.codes, e.scales, e.biases, cfg.hidden_size, e.group_size,
+                              e.scale_dtype)
         if e is not None:
             # embedding_lookup (transformer.metal:428-481): +-s of row `id`
             return O.embed_q1(ids, e.codes.view(np.uint8).reshape(-1),
@@ -63,9 +75,16 @@ class OracleDecoder:
             out.append(self._emb_cache[t])
         return np.stack(out)
 
+    def _t(self, x):
+        """The Q4 path's BF16 truncation of a float32 result (identity for Q1)."""
+        return O.bf16_trunc(_f32(x)) if self.q4 else x
+
+    def _norm16(self, x, w):
+        return O.f16(self._t(O.rmsnorm(x, w, self.cfg.rms_eps)))
+
     def lm_head(self, xf: np.ndarray) -> np.ndarray:
         if self.lm is not None:
-            return _f32(xf @ self.lm.T)
+            return _f32(self._t(xf @ self.lm.T))
         table = S.bf16_bits_to_f32(self.w.embed_bf16).astype(np.float64)
         return _f32(xf @ table.T)
 
@@ -81,10 +100,10 @@ class OracleDecoder:
         positions = np.arange(start, start + P)
         for l, layer in enumerate(self.w.layers):
             W = self.W[l]
-            xn = O.f16(O.rmsnorm(res, layer["attn_norm"], cfg.rms_eps))
-            q = O.f16(xn @ W["q"].T)
-            k = O.f16(xn @ W["k"].T)
-            v = O.f16(xn @ W["v"].T)
+            xn = self._norm16(res, layer["attn_norm"])
+            q = O.f16(self._t(xn @ W["q"].T))
+            k = O.f16(self._t(xn @ W["k"].T))
+            v = O.f16(self._t(xn @ W["v"].T))
             qn = np.stack([O.head_norm_rope(q[p].reshape(Hq, D), layer["q_norm"], int(positions[p]),
                                             cfg.rope_theta, cfg.rms_eps) for p in range(P)])
             kn = np.stack([O.f16(O.head_norm_rope(k[p].reshape(Hkv, D), layer["k_norm"],
@@ -105,11 +124,11 @@ class OracleDecoder:
                 s /= s.sum(axis=1, keepdims=True)
                 att[:, h, :] = s @ V[h // g]
             att = O.f16(att.reshape(P, Hq * D))
-            res = _f32(res + att @ W["o"].T)
-            xn2 = O.f16(O.rmsnorm(res, layer["ffn_norm"], cfg.rms_eps))
-            hmid = O.f16(O.silu(xn2 @ W["gate"].T) * (xn2 @ W["up"].T))
-            res = _f32(res + hmid @ W["down"].T)
-        xf = O.f16(O.rmsnorm(res, self.w.final_norm, cfg.rms_eps))
+            res = _f32(res + self._t(att @ W["o"].T))
+            xn2 = self._norm16(res, layer["ffn_norm"])
+            hmid = O.f16(self._t(O.silu(xn2 @ W["gate"].T) * (xn2 @ W["up"].T)))
+            res = _f32(res + self._t(hmid @ W["down"].T))
+        xf = self._norm16(res, self.w.final_norm)
         return self.lm_head(xf)
 
     def generate(self, prompt, n_new: int, eos=()):

@@ -305,3 +305,4 @@ def test_config_from_hf(tmp_path):
     cfg_json["vocab_size"] = 151936
     cfg4, quant4, _ = ck.config_from_hf(cfg_json)
     assert quant4 == ck.QUANT_Q4 and cfg4.group_size == 64
+    assert (cfg4.embed_kind, cfg4.lm_head_kind, cfg4.quant_format) == (2, 2, 1)

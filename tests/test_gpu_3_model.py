@@ -180,6 +180,80 @@ def test_checkpoint_model_matches_oracle(mdev, tmp_path, tie):
         m.close()
 
 
+# -- q4_mlx models (Bonsai*_Q4 presets, transformer.zig:336-382) ------------------
+# The Q4 path truncates results to bfloat16 at the reference's rounding points;
+# the oracle does the same, so the two differ only where their fp32 sums fall
+# on opposite sides of a bf16 boundary (one bf16 ulp, 2^-8 relative, on rare
+# elements).  Bar: logits within 5e-3 of max|logit|, greedy tokens identical.
+Q4_RTOL = 5e-3
+
+
+@pytest.fixture(scope="module")
+def tiny_q4():
+    cfg = cf.TINY_Q4
+    return cfg, cf.decoder_weights(cfg, norm_mode="unit")
+
+
+def test_tiny_q4_prefill_and_decode_logits(mdev, tiny_q4):
+    """Q4 prefill (token by token through the decode step, as the reference's
+    chunkedPrefill) and single decode steps against the oracle."""
+    cfg, w = tiny_q4
+    m = DecoderModel(mdev, cfg)
+    try:
+        m.load(w)
+        ids = cf.prompt_ids(cfg, 40)
+        ref = OracleDecoder(w)
+        ref_logits = ref.forward(list(ids), 0)
+        got = m.prefill(ids, 0)
+        assert_close_normwise(got, ref_logits[-1], rtol=Q4_RTOL, what="q4 prefill logits")
+        assert int(np.argmax(got)) == int(np.argmax(ref_logits[-1]))
+        for i, t in enumerate([5, 77, 300]):
+            pos = len(ids) + i
+            r = ref.forward([t], pos)[0]
+            g = m.forward_decode(t, pos)
+            assert_close_normwise(g, r, rtol=Q4_RTOL, what=f"q4 decode pos {pos}")
+    finally:
+        m.close()
+
+
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_tiny_q4_generate_matches_oracle(mdev, tiny_q4, use_graph):
+    cfg, w = tiny_q4
+    m = DecoderModel(mdev, cfg)
+    try:
+        m.load(w)
+        prompt = cf.prompt_ids(cfg, 32)
+        toks, margins, _ = m.generate(prompt, 32, use_graph=use_graph)
+        ref_toks, ref_margins = OracleDecoder(w).generate(prompt, 32)
+        assert np.array_equal(toks, ref_toks), (toks, ref_toks, ref_margins)
+        assert np.max(np.abs(margins - ref_margins)) < 2e-2   # two logit errors, logits O(1)
+    finally:
+        m.close()
+
+
+def test_q4_checkpoint_model_matches_oracle(mdev, tmp_path):
+    """A q4_mlx checkpoint (raw bf16 scales and biases, tied embedding) loaded
+    from mapped shards: prefill logits and 16 greedy tokens against the oracle
+    on the host-side load of the same shards."""
+    from dataclasses import replace
+    from nnzap_amd import checkpoint as ck
+    from ckpt_util import write_mlx_checkpoint
+    cfg = replace(CKPT_CFG, group_size=64, embed_kind=2, lm_head_kind=2, quant_format=1)
+    write_mlx_checkpoint(tmp_path, cfg, bits=4, tie=True, scale_dtype="BF16")
+    w = ck.load_checkpoint(tmp_path, cfg, quant=ck.QUANT_Q4, tie_word_embeddings=True)
+    m = DecoderModel(mdev, cfg)
+    try:
+        m.load_weights(tmp_path, quant=ck.QUANT_Q4, tie_word_embeddings=True)
+        ids = cf.prompt_ids(cfg, 24)
+        ref_logits = OracleDecoder(w).forward(list(ids), 0)[-1]
+        assert_close_normwise(m.prefill(ids, 0), ref_logits, rtol=Q4_RTOL, what="q4 checkpoint prefill")
+        toks, _, _ = m.generate(ids, 16)
+        ref_toks, ref_margins = OracleDecoder(w).generate(ids, 16)
+        assert np.array_equal(toks, ref_toks), (toks, ref_toks, ref_margins)
+    finally:
+        m.close()
+
+
 # nnmetal/examples/bonsai_golden.zig:30-43: PrismML Bonsai-1.7B (1-bit MLX),
 # prompt "The capital of France is" in the chat template, greedy.
 BONSAI_GOLDEN_PROMPT = "The capital of France is"

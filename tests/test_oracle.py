@@ -281,11 +281,12 @@ def test_embed_q4_truncates():
 
 
 # -------------------------------------------------------------- decoder ----
-def test_decoder_batched_prefill_equals_token_by_token():
+@pytest.mark.parametrize("cfg", [cf.TINY, cf.TINY_Q4], ids=["q1", "q4"])
+def test_decoder_batched_prefill_equals_token_by_token(cfg):
     """The oracle's batched prefill must equal the reference's token-by-token
-    prefill (transformer.zig:4032-4068) on a tiny model."""
+    prefill (transformer.zig:4032-4068) on a tiny model (1-bit, and q4_mlx
+    with its bf16 rounding points)."""
     from oracle.decoder import OracleDecoder
-    cfg = cf.TINY
     w = cf.decoder_weights(cfg, norm_mode="unit")
     ids = cf.prompt_ids(cfg, 6)
     a = OracleDecoder(w)

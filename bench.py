@@ -108,6 +108,60 @@ def bench_decode(args, dev):
     return out
 
 
+def bench_decode_q4(args, dev):
+    """Decode tok/s of a Bonsai-1.7B_Q4-shaped decoder (q4_mlx: 4-bit gs64
+    linears, Q4 embedding tied into the LM head, transformer.zig:336-350).
+    Codes, scales and biases are filled on the device from a seeded normal
+    stream (throughput only; the Q4 numerics are covered by the parity
+    tests); a 32-token prompt runs token by token, then ``steps`` decode steps
+    are timed like the headline figure."""
+    from nnzap_amd import configs as cf
+    from nnzap_amd import model as MD
+    import ctypes as C
+
+    cfg = cf.DecoderConfig(**{**cf.BONSAI_1_7B.__dict__, "group_size": 64, "embed_kind": 2,
+                              "lm_head_kind": 2, "quant_format": 1})
+    m = MD.DecoderModel(dev, cfg)
+    seed = [7000]
+
+    def fill(tid, layer=0, scale=1.0):
+        ptr, nbytes = m.tensor(tid, layer)
+        dev.call("nnz_synth_normal_bf16", C.c_void_p(ptr), nbytes // 2, seed[0], scale)
+        seed[0] += 1
+
+    for base in ((MD.T_EMBED_CODES, MD.T_EMBED_SCALES, MD.T_EMBED_BIASES),
+                 (MD.T_LM_CODES, MD.T_LM_SCALES, MD.T_LM_BIASES)):
+        fill(base[0]), fill(base[1], 0, 0.01), fill(base[2], 0, 0.01)
+    for l in range(cfg.num_layers):
+        for name in cf.PROJS:
+            fill(MD._CODES[name], l), fill(MD._CODES[name] + 1, l, 0.01), fill(MD._BIASES[name], l, 0.01)
+        for tid, n in ((MD.T_ATTN_NORM, cfg.hidden_size), (MD.T_FFN_NORM, cfg.hidden_size),
+                       (MD.T_Q_NORM, cfg.head_dim), (MD.T_K_NORM, cfg.head_dim)):
+            m.upload(tid, l, cf.norm_weights(tid + 64 * l, n, "unit"))
+    m.upload(MD.T_FINAL_NORM, 0, cf.norm_weights(3, cfg.hidden_size, "unit"))
+    prompt = cf.prompt_ids(cfg, 32)
+    m.decode_begin(prompt, max(args.warmup, 1))
+    m.decode_steps(max(args.warmup, 1))
+    m.decode_read(1)
+    m.decode_end()
+    dev.sync()
+    tp0 = time.perf_counter()
+    m.decode_begin(prompt, args.steps)
+    dev.sync()
+    tp1 = time.perf_counter()
+    m.decode_steps(args.steps)
+    dev.sync()
+    t1 = time.perf_counter()
+    m.decode_read(args.steps)
+    m.decode_end()
+    m.close()
+    dt = t1 - tp1
+    return {"tok_s": round(args.steps / dt, 2), "ms_per_step": round(1000.0 * dt / args.steps, 4),
+            "prefill_32_token_by_token_ms": round(1000.0 * (tp1 - tp0), 2),
+            "workload": "Bonsai-1.7B_Q4 shape: 28 layers, q4_mlx gs64 linears, Q4 tied "
+                        "embedding/LM head (vocab 151936), device-filled random weights"}
+
+
 # --------------------------------------------------------------- kernels ----
 class Rot:
     """Distinct device copies of one quantised matrix (same values, distinct
@@ -569,6 +623,7 @@ def main():
     ap.add_argument("--cpu-full", action="store_true",
                     help="per-config CPU timings with 5 warm-ups and the median of 30")
     ap.add_argument("--skip-kernels", action="store_true")
+    ap.add_argument("--skip-q4", action="store_true", help="leave out the 4-bit decode figure")
     ap.add_argument("--skip-decode", action="store_true",
                     help="kernel timings only (profiling runs); no JSON line")
     ap.add_argument("--only", default=None,
@@ -591,6 +646,9 @@ def main():
         bench_kernels(dev, quick=args.quick, only=args.only)
         return
     dec = bench_decode(args, dev)
+    dec_q4 = None if args.skip_q4 else bench_decode_q4(args, dev)
+    if dec_q4:
+        log(f"q4 decode: {dec_q4['tok_s']} tok/s")
     log(f"decode: {dec['tok_s']:.1f} tok/s ({dec['ms_per_step']:.3f} ms/step)")
     kern = {} if args.skip_kernels else bench_kernels(dev, quick=args.quick, only=args.only)
 
@@ -629,6 +687,7 @@ def main():
         "cpu_baseline": cpu,
         "cpu_configs": cpu_cfg,
         "decode": dec,
+        "decode_q4": dec_q4,
         "qmv": {k: v for k, v in kern.items() if k.startswith("config")},
         "prefill_gemm": {k: v for k, v in kern.items() if k.startswith("prefill_gemm")},
         "decode_kernels": dec_k,

@@ -7,13 +7,14 @@
 // (`qmm`, compute.metal:2975-3083) stores W as [K x N] for the MNIST network.
 //
 // Design (v_mfma_f32_16x16x32_f16, fp32 accumulate):
-//   * One 64 (tokens) x 64 (W rows) output tile per 512-thread block.  The 8
-//     waves are 2 W-row halves x 4 k-phases: wave (wn, kq) computes a 64 x 32
-//     tile over the k-steps (64 k each) with index = kq mod 4, so a W
-//     fragment expanded in registers feeds 4 MFMAs, an A fragment read from
-//     LDS feeds 2, and the four partial tiles are summed through LDS at the
-//     end.
-//   * A is staged in LDS 4 k-steps (256 k) at a time, double-buffered, with
+//   * One 64 (tokens) x 64 (W rows) output tile per block of 2 KQ waves:
+//     2 W-row halves x KQ k-phases (KQ = 8 for single matrices, 4 for the
+//     gate/up pair, whose LDS would not fit 8).  Wave (wn, kq) computes a
+//     64 x 32 tile over the k-steps (64 k each) with index = kq mod KQ, so a
+//     W fragment expanded in registers feeds 4 MFMAs, an A fragment read
+//     from LDS feeds 2, and the KQ partial tiles are summed through LDS at
+//     the end.
+//   * A is staged in LDS KQ k-steps (64 KQ k) at a time, double-buffered, with
 //     one barrier per stage; the 16-byte piece p of row r sits at slot
 //     p ^ (r & 15), so the 16 rows of an MFMA fragment read hit distinct banks.
 //   * W is staged as packed bits (a 16-byte entry per row and k-step: two
@@ -36,11 +37,12 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // register arrays 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int BM = 64, BN = 64, BK = 64;
-constexpr int KQ = 4;                      // k-phases (waves along k)
-constexpr int SK = BK * KQ;                // k per LDS stage
-constexpr int PIECES = SK / 8;             // 16-byte pieces per A row and stage (32)
-constexpr int A_LOADS = BM * PIECES / 512; // pieces per thread and stage (4)
-constexpr int WROW = KQ + 1;               // W entries per LDS row (one of padding)
+// KQ k-phases (2 KQ waves, 128 KQ threads); an LDS stage holds KQ k-steps.
+// Every thread loads A_LOADS 16-byte A pieces per stage for either KQ.
+constexpr int A_LOADS = 4;
+template <int KQ> constexpr int SK = BK * KQ;        // k per LDS stage
+template <int KQ> constexpr int PIECES = SK<KQ> / 8; // 16-byte pieces per A row and stage
+template <int KQ> constexpr int WROW = KQ + 1;       // W entries per LDS row (one of padding)
 
 // waitcnt immediate for gfx9: lgkmcnt = 0 only (the wave's LDS stores done)
 constexpr int LGKM0_IMM = 15 | (3 << 14) | (7 << 4);
@@ -84,8 +86,8 @@ struct GemmSegs {
     void *out1, *out2;
 };
 
-template <int MODE, int NMAT>
-__global__ __launch_bounds__(512) void dq_gemm_kernel(const f16_t *A, const uint32_t *codes0,
+template <int MODE, int NMAT, int KQ>
+__global__ __launch_bounds__(128 * KQ) void dq_gemm_kernel(const f16_t *A, const uint32_t *codes0,
                                                       const uint16_t *scales0,
                                                       const uint32_t *codes1,
                                                       const uint16_t *scales1, void *out,
@@ -93,6 +95,8 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const f16_t *A, const uint
                                                       uint32_t gs_log2, GemmSegs sg) {
     // Two A stages (64 rows x 256 k of f16 each); reused for the k-phase
     // reduction after the main loop.
+    constexpr int SK = ::SK<KQ>, PIECES = ::PIECES<KQ>, WROW = ::WROW<KQ>;
+    static_assert(BM * PIECES == A_LOADS * 128 * KQ, "A pieces per thread");
     __shared__ __attribute__((aligned(16))) f16_t As[2][BM * SK];
     // W per stage: for each matrix and row, one 16-byte entry per k-step
     // (code words of its 64 k, scale), rows padded to WROW entries so the 16
@@ -150,13 +154,14 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const f16_t *A, const uint
     // re-read row P - 1, discarded at the store; k-steps past the end re-read
     // the last one, never used).
     const int lp = tid & (PIECES - 1), lr = tid / PIECES;
+    constexpr int A_ROW_STEP = 128 * KQ / PIECES;   // rows between a thread's pieces (16)
     const f16_t *arow[A_LOADS];
 #pragma unroll
     for (int u = 0; u < A_LOADS; ++u)
-        arow[u] = A + (size_t)min(p0 + (uint32_t)(lr + 16 * u), P - 1) * K + (lp & 7) * 8;
+        arow[u] = A + (size_t)min(p0 + (uint32_t)(lr + A_ROW_STEP * u), P - 1) * K + (lp & 7) * 8;
     // W loader: thread t < 256 NMAT loads k-step t % 4 of the stage for row
     // (t / 4) % 64 of matrix t / 256: the step's two code words and its scale.
-    const int wl_m = tid >> 8, wl_row = (tid >> 2) & 63, wl_q = tid & 3;
+    const int wl_m = tid / (64 * KQ), wl_row = (tid / KQ) & 63, wl_q = tid % KQ;
     const bool wl = wl_m < NMAT;
     const uint32_t *wl_codes = (NMAT == 2 && wl_m == 1 ? codes1 : codes0) +
                                (size_t)(n0 + wl_row) * words_per_row;
@@ -183,7 +188,7 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const f16_t *A, const uint
         f16_t *buf = As[st & 1];
 #pragma unroll
         for (int u = 0; u < A_LOADS; ++u) {
-            const int r = lr + 16 * u;
+            const int r = lr + A_ROW_STEP * u;
             ((u32x4 *)(buf + r * SK))[lp ^ (r & 15)] = areg[u];
         }
         if (wl) Ws[st & 1][wl_m][wl_row * WROW + wl_q] = (u32x4){wreg[0], wreg[1], sreg, 0u};
@@ -256,15 +261,16 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const f16_t *A, const uint
 #pragma unroll
                 for (int j = 0; j < 2; ++j) acc[m][i][j] += red[(slot * NF + (m * 8 + i * 2 + j)) * 64 + lane];
     };
-    static_assert(4 * NF * 64 * 16 <= (int)sizeof(As), "reduction slots fit the stage buffers");
-    if (kq >= 2) put((kq - 2) * 2 + wn);
-    __syncthreads();
-    if (kq < 2) add(kq * 2 + wn);
-    __syncthreads();
-    if (kq == 1) put(wn);
-    __syncthreads();
+    static_assert(KQ * NF * 64 * 16 <= (int)sizeof(As), "reduction slots fit the stage buffers");
+    // tree over the k-phases: phases [h, 2h) hand their tiles to [0, h)
+#pragma unroll
+    for (int h = KQ / 2; h >= 1; h /= 2) {
+        if (kq >= h && kq < 2 * h) put((kq - h) * 2 + wn);
+        __syncthreads();
+        if (kq < h) add(kq * 2 + wn);
+        __syncthreads();
+    }
     if (kq != 0) return;   // after the last barrier
-    add(wn);
 
     // D layout: lane holds rows 4*(lane/16)+r, column lane%16 of each 16x16 tile.
 #pragma unroll
@@ -288,6 +294,10 @@ __global__ __launch_bounds__(512) void dq_gemm_kernel(const f16_t *A, const uint
             }
         }
 }
+
+// k-phases of the single-matrix launches (measured against 4: 2-10 %
+// faster; the pair keeps 4, eight would need 164 KB of LDS)
+constexpr int KQ1 = 8;
 
 }  // namespace
 
@@ -320,16 +330,16 @@ int nnz_gemm_launch(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, 
     const uint16_t *s0 = (const uint16_t *)wa->scales;
     switch (mode) {
     case NNZ_GEMM_STORE_F16:
-        dq_gemm_kernel<NNZ_GEMM_STORE_F16, 1><<<grid, 512, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl, GemmSegs{});
+        dq_gemm_kernel<NNZ_GEMM_STORE_F16, 1, KQ1><<<grid, 128 * KQ1, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl, GemmSegs{});
         break;
     case NNZ_GEMM_STORE_F32:
-        dq_gemm_kernel<NNZ_GEMM_STORE_F32, 1><<<grid, 512, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl, GemmSegs{});
+        dq_gemm_kernel<NNZ_GEMM_STORE_F32, 1, KQ1><<<grid, 128 * KQ1, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl, GemmSegs{});
         break;
     case NNZ_GEMM_RESADD:
-        dq_gemm_kernel<NNZ_GEMM_RESADD, 1><<<grid, 512, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl, GemmSegs{});
+        dq_gemm_kernel<NNZ_GEMM_RESADD, 1, KQ1><<<grid, 128 * KQ1, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl, GemmSegs{});
         break;
     case NNZ_GEMM_SILU_PAIR:
-        dq_gemm_kernel<NNZ_GEMM_SILU_PAIR, 2><<<grid, 512, 0, ctx->stream>>>(
+        dq_gemm_kernel<NNZ_GEMM_SILU_PAIR, 2, 4><<<grid, 512, 0, ctx->stream>>>(
             A, c0, s0, (const uint32_t *)wb->codes, (const uint16_t *)wb->scales, out, P, d.M, d.K, gl, GemmSegs{});
         break;
     default:
@@ -366,7 +376,7 @@ int nnz_gemm_segments_launch(nnz_ctx *ctx, const nnz_qweight *const *w, void *co
                 nw > 2 ? (const uint16_t *)w[2]->scales : nullptr,
                 nw > 1 ? out[1] : nullptr, nw > 2 ? out[2] : nullptr};
     const uint32_t grid = M / BN * ceil_div(P, BM);
-    dq_gemm_kernel<NNZ_GEMM_STORE_F16, 1><<<grid, 512, 0, ctx->stream>>>(
+    dq_gemm_kernel<NNZ_GEMM_STORE_F16, 1, KQ1><<<grid, 128 * KQ1, 0, ctx->stream>>>(
         (const f16_t *)a, (const uint32_t *)w[0]->codes, (const uint16_t *)w[0]->scales, nullptr,
         nullptr, out[0], P, M, K, (uint32_t)__builtin_ctz(group_size), sg);
     NNZ_LAUNCHED(ctx);

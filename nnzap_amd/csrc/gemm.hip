@@ -38,8 +38,6 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int BM = 64, BN = 64, BK = 64;
 // KQ k-phases (2 KQ waves, 128 KQ threads); an LDS stage holds KQ k-steps.
-// Every thread loads A_LOADS 16-byte A pieces per stage for either KQ.
-constexpr int A_LOADS = 4;
 template <int KQ> constexpr int SK = BK * KQ;        // k per LDS stage
 template <int KQ> constexpr int PIECES = SK<KQ> / 8; // 16-byte pieces per A row and stage
 template <int KQ> constexpr int WROW = KQ + 1;       // W entries per LDS row (one of padding)
@@ -86,8 +84,8 @@ struct GemmSegs {
     void *out1, *out2;
 };
 
-template <int MODE, int NMAT, int KQ>
-__global__ __launch_bounds__(128 * KQ) void dq_gemm_kernel(const f16_t *A, const uint32_t *codes0,
+template <int MODE, int NMAT, int KQ, int WN>
+__global__ __launch_bounds__(64 * WN * KQ) void dq_gemm_kernel(const f16_t *A, const uint32_t *codes0,
                                                       const uint16_t *scales0,
                                                       const uint32_t *codes1,
                                                       const uint16_t *scales1, void *out,
@@ -96,7 +94,9 @@ __global__ __launch_bounds__(128 * KQ) void dq_gemm_kernel(const f16_t *A, const
     // Two A stages (64 rows x 256 k of f16 each); reused for the k-phase
     // reduction after the main loop.
     constexpr int SK = ::SK<KQ>, PIECES = ::PIECES<KQ>, WROW = ::WROW<KQ>;
-    static_assert(BM * PIECES == A_LOADS * 128 * KQ, "A pieces per thread");
+    // WN W-row groups x KQ k-phases of waves; a wave's tile is 64 x (64 / WN)
+    constexpr int THREADS = 64 * WN * KQ, NJ = 4 / WN, A_LOADS = BM * PIECES / THREADS;
+    static_assert(BM * PIECES == A_LOADS * THREADS && 64 * KQ * NMAT <= THREADS, "loader shapes");
     __shared__ __attribute__((aligned(16))) f16_t As[2][BM * SK];
     // W per stage: for each matrix and row, one 16-byte entry per k-step
     // (code words of its 64 k, scale), rows padded to WROW entries so the 16
@@ -105,7 +105,7 @@ __global__ __launch_bounds__(128 * KQ) void dq_gemm_kernel(const f16_t *A, const
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wn = wave & 1, kq = wave >> 1;
+    const int wn = wave % WN, kq = wave / WN;
 
     // Block -> (W tile x, token tile y).  Workgroups are dispatched to the 8
     // XCDs round-robin, so block L runs on XCD L % 8; with the token tiles a
@@ -142,19 +142,19 @@ __global__ __launch_bounds__(128 * KQ) void dq_gemm_kernel(const f16_t *A, const
     const uint32_t words_per_row = K / 32, groups_per_row = K >> gs_log2;
     const uint32_t nk = K / BK, nst = ceil_div(nk, (uint32_t)KQ);
 
-    float4v acc[NMAT][4][2];
+    float4v acc[NMAT][4][NJ];
 #pragma unroll
     for (int m = 0; m < NMAT; ++m)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) acc[m][i][j] = (float4v){0.f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < NJ; ++j) acc[m][i][j] = (float4v){0.f, 0.f, 0.f, 0.f};
 
     // A loader: piece (tid % 32) of rows tid / 32 + 16 u, u < 4 (rows past P
     // re-read row P - 1, discarded at the store; k-steps past the end re-read
     // the last one, never used).
     const int lp = tid & (PIECES - 1), lr = tid / PIECES;
-    constexpr int A_ROW_STEP = 128 * KQ / PIECES;   // rows between a thread's pieces (16)
+    constexpr int A_ROW_STEP = THREADS / PIECES;   // rows between a thread's pieces
     const f16_t *arow[A_LOADS];
 #pragma unroll
     for (int u = 0; u < A_LOADS; ++u)
@@ -196,12 +196,12 @@ __global__ __launch_bounds__(128 * KQ) void dq_gemm_kernel(const f16_t *A, const
     auto compute = [&](uint32_t st) __attribute__((always_inline)) {
         if (st * KQ + kq >= nk) return;   // wave-uniform
         const f16_t *buf = As[st & 1];
-        uint32_t w[NMAT][2][2], ns2[NMAT][2];
+        uint32_t w[NMAT][NJ][2], ns2[NMAT][NJ];
 #pragma unroll
         for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const u32x4 e = Ws[st & 1][m][(32 * wn + 16 * j + (lane & 15)) * WROW + kq];
+            for (int j = 0; j < NJ; ++j) {
+                const u32x4 e = Ws[st & 1][m][(16 * NJ * wn + 16 * j + (lane & 15)) * WROW + kq];
                 w[m][j][0] = e[0];
                 w[m][j][1] = e[1];
                 ns2[m][j] = (e[2] | (e[2] << 16)) ^ 0x80008000u;
@@ -218,7 +218,7 @@ __global__ __launch_bounds__(128 * KQ) void dq_gemm_kernel(const f16_t *A, const
 #pragma unroll
             for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
+                for (int j = 0; j < NJ; ++j) {
                     const half8 bf = expand_bits((w[m][j][kk] >> bsh) & 0xFFu, ns2[m][j]);
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
@@ -243,7 +243,7 @@ __global__ __launch_bounds__(128 * KQ) void dq_gemm_kernel(const f16_t *A, const
     // k-phase reduction through LDS (the stage buffers are free): phases 2, 3
     // hand their tiles to 0, 1, then phase 1 to phase 0.  Slot layout: one
     // float4 per (fragment, lane), lanes adjacent.
-    constexpr int NF = NMAT * 8;
+    constexpr int NF = NMAT * 4 * NJ;
     float4v *red = (float4v *)&As[0][0];
     auto put = [&](int slot) __attribute__((always_inline)) {
 #pragma unroll
@@ -251,7 +251,7 @@ __global__ __launch_bounds__(128 * KQ) void dq_gemm_kernel(const f16_t *A, const
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) red[(slot * NF + (m * 8 + i * 2 + j)) * 64 + lane] = acc[m][i][j];
+                for (int j = 0; j < NJ; ++j) red[(slot * NF + (m * 4 + i) * NJ + j) * 64 + lane] = acc[m][i][j];
     };
     auto add = [&](int slot) __attribute__((always_inline)) {
 #pragma unroll
@@ -259,15 +259,15 @@ __global__ __launch_bounds__(128 * KQ) void dq_gemm_kernel(const f16_t *A, const
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) acc[m][i][j] += red[(slot * NF + (m * 8 + i * 2 + j)) * 64 + lane];
+                for (int j = 0; j < NJ; ++j) acc[m][i][j] += red[(slot * NF + (m * 4 + i) * NJ + j) * 64 + lane];
     };
-    static_assert(KQ * NF * 64 * 16 <= (int)sizeof(As), "reduction slots fit the stage buffers");
+    static_assert(KQ / 2 * WN * NF * 64 * 16 <= (int)sizeof(As), "reduction slots fit the stage buffers");
     // tree over the k-phases: phases [h, 2h) hand their tiles to [0, h)
 #pragma unroll
     for (int h = KQ / 2; h >= 1; h /= 2) {
-        if (kq >= h && kq < 2 * h) put((kq - h) * 2 + wn);
+        if (kq >= h && kq < 2 * h) put((kq - h) * WN + wn);
         __syncthreads();
-        if (kq < h) add(kq * 2 + wn);
+        if (kq < h) add(kq * WN + wn);
         __syncthreads();
     }
     if (kq != 0) return;   // after the last barrier
@@ -280,8 +280,8 @@ __global__ __launch_bounds__(128 * KQ) void dq_gemm_kernel(const f16_t *A, const
             const uint32_t p = p0 + i * 16 + 4 * (lane >> 4) + r;
             if (p >= P) continue;
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const uint32_t n = n0 + 32 * wn + 16 * j + (lane & 15);
+            for (int j = 0; j < NJ; ++j) {
+                const uint32_t n = n0 + 16 * NJ * wn + 16 * j + (lane & 15);
                 const size_t o = (size_t)p * M + n;
                 const float c = acc[0][i][j][r];
                 if constexpr (MODE == NNZ_GEMM_STORE_F16) ((f16_t *)out)[o] = (f16_t)c;
@@ -295,9 +295,11 @@ __global__ __launch_bounds__(128 * KQ) void dq_gemm_kernel(const f16_t *A, const
         }
 }
 
-// k-phases of the single-matrix launches (measured against 4: 2-10 %
-// faster; the pair keeps 4, eight would need 164 KB of LDS)
-constexpr int KQ1 = 8;
+// k-phases and W-row groups of the single-matrix launches.  Measured: 8
+// k-phases are 2-10 % faster than 4 (the pair keeps 4; 8 would need 164 KB
+// of LDS); one W-row group (64 x 64 wave tiles, half the A reads from LDS,
+// 8 waves) is 7-12 % slower than two (16 waves).
+constexpr int KQ1 = 8, WN1 = 2;
 
 }  // namespace
 
@@ -330,16 +332,16 @@ int nnz_gemm_launch(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, 
     const uint16_t *s0 = (const uint16_t *)wa->scales;
     switch (mode) {
     case NNZ_GEMM_STORE_F16:
-        dq_gemm_kernel<NNZ_GEMM_STORE_F16, 1, KQ1><<<grid, 128 * KQ1, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl, GemmSegs{});
+        dq_gemm_kernel<NNZ_GEMM_STORE_F16, 1, KQ1, WN1><<<grid, 64 * WN1 * KQ1, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl, GemmSegs{});
         break;
     case NNZ_GEMM_STORE_F32:
-        dq_gemm_kernel<NNZ_GEMM_STORE_F32, 1, KQ1><<<grid, 128 * KQ1, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl, GemmSegs{});
+        dq_gemm_kernel<NNZ_GEMM_STORE_F32, 1, KQ1, WN1><<<grid, 64 * WN1 * KQ1, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl, GemmSegs{});
         break;
     case NNZ_GEMM_RESADD:
-        dq_gemm_kernel<NNZ_GEMM_RESADD, 1, KQ1><<<grid, 128 * KQ1, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl, GemmSegs{});
+        dq_gemm_kernel<NNZ_GEMM_RESADD, 1, KQ1, WN1><<<grid, 64 * WN1 * KQ1, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl, GemmSegs{});
         break;
     case NNZ_GEMM_SILU_PAIR:
-        dq_gemm_kernel<NNZ_GEMM_SILU_PAIR, 2, 4><<<grid, 512, 0, ctx->stream>>>(
+        dq_gemm_kernel<NNZ_GEMM_SILU_PAIR, 2, 4, 2><<<grid, 512, 0, ctx->stream>>>(
             A, c0, s0, (const uint32_t *)wb->codes, (const uint16_t *)wb->scales, out, P, d.M, d.K, gl, GemmSegs{});
         break;
     default:
@@ -376,7 +378,7 @@ int nnz_gemm_segments_launch(nnz_ctx *ctx, const nnz_qweight *const *w, void *co
                 nw > 2 ? (const uint16_t *)w[2]->scales : nullptr,
                 nw > 1 ? out[1] : nullptr, nw > 2 ? out[2] : nullptr};
     const uint32_t grid = M / BN * ceil_div(P, BM);
-    dq_gemm_kernel<NNZ_GEMM_STORE_F16, 1, KQ1><<<grid, 128 * KQ1, 0, ctx->stream>>>(
+    dq_gemm_kernel<NNZ_GEMM_STORE_F16, 1, KQ1, WN1><<<grid, 64 * WN1 * KQ1, 0, ctx->stream>>>(
         (const f16_t *)a, (const uint32_t *)w[0]->codes, (const uint16_t *)w[0]->scales, nullptr,
         nullptr, out[0], P, M, K, (uint32_t)__builtin_ctz(group_size), sg);
     NNZ_LAUNCHED(ctx);

@@ -10,7 +10,10 @@
 //
 // Layout on the MFMA (v_mfma_f32_16x16x32_f16, fp32 accumulate):
 //   * a wave owns 16 queries of one query head; a block holds the G query
-//     heads of one KV head, so the K/V tiles staged in LDS serve all of them;
+//     heads of one KV head, so the K/V tiles staged in LDS serve all of them
+//     (and, for G = 2, four key splits of each head: S consecutive tiles are
+//     staged per step, wave split s takes tile s, and the partial softmax
+//     states are merged through LDS at the end);
 //   * scores are computed transposed, S^T[key][q] = K . Q^T: A = 16 keys x
 //     32 dims of K from LDS, B = Q^T from registers.  The accumulator puts
 //     keys 4g..4g+3 of a 16-key block in lane group g's four registers, all
@@ -34,6 +37,10 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 
 constexpr int KT = 64;  // keys per LDS tile
+// Key splits of the G = 2 blocks (8 waves; measured per layer at P = 512:
+// 24.5 us unsplit, 18.6 us with 2 splits, 16.5 us with 4).  G = 4 and 8
+// blocks already hold 4 and 8 waves.
+constexpr int S_G2 = 4;
 
 struct PrefillArgs {
     const float *q;      // [n][hq][D] f32
@@ -49,17 +56,25 @@ __device__ __forceinline__ void split_f16(float v, _Float16 &hi, _Float16 &lo) {
     lo = (_Float16)(v - (float)hi);
 }
 
-template <int D, int G>
-__global__ __launch_bounds__(64 * G) void attn_prefill_kernel(PrefillArgs a) {
-    constexpr int NT = 64 * G;
+// S key splits: the block holds S x G waves; wave (ws, w) walks the key
+// tiles ws, ws + S, ... of query head w and the S partial softmax states
+// (running max, sum, O) of each head are merged through LDS at the end.
+template <int D, int G, int S>
+__global__ __launch_bounds__(64 * G * S) void attn_prefill_kernel(PrefillArgs a) {
+    constexpr int NT = 64 * G * S;
     constexpr int NKS = D / 32;  // 32-dim steps of the score MFMAs
     constexpr int NDT = D / 16;  // 16-dim tiles of O^T
     constexpr int KP = D + 8;    // LDS pitch (halves) of a K row
     constexpr int VP = KT + 8;   // LDS pitch (halves) of a V^T row
-    __shared__ __align__(16) _Float16 Ks[KT * KP];
-    __shared__ __align__(16) _Float16 Vs[D * VP];
+    constexpr int KTILE = KT * KP, VTILE = D * VP;          // halves per staged tile
+    constexpr int MSLOT = (NDT * 4 + 2) * 64;               // floats per merge slot
+    constexpr int SMEM = S * (KTILE + VTILE) * 2 > (S - 1) * G * MSLOT * 4
+                             ? S * (KTILE + VTILE) * 2 : (S - 1) * G * MSLOT * 4;
+    __shared__ __align__(16) unsigned char smem[SMEM];
+    _Float16 *Ks = (_Float16 *)smem;              // [S][KT][KP]
+    _Float16 *Vs = (_Float16 *)smem + S * KTILE;  // [S][D][VP]
 
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = (tid >> 6) % G, ws = (tid >> 6) / G;
     const int g = lane >> 4, c = lane & 15;
     const uint32_t hkv = blockIdx.y;
     const uint32_t h = hkv * G + (uint32_t)w;
@@ -69,7 +84,7 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(PrefillArgs a) {
     const uint32_t qpos = a.start + qi;
     const uint32_t seq_end = a.start + a.n;
     const uint32_t qlast = (q0 + 15u < a.n ? q0 + 15u : a.n - 1u) + a.start;
-    const uint32_t ntiles = qlast / KT + 1u;
+    const uint32_t ntiles = qlast / KT + 1u, nsteps = (ntiles + S - 1) / S;
 
     // Q^T fragments: lane (g, c) holds dims 32 ks + 8 g .. +8 of query c
     half8 qh[NKS], ql[NKS];
@@ -101,13 +116,14 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(PrefillArgs a) {
     // branched around: addresses are clamped into the cache and keys past
     // the sequence are zeroed by selects (8-key V pieces never cross
     // max_ctx: max_ctx % 8 == 0).
-    constexpr int KPT = KT * D / 8 / NT, VPT = D * KT / 8 / NT;
+    // A step stages S consecutive tiles, tile j of the step in LDS slot j.
+    constexpr int KPT = S * KT * D / 8 / NT, VPT = S * D * KT / 8 / NT;
     uint4 kr[KPT], vr[VPT];
     auto load_tile = [&](uint32_t k0) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
             const int p = tid + i * NT;
-            const uint32_t key = k0 + (uint32_t)(p / (D / 8));
+            const uint32_t key = k0 + (uint32_t)(p / (D / 8));   // p / (D/8) spans the S tiles
             const uint32_t kc = key < seq_end ? key : 0u;
             const uint4 v = *(const uint4 *)(kbase + (size_t)kc * D + (p % (D / 8)) * 8);
             kr[i] = key < seq_end ? v : make_uint4(0u, 0u, 0u, 0u);
@@ -115,9 +131,10 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const int p = tid + i * NT;
-            const uint32_t key = k0 + (uint32_t)(p % (KT / 8)) * 8u;
+            const int j = p / (D * KT / 8), pp = p % (D * KT / 8);   // tile j of the step
+            const uint32_t key = k0 + (uint32_t)(j * KT) + (uint32_t)(pp % (KT / 8)) * 8u;
             const uint32_t kc = key < seq_end ? key : 0u;
-            uint4 v = *(const uint4 *)(vbase + (size_t)(p / (KT / 8)) * a.max_ctx + kc);
+            uint4 v = *(const uint4 *)(vbase + (size_t)(pp / (KT / 8)) * a.max_ctx + kc);
             // halves e with key + e >= seq_end become 0
             const int keep = key >= seq_end ? 0 : (int)(seq_end - key < 8u ? seq_end - key : 8u);
             const uint32_t m[4] = {keep >= 2 ? ~0u : (keep >= 1 ? 0xFFFFu : 0u),
@@ -140,15 +157,19 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const int p = tid + i * NT;
-            *(uint4 *)(Vs + (p / (KT / 8)) * VP + (p % (KT / 8)) * 8) = vr[i];
+            const int j = p / (D * KT / 8), pp = p % (D * KT / 8);
+            *(uint4 *)(Vs + j * VTILE + (pp / (KT / 8)) * VP + (pp % (KT / 8)) * 8) = vr[i];
         }
     };
     load_tile(0);
-    for (uint32_t t = 0; t < ntiles; ++t) {
-        const uint32_t k0 = t * KT;
+    for (uint32_t step = 0; step < nsteps; ++step) {
         store_tile();
         __syncthreads();
-        load_tile((t + 1 < ntiles ? t + 1 : t) * KT);
+        load_tile((step + 1 < nsteps ? step + 1 : step) * (S * KT));
+        const uint32_t t = step * S + (uint32_t)ws;   // this wave's tile
+        if (t < ntiles) {   // wave-uniform
+        const uint32_t k0 = t * KT;
+        const _Float16 *Kt = Ks + ws * KTILE, *Vt = Vs + ws * VTILE;
 
         // S^T = K . Q^T, 4 blocks of 16 keys
         float4v s[KT / 16];
@@ -157,7 +178,7 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(PrefillArgs a) {
             s[st] = (float4v){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < NKS; ++ks) {
-                const half8 ka = *(const half8 *)(Ks + (st * 16 + c) * KP + 32 * ks + 8 * g);
+                const half8 ka = *(const half8 *)(Kt + (st * 16 + c) * KP + 32 * ks + 8 * g);
                 s[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh[ks], s[st], 0, 0, 0);
                 s[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[ks], s[st], 0, 0, 0);
             }
@@ -209,7 +230,7 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(PrefillArgs a) {
         // O^T += V^T . P^T
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
-            const _Float16 *vrow = Vs + (16 * dt + c) * VP + 4 * g;
+            const _Float16 *vrow = Vt + (16 * dt + c) * VP + 4 * g;
 #pragma unroll
             for (int kk = 0; kk < KT / 32; ++kk) {
                 const uint2 lo4 = *(const uint2 *)(vrow + (2 * kk) * 16);
@@ -220,9 +241,44 @@ __global__ __launch_bounds__(64 * G) void attn_prefill_kernel(PrefillArgs a) {
                 o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl[kk], o[dt], 0, 0, 0);
             }
         }
+        }   // t < ntiles
         __syncthreads();
     }
 
+    if constexpr (S > 1) {
+        // merge the S partial states of head w into split 0 (the tile
+        // buffers are free: the loop ended with a barrier)
+        float *mrg = (float *)smem;
+        if (ws > 0) {
+            float *slot = mrg + ((ws - 1) * G + w) * MSLOT + lane;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) slot[(dt * 4 + r) * 64] = o[dt][r];
+            slot[(NDT * 4) * 64] = m_run;
+            slot[(NDT * 4 + 1) * 64] = l_run;
+        }
+        __syncthreads();
+        if (ws != 0) return;   // after the last barrier
+        float m = m_run;
+#pragma unroll
+        for (int s2 = 1; s2 < S; ++s2) m = fmaxf(m, mrg[((s2 - 1) * G + w) * MSLOT + (NDT * 4) * 64 + lane]);
+        const float c0 = m_run == -INFINITY ? 0.f : expf(m_run - m);
+        l_run *= c0;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) o[dt] *= c0;
+#pragma unroll
+        for (int s2 = 1; s2 < S; ++s2) {
+            const float *slot = mrg + ((s2 - 1) * G + w) * MSLOT + lane;
+            const float ms = slot[(NDT * 4) * 64];
+            const float cs = ms == -INFINITY ? 0.f : expf(ms - m);
+            l_run += slot[(NDT * 4 + 1) * 64] * cs;
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) o[dt][r] += slot[(dt * 4 + r) * 64] * cs;
+        }
+    }
     if (qvalid) {
         const float inv = 1.0f / l_run;
         f16_t *op = a.out + ((size_t)qi * a.hq + h) * D;
@@ -242,9 +298,9 @@ template <int D>
 int launch_d(nnz_ctx *ctx, const PrefillArgs &a, uint32_t hkv, uint32_t G) {
     const dim3 grid((a.n + 15) / 16, hkv);
     switch (G) {
-    case 2: attn_prefill_kernel<D, 2><<<grid, 128, 0, ctx->stream>>>(a); break;
-    case 4: attn_prefill_kernel<D, 4><<<grid, 256, 0, ctx->stream>>>(a); break;
-    default: attn_prefill_kernel<D, 8><<<grid, 512, 0, ctx->stream>>>(a); break;
+    case 2: attn_prefill_kernel<D, 2, S_G2><<<grid, 128 * S_G2, 0, ctx->stream>>>(a); break;
+    case 4: attn_prefill_kernel<D, 4, 1><<<grid, 256, 0, ctx->stream>>>(a); break;
+    default: attn_prefill_kernel<D, 8, 1><<<grid, 512, 0, ctx->stream>>>(a); break;
     }
     NNZ_LAUNCHED(ctx);
     return NNZ_OK;

@@ -8,8 +8,8 @@
 //
 // Design (v_mfma_f32_16x16x32_f16, fp32 accumulate):
 //   * One 64 (tokens) x 64 (W rows) output tile per block of 2 KQ waves:
-//     2 W-row halves x KQ k-phases (KQ = 8 for single matrices, 4 for the
-//     gate/up pair, whose LDS would not fit 8).  Wave (wn, kq) computes a
+//     2 W-row halves x KQ k-phases (KQ = 8 for single matrices whose grid
+//     fits one block per CU, else 4).  Wave (wn, kq) computes a
 //     64 x 32 tile over the k-steps (64 k each) with index = kq mod KQ, so a
 //     W fragment expanded in registers feeds 4 MFMAs, an A fragment read
 //     from LDS feeds 2, and the KQ partial tiles are summed through LDS at
@@ -295,11 +295,26 @@ __global__ __launch_bounds__(64 * WN * KQ) void dq_gemm_kernel(const f16_t *A, c
         }
 }
 
-// k-phases and W-row groups of the single-matrix launches.  Measured: 8
-// k-phases are 2-10 % faster than 4 (the pair keeps 4; 8 would need 164 KB
-// of LDS); one W-row group (64 x 64 wave tiles, half the A reads from LDS,
-// 8 waves) is 7-12 % slower than two (16 waves).
-constexpr int KQ1 = 8, WN1 = 2;
+// k-phases and W-row groups of the single-matrix launches.  Measured at P =
+// 512: with a grid of at most one block per CU, 8 k-phases (16 waves, 149
+// KB of LDS) are 2-10 % faster than 4; larger grids run 4 (75 KB: two
+// blocks per CU; the fused Q/K/V launch, 512 blocks: 17.1 us against 20.6).
+// The pair always runs 4 (8 would need 164 KB).  One W-row group (64 x 64
+// wave tiles, half the A reads from LDS, 8 waves) is 7-12 % slower than two.
+constexpr int WN1 = 2;
+constexpr uint32_t ONE_ROUND_BLOCKS = 256;   // CUs of an MI355X
+
+template <int MODE>
+void launch_single(nnz_ctx *ctx, uint32_t grid, const f16_t *A, const uint32_t *c0,
+                   const uint16_t *s0, void *out, uint32_t P, uint32_t M, uint32_t K, uint32_t gl,
+                   const GemmSegs &sg) {
+    if (grid <= ONE_ROUND_BLOCKS)
+        dq_gemm_kernel<MODE, 1, 8, WN1><<<grid, 64 * WN1 * 8, 0, ctx->stream>>>(
+            A, c0, s0, nullptr, nullptr, out, P, M, K, gl, sg);
+    else
+        dq_gemm_kernel<MODE, 1, 4, WN1><<<grid, 64 * WN1 * 4, 0, ctx->stream>>>(
+            A, c0, s0, nullptr, nullptr, out, P, M, K, gl, sg);
+}
 
 }  // namespace
 
@@ -332,13 +347,13 @@ int nnz_gemm_launch(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, 
     const uint16_t *s0 = (const uint16_t *)wa->scales;
     switch (mode) {
     case NNZ_GEMM_STORE_F16:
-        dq_gemm_kernel<NNZ_GEMM_STORE_F16, 1, KQ1, WN1><<<grid, 64 * WN1 * KQ1, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl, GemmSegs{});
+        launch_single<NNZ_GEMM_STORE_F16>(ctx, grid, A, c0, s0, out, P, d.M, d.K, gl, GemmSegs{});
         break;
     case NNZ_GEMM_STORE_F32:
-        dq_gemm_kernel<NNZ_GEMM_STORE_F32, 1, KQ1, WN1><<<grid, 64 * WN1 * KQ1, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl, GemmSegs{});
+        launch_single<NNZ_GEMM_STORE_F32>(ctx, grid, A, c0, s0, out, P, d.M, d.K, gl, GemmSegs{});
         break;
     case NNZ_GEMM_RESADD:
-        dq_gemm_kernel<NNZ_GEMM_RESADD, 1, KQ1, WN1><<<grid, 64 * WN1 * KQ1, 0, ctx->stream>>>(A, c0, s0, nullptr, nullptr, out, P, d.M, d.K, gl, GemmSegs{});
+        launch_single<NNZ_GEMM_RESADD>(ctx, grid, A, c0, s0, out, P, d.M, d.K, gl, GemmSegs{});
         break;
     case NNZ_GEMM_SILU_PAIR:
         dq_gemm_kernel<NNZ_GEMM_SILU_PAIR, 2, 4, 2><<<grid, 512, 0, ctx->stream>>>(
@@ -378,9 +393,9 @@ int nnz_gemm_segments_launch(nnz_ctx *ctx, const nnz_qweight *const *w, void *co
                 nw > 2 ? (const uint16_t *)w[2]->scales : nullptr,
                 nw > 1 ? out[1] : nullptr, nw > 2 ? out[2] : nullptr};
     const uint32_t grid = M / BN * ceil_div(P, BM);
-    dq_gemm_kernel<NNZ_GEMM_STORE_F16, 1, KQ1, WN1><<<grid, 64 * WN1 * KQ1, 0, ctx->stream>>>(
-        (const f16_t *)a, (const uint32_t *)w[0]->codes, (const uint16_t *)w[0]->scales, nullptr,
-        nullptr, out[0], P, M, K, (uint32_t)__builtin_ctz(group_size), sg);
+    launch_single<NNZ_GEMM_STORE_F16>(ctx, grid, (const f16_t *)a, (const uint32_t *)w[0]->codes,
+                                      (const uint16_t *)w[0]->scales, out[0], P, M, K,
+                                      (uint32_t)__builtin_ctz(group_size), sg);
     NNZ_LAUNCHED(ctx);
     return NNZ_OK;
 }

@@ -364,10 +364,12 @@ def test_dequant_gemm_modes(dev, P):
 
 
 @pytest.mark.parametrize("P,M,K,gs", [(100, 192, 2112, 64), (512, 128, 6144, 128),
-                                       (64, 64, 192, 64), (1024, 64, 320, 64)])
+                                       (64, 64, 192, 64), (1024, 64, 320, 64),
+                                       (512, 4096, 576, 64)])
 def test_dequant_gemm_shapes(dev, P, M, K, gs):
-    """K not a multiple of the 256-k stage (last stage partial), group size 64,
-    token tiles that do and do not divide by 8, and the silu pair."""
+    """K not a multiple of the stage (last stage partial), group size 64,
+    token tiles that do and do not divide by 8, grids of up to one block per
+    CU (eight k-phases) and beyond (four), and the silu pair."""
     wa, wb = cf.q1_matrix(M, K, gs, 490, 491), cf.q1_matrix(M, K, gs, 492, 493)
     a16 = (0.5 * S.normal(494, P * K)).astype(np.float16).reshape(P, K)
     A = a16.astype(np.float64)

@@ -9,7 +9,7 @@
 // Design (v_mfma_f32_16x16x32_f16, fp32 accumulate):
 //   * One 64 (tokens) x 64 (W rows) output tile per block of 2 KQ waves:
 //     2 W-row halves x KQ k-phases (KQ = 8 for single matrices whose grid
-//     fits one block per CU, else 4).  Wave (wn, kq) computes a
+//     fits one block per CU, else 4; 2 for the gate/up pair).  Wave (wn, kq) computes a
 //     64 x 32 tile over the k-steps (64 k each) with index = kq mod KQ, so a
 //     W fragment expanded in registers feeds 4 MFMAs, an A fragment read
 //     from LDS feeds 2, and the KQ partial tiles are summed through LDS at
@@ -97,6 +97,7 @@ __global__ __launch_bounds__(64 * WN * KQ) void dq_gemm_kernel(const f16_t *A, c
     // WN W-row groups x KQ k-phases of waves; a wave's tile is 64 x (64 / WN)
     constexpr int THREADS = 64 * WN * KQ, NJ = 4 / WN, A_LOADS = BM * PIECES / THREADS;
     static_assert(BM * PIECES == A_LOADS * THREADS && 64 * KQ * NMAT <= THREADS, "loader shapes");
+    static_assert(PIECES >= 16, "the swizzle p ^ (r & 15) needs 16 pieces per row (KQ >= 2)");
     __shared__ __attribute__((aligned(16))) f16_t As[2][BM * SK];
     // W per stage: for each matrix and row, one 16-byte entry per k-step
     // (code words of its 64 k, scale), rows padded to WROW entries so the 16
@@ -299,8 +300,10 @@ __global__ __launch_bounds__(64 * WN * KQ) void dq_gemm_kernel(const f16_t *A, c
 // 512: with a grid of at most one block per CU, 8 k-phases (16 waves, 149
 // KB of LDS) are 2-10 % faster than 4; larger grids run 4 (75 KB: two
 // blocks per CU; the fused Q/K/V launch, 512 blocks: 17.1 us against 20.6).
-// The pair always runs 4 (8 would need 164 KB).  One W-row group (64 x 64
-// wave tiles, half the A reads from LDS, 8 waves) is 7-12 % slower than two.
+// The gate/up pair runs 2 (4-wave blocks, 44 KB, 88 VGPRs: its 768 blocks
+// are all resident at once; 48.7 us with 4 k-phases, 39.5 us with 2).  One
+// W-row group (64 x 64 wave tiles, half the A reads from LDS, 8 waves) is
+// 7-12 % slower than two.
 constexpr int WN1 = 2;
 constexpr uint32_t ONE_ROUND_BLOCKS = 256;   // CUs of an MI355X
 
@@ -356,7 +359,7 @@ int nnz_gemm_launch(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, 
         launch_single<NNZ_GEMM_RESADD>(ctx, grid, A, c0, s0, out, P, d.M, d.K, gl, GemmSegs{});
         break;
     case NNZ_GEMM_SILU_PAIR:
-        dq_gemm_kernel<NNZ_GEMM_SILU_PAIR, 2, 4, 2><<<grid, 512, 0, ctx->stream>>>(
+        dq_gemm_kernel<NNZ_GEMM_SILU_PAIR, 2, 2, 2><<<grid, 256, 0, ctx->stream>>>(
             A, c0, s0, (const uint32_t *)wb->codes, (const uint16_t *)wb->scales, out, P, d.M, d.K, gl, GemmSegs{});
         break;
     default:

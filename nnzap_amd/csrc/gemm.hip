@@ -296,6 +296,224 @@ __global__ __launch_bounds__(64 * WN * KQ) void dq_gemm_kernel(const f16_t *A, c
         }
 }
 
+// ---------------------------------------------------------------------------
+// 4-bit (q4_mlx) weights: W = s * n + b per group of >= 64 columns, n a
+// nibble, s and b bf16 (or f16).  s * n + b is not exact in f16, so the
+// MFMA takes the nibbles themselves, exactly: per 64-k step and W row,
+//   sum_k A[p][k] W[r][k] = s_r * (A . n)[p][r] + b_r * (sum_k A[p][k]),
+// with (A . n) and the row sums (A against a fragment of ones) on the MFMA
+// and the two scalings in fp32 -- the Q4 QMV's arithmetic up to fp32
+// summation order.  Nibble pairs become f16 through the exponent trick:
+// 0x6400 | n is the f16 value 1024 + n, and subtracting 1024 (v_pk_add_f16)
+// leaves n exactly.  Epilogues are the BF16-faithful ones of the Q4 decode
+// kernels (q4mv_bf16_specialized.metal:52-57): each result is BF16-truncated
+// before the f16 store, the residual += or the SiLU*mul product's store.
+// Block: 64 tokens x 64 W rows, 4 waves = 2 W-row halves x 2 k-phases;
+// an LDS stage holds 2 k-steps: A (swizzled as above) and, per matrix and
+// row, the 16 code words of the two steps plus their (s | b << 16) words,
+// rows padded to 20 words so a fragment read of 16 rows hits distinct banks.
+constexpr int Q4_KQ = 2, Q4_SK = BK * Q4_KQ, Q4_PIECES = Q4_SK / 8, Q4_THREADS = 256;
+constexpr int Q4_WROW = 20;   // words per W row and stage in LDS
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float q4_param(uint32_t raw16, int sdt) {
+    return sdt == NNZ_BF16 ? bf16_to_f32((uint16_t)raw16) : (float)__builtin_bit_cast(f16_t, (uint16_t)raw16);
+}
+
+// The 8 nibbles of one code word (k ascending from bit 0) as f16 values.
+__device__ __forceinline__ half8 expand_nibbles(uint32_t w) {
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;   // bytes: n[2q], n[2q+1]
+    const half2v k1024 = {(_Float16)1024.f, (_Float16)1024.f};
+    half8 r;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        // byte q of lo into byte 0, byte q of hi into byte 2, zeros elsewhere
+        const uint32_t sel = (uint32_t)q | (0x0Cu << 8) | ((uint32_t)(4 + q) << 16) | (0x0Cu << 24);
+        const uint32_t d = __builtin_amdgcn_perm(hi, lo, sel) | 0x64006400u;
+        const half2v v = __builtin_bit_cast(half2v, d) - k1024;
+        r[2 * q] = v[0];
+        r[2 * q + 1] = v[1];
+    }
+    return r;
+}
+
+template <int MODE, int NMAT>
+__global__ __launch_bounds__(Q4_THREADS) void dq4_gemm_kernel(const f16_t *A, const uint32_t *codes0,
+                                                              const uint16_t *scales0,
+                                                              const uint16_t *biases0,
+                                                              const uint32_t *codes1,
+                                                              const uint16_t *scales1,
+                                                              const uint16_t *biases1, void *out,
+                                                              uint32_t P, uint32_t M, uint32_t K,
+                                                              uint32_t gs_log2, int sdt) {
+    constexpr int A_LOADS = BM * Q4_PIECES / Q4_THREADS;   // 4
+    static_assert(Q4_PIECES >= 16 && 64 * Q4_KQ * NMAT <= Q4_THREADS, "loader shapes");
+    __shared__ __attribute__((aligned(16))) f16_t As[2][BM * Q4_SK];
+    __shared__ __attribute__((aligned(16))) uint32_t Ws[2][NMAT][BN * Q4_WROW];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn = wave & 1, kq = wave >> 1;
+    const uint32_t nx = M / BN, ny = ceil_div(P, BM), L = blockIdx.x;
+    uint32_t bx, by;
+    if ((ny & 7) == 0) {
+        const uint32_t slot = L >> 3;
+        by = 8 * (slot / nx) + (L & 7);
+        bx = slot % nx;
+    } else {
+        bx = L % nx;
+        by = L / nx;
+    }
+    const uint32_t p0 = by * BM, n0 = bx * BN;
+    const uint32_t words_per_row = K / 8, groups_per_row = K >> gs_log2;
+    const uint32_t nk = K / BK, nst = ceil_div(nk, (uint32_t)Q4_KQ);
+
+    float4v acc[NMAT][4][2];
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[m][i][j] = (float4v){0.f, 0.f, 0.f, 0.f};
+
+    const int lp = tid & (Q4_PIECES - 1), lr = tid / Q4_PIECES;
+    constexpr int A_ROW_STEP = Q4_THREADS / Q4_PIECES;
+    const f16_t *arow[A_LOADS];
+#pragma unroll
+    for (int u = 0; u < A_LOADS; ++u)
+        arow[u] = A + (size_t)min(p0 + (uint32_t)(lr + A_ROW_STEP * u), P - 1) * K + (lp & 7) * 8;
+    // W loader: thread t < 128 NMAT takes step t % 2 of row (t / 2) % 64 of
+    // matrix t / 128: 8 code words (two 16-byte loads), scale and bias.
+    const int wl_m = tid >> 7, wl_row = (tid >> 1) & 63, wl_q = tid & 1;
+    const bool wl = wl_m < NMAT;
+    const uint32_t wrow_g = n0 + wl_row;
+    const uint32_t *wl_codes = (NMAT == 2 && wl_m == 1 ? codes1 : codes0) + (size_t)wrow_g * words_per_row;
+    const uint16_t *wl_s = (NMAT == 2 && wl_m == 1 ? scales1 : scales0) + (size_t)wrow_g * groups_per_row;
+    const uint16_t *wl_b = (NMAT == 2 && wl_m == 1 ? biases1 : biases0) + (size_t)wrow_g * groups_per_row;
+    const int gsel = lane >> 4;   // the lane's code word within a 32-k half step
+
+    u32x4 areg[A_LOADS], wc0 = {0u, 0u, 0u, 0u}, wc1 = {0u, 0u, 0u, 0u};
+    uint32_t sbreg = 0;
+    auto issue = [&](uint32_t st) __attribute__((always_inline)) {
+        const uint32_t ka = min(st * Q4_KQ + (uint32_t)(lp >> 3), nk - 1) * BK;
+#pragma unroll
+        for (int u = 0; u < A_LOADS; ++u) areg[u] = *(const u32x4 *)(arow[u] + ka);
+        if (wl) {
+            const uint32_t ks = min(st * Q4_KQ + (uint32_t)wl_q, nk - 1);
+            wc0 = *(const u32x4 *)(wl_codes + 8 * ks);
+            wc1 = *(const u32x4 *)(wl_codes + 8 * ks + 4);
+            const uint32_t g = (ks * BK) >> gs_log2;
+            sbreg = (uint32_t)wl_s[g] | ((uint32_t)wl_b[g] << 16);
+        }
+    };
+    auto stage = [&](uint32_t st) __attribute__((always_inline)) {
+        f16_t *buf = As[st & 1];
+#pragma unroll
+        for (int u = 0; u < A_LOADS; ++u) {
+            const int r = lr + A_ROW_STEP * u;
+            ((u32x4 *)(buf + r * Q4_SK))[lp ^ (r & 15)] = areg[u];
+        }
+        if (wl) {
+            uint32_t *row = Ws[st & 1][wl_m] + wl_row * Q4_WROW;
+            *(u32x4 *)(row + 8 * wl_q) = wc0;
+            *(u32x4 *)(row + 8 * wl_q + 4) = wc1;
+            row[16 + wl_q] = sbreg;
+        }
+    };
+    const half8 ones = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f,
+                        (_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f};
+    auto compute = [&](uint32_t st) __attribute__((always_inline)) {
+        if (st * Q4_KQ + kq >= nk) return;   // wave-uniform
+        const f16_t *buf = As[st & 1];
+        half8 af[2][4];
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const int piece = kq * 8 + kk * 4 + (lane >> 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = i * 16 + (lane & 15);
+                af[kk][i] = *(const half8 *)(buf + r * Q4_SK + 8 * (piece ^ (r & 15)));
+            }
+        }
+        // row sums of A over the step: every column of the product with ones
+        float4v xs[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xs[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[0][i], ones, (float4v){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            xs[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[1][i], ones, xs[i], 0, 0, 0);
+        }
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t *row = Ws[st & 1][m] + (32 * wn + 16 * j + (lane & 15)) * Q4_WROW;
+                const uint32_t sb = row[16 + kq];
+                const float sc = q4_param(sb & 0xFFFFu, sdt), bi = q4_param(sb >> 16, sdt);
+                const half8 b0 = expand_nibbles(row[8 * kq + gsel]);
+                const half8 b1 = expand_nibbles(row[8 * kq + 4 + gsel]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    float4v t = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[0][i], b0, (float4v){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[1][i], b1, t, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[m][i][j][r] += fmaf(sc, t[r], bi * xs[i][r]);
+                }
+            }
+    };
+
+    issue(0);
+    stage(0);
+    step_barrier();
+    for (uint32_t st = 0; st < nst; ++st) {
+        if (st + 1 < nst) issue(st + 1);   // block-uniform
+        compute(st);
+        if (st + 1 < nst) stage(st + 1);
+        step_barrier();
+    }
+
+    // k-phase 1 hands its tiles to phase 0 through the (free) A buffers
+    constexpr int NF = NMAT * 8;
+    static_assert(2 * NF * 64 * 16 <= (int)sizeof(As), "reduction slots fit the stage buffers");
+    float4v *red = (float4v *)&As[0][0];
+    if (kq == 1) {
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) red[((wn * NF) + (m * 4 + i) * 2 + j) * 64 + lane] = acc[m][i][j];
+    }
+    __syncthreads();
+    if (kq != 0) return;   // after the last barrier
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[m][i][j] += red[((wn * NF) + (m * 4 + i) * 2 + j) * 64 + lane];
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t p = p0 + i * 16 + 4 * (lane >> 4) + r;
+            if (p >= P) continue;
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const uint32_t n = n0 + 32 * wn + 16 * j + (lane & 15);
+                const size_t o = (size_t)p * M + n;
+                const float c = acc[0][i][j][r];
+                if constexpr (MODE == NNZ_GEMM_STORE_F16) ((f16_t *)out)[o] = (f16_t)bf16_trunc(c);
+                else if constexpr (MODE == NNZ_GEMM_STORE_F32) ((float *)out)[o] = bf16_trunc(c);
+                else if constexpr (MODE == NNZ_GEMM_RESADD) ((float *)out)[o] += bf16_trunc(c);
+                else {
+                    const float u = acc[NMAT - 1][i][j][r];
+                    ((f16_t *)out)[o] = (f16_t)bf16_trunc(c / (1.f + expf(-c)) * u);
+                }
+            }
+        }
+}
+
 // k-phases and W-row groups of the single-matrix launches.  Measured at P =
 // 512: with a grid of at most one block per CU, 8 k-phases (16 waves, 149
 // KB of LDS) are 2-10 % faster than 4; larger grids run 4 (75 KB: two
@@ -321,11 +539,67 @@ void launch_single(nnz_ctx *ctx, uint32_t grid, const f16_t *A, const uint32_t *
 
 }  // namespace
 
+namespace {
+
+// 4-bit weights (every mode; results BF16-faithful, see dq4_gemm_kernel).
+int gemm4_launch(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, const void *a,
+                 uint32_t P, void *out, int mode, const nnz_qmv_dims &d) {
+    const bool pair = mode == NNZ_GEMM_SILU_PAIR;
+    auto ok = [&](const nnz_qweight *w) {
+        return w && w->bits == 4 && w->codes && w->scales && w->biases &&
+               (uint64_t)w->packed_count == (uint64_t)d.M * d.K && w->group_size == d.group_size &&
+               w->scale_dtype == wa->scale_dtype && ((uintptr_t)w->codes & 15) == 0 &&
+               ((uintptr_t)w->scales & 1) == 0 && ((uintptr_t)w->biases & 1) == 0;
+    };
+    NNZ_REQUIRE(ctx, ok(wa) && (!pair || ok(wb)), NNZ_EINVAL,
+                "dequant_gemm: 4-bit weights need codes (16-byte aligned), scales and biases "
+                "matching the dims");
+    NNZ_REQUIRE(ctx, wa->scale_dtype == NNZ_BF16 || wa->scale_dtype == NNZ_F16, NNZ_EINVAL,
+                "dequant_gemm: scale dtype must be bf16 or f16");
+    NNZ_REQUIRE(ctx, d.M % BN == 0 && d.K % BK == 0 && d.group_size % BK == 0 &&
+                         d.K % d.group_size == 0 && (d.group_size & (d.group_size - 1)) == 0,
+                NNZ_EUNSUPPORTED,
+                "dequant_gemm: need M %% 64 == 0, K %% 64 == 0, power-of-two group size %% 64 == 0");
+    NNZ_REQUIRE(ctx, ((uintptr_t)a & 15) == 0, NNZ_EINVAL, "dequant_gemm: A must be 16-byte aligned");
+    const uint32_t gl = (uint32_t)__builtin_ctz(d.group_size);
+    const uint32_t grid = d.M / BN * ceil_div(P, BM);
+    const f16_t *A = (const f16_t *)a;
+    const uint32_t *c0 = (const uint32_t *)wa->codes;
+    const uint16_t *s0 = (const uint16_t *)wa->scales, *b0 = (const uint16_t *)wa->biases;
+    const int sdt = wa->scale_dtype;
+    switch (mode) {
+    case NNZ_GEMM_STORE_F16:
+        dq4_gemm_kernel<NNZ_GEMM_STORE_F16, 1><<<grid, Q4_THREADS, 0, ctx->stream>>>(
+            A, c0, s0, b0, nullptr, nullptr, nullptr, out, P, d.M, d.K, gl, sdt);
+        break;
+    case NNZ_GEMM_STORE_F32:
+        dq4_gemm_kernel<NNZ_GEMM_STORE_F32, 1><<<grid, Q4_THREADS, 0, ctx->stream>>>(
+            A, c0, s0, b0, nullptr, nullptr, nullptr, out, P, d.M, d.K, gl, sdt);
+        break;
+    case NNZ_GEMM_RESADD:
+        dq4_gemm_kernel<NNZ_GEMM_RESADD, 1><<<grid, Q4_THREADS, 0, ctx->stream>>>(
+            A, c0, s0, b0, nullptr, nullptr, nullptr, out, P, d.M, d.K, gl, sdt);
+        break;
+    case NNZ_GEMM_SILU_PAIR:
+        dq4_gemm_kernel<NNZ_GEMM_SILU_PAIR, 2><<<grid, Q4_THREADS, 0, ctx->stream>>>(
+            A, c0, s0, b0, (const uint32_t *)wb->codes, (const uint16_t *)wb->scales,
+            (const uint16_t *)wb->biases, out, P, d.M, d.K, gl, sdt);
+        break;
+    default:
+        return nnz_fail(ctx, NNZ_EINVAL, "dequant_gemm: unknown mode %d", mode);
+    }
+    NNZ_LAUNCHED(ctx);
+    return NNZ_OK;
+}
+
+}  // namespace
+
 int nnz_gemm_launch(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, const void *a,
                     uint32_t P, void *out, int mode, const nnz_qmv_dims &d) {
     NNZ_REQUIRE(ctx, wa && a && out && P > 0, NNZ_EINVAL, "dequant_gemm: null argument");
+    if (wa->bits == 4) return gemm4_launch(ctx, wa, wb, a, P, out, mode, d);
     NNZ_REQUIRE(ctx, wa->bits == 1 && wa->codes && wa->scales, NNZ_EUNSUPPORTED,
-                "dequant_gemm: Q1 weights only");
+                "dequant_gemm: 1-bit or 4-bit weights");
     NNZ_REQUIRE(ctx, (uint64_t)wa->packed_count == (uint64_t)d.M * d.K && wa->group_size == d.group_size,
                 NNZ_EINVAL, "dequant_gemm: descriptor does not match dims");
     NNZ_REQUIRE(ctx, d.M % BN == 0 && d.K % BK == 0 && d.group_size % BK == 0 &&

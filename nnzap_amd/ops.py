@@ -50,6 +50,14 @@ class Device:
         self.index = index
         self.torch_device = torch.device("cuda", index)
         self.stream = None if own_stream else torch.cuda.current_stream(index)
+        if self.stream is not None and self.stream.cuda_stream == 0:
+            # torch's legacy default stream has handle 0, which nnz_ctx_create
+            # reads as "create your own stream": the library's launches would
+            # then not be ordered with torch's ops (nor with its caching
+            # allocator's reuse of freed tensors).  Make a dedicated stream
+            # (default priority) current for torch and share it instead.
+            self.stream = torch.cuda.Stream(index)
+            torch.cuda.set_stream(self.stream)
         ctx = C.c_void_p()
         handle = None if own_stream else C.c_void_p(self.stream.cuda_stream)
         rc = lib().nnz_ctx_create(index, handle, C.byref(ctx))

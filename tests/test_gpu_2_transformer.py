@@ -10,7 +10,8 @@ from nnzap_amd import ops
 from nnzap_amd import synth as S
 from oracle import oracle as O
 
-from gpu_util import assert_close, assert_close_normwise, from_bits16, host, tdev
+from gpu_util import (assert_bf16_faithful, assert_close, assert_close_normwise, from_bits16, host,
+                      tdev)
 
 pytestmark = pytest.mark.gpu
 
@@ -375,13 +376,49 @@ def test_dequant_gemm_shapes(dev, P, M, K, gs):
     A = a16.astype(np.float64)
     da, db = ops.DeviceQWeight(dev, wa), ops.DeviceQWeight(dev, wb)
     ra, rb = A @ O.dequant(wa).T, A @ O.dequant(wb).T
+    ad = tdev(a16)   # held until the sync: the kernels run on the library's stream
     out32 = torch.empty(P, M, dtype=torch.float32, device="cuda")
-    ops.dispatch_dequant_gemm(dev, da, tdev(a16), out32, L.GEMM_STORE_F32)
+    ops.dispatch_dequant_gemm(dev, da, ad, out32, L.GEMM_STORE_F32)
     out16 = torch.empty(P, M, dtype=torch.float16, device="cuda")
-    ops.dispatch_dequant_gemm(dev, da, tdev(a16), out16, L.GEMM_SILU_PAIR, wb=db)
+    ops.dispatch_dequant_gemm(dev, da, ad, out16, L.GEMM_SILU_PAIR, wb=db)
     dev.sync()
     assert_close(host(out32), ra, what="gemm f32")
     assert_close(host(out16), O.f16(O.silu(ra) * rb), what="gemm silu pair")
+
+
+@pytest.mark.parametrize("P,M,K,gs,sdt", [(37, 256, 2048, 64, 2), (512, 512, 2048, 64, 2),
+                                           (100, 128, 6144, 128, 1), (64, 64, 192, 64, 2)])
+def test_dequant_gemm_q4_modes(dev, P, M, K, gs, sdt):
+    """4-bit (q4_mlx) weights: s * (A . n) + b * sum(A) per group on the MFMA,
+    every mode BF16-faithful like the Q4 decode kernels (one bf16 ulp bar)."""
+    from nnzap_amd import formats as fm
+    sd = fm.DT_BF16 if sdt == 2 else fm.DT_F16
+    wa = cf.q4_matrix(M, K, gs, 520, 521, 522, scale_dtype=sd)
+    wb = cf.q4_matrix(M, K, gs, 523, 524, 525, scale_dtype=sd)
+    a16 = (0.5 * S.normal(526, P * K)).astype(np.float16).reshape(P, K)
+    A = a16.astype(np.float64)
+    da, db = ops.DeviceQWeight(dev, wa), ops.DeviceQWeight(dev, wb)
+    ra, rb = A @ O.dequant(wa).T, A @ O.dequant(wb).T
+    ad = tdev(a16)   # held until the sync: the kernels run on the library's stream
+    out16 = torch.empty(P, M, dtype=torch.float16, device="cuda")
+    ops.dispatch_dequant_gemm(dev, da, ad, out16, L.GEMM_STORE_F16)
+    out32 = torch.empty(P, M, dtype=torch.float32, device="cuda")
+    ops.dispatch_dequant_gemm(dev, da, ad, out32, L.GEMM_STORE_F32)
+    res0 = S.normal(527, P * M).astype(np.float32).reshape(P, M)
+    res = tdev(res0)
+    ops.dispatch_dequant_gemm(dev, da, ad, res, L.GEMM_RESADD)
+    pair = torch.empty(P, M, dtype=torch.float16, device="cuda")
+    ops.dispatch_dequant_gemm(dev, da, ad, pair, L.GEMM_SILU_PAIR, wb=db)
+    dev.sync()
+    assert_bf16_faithful(host(out32), ra, "q4 gemm f32")
+    assert_bf16_faithful(host(out16), ra, "q4 gemm f16")
+    # residual += bf16(sum): one bf16 ulp of the added term (the GPU's fp32 sum
+    # and the fp64 oracle may straddle a truncation boundary) plus the f32 add
+    ref = res0 + O.bf16_trunc(ra)
+    err = np.abs(host(res).astype(np.float64) - ref)
+    assert (err <= 2.0 ** -7 * np.abs(ra) + 2.0 ** -23 * np.abs(ref) + 2.0 ** -30).all(), \
+        f"q4 gemm resadd: {int((err > 2.0 ** -7 * np.abs(ra)).sum())} elements beyond one bf16 ulp"
+    assert_bf16_faithful(host(pair), O.silu(ra) * rb, "q4 gemm silu pair")
 
 
 def test_gemm_row_equals_decode_qmv(dev):

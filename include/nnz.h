@@ -492,8 +492,8 @@ int nnz_model_forward_decode(nnz_model *m, uint32_t token_id, uint32_t position)
 /* Batched prefill (new; the reference prefills token by token through
  * forwardDecode, transformer.zig:4032-4068): tokens[0..n) at positions
  * start..start+n-1 via the dequant-GEMM; leaves the last token's logits in
- * NNZ_T_LOGITS.  `tokens_host` is a host array.  Q4 models run the prompt
- * token by token through the decode step, as the reference does. */
+ * NNZ_T_LOGITS.  `tokens_host` is a host array.  Q4 models use the 4-bit
+ * GEMM with the Q4 rounding points. */
 int nnz_model_prefill(nnz_model *m, const uint32_t *tokens_host, uint32_t n, uint32_t start);
 /* generate (transformer.zig:3942): prefill the prompt, then up to `n_new`
  * decode steps; each step is one replay of a captured hipGraph that picks

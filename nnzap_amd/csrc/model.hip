@@ -67,15 +67,6 @@ __global__ void embed_state_bf16_kernel(const uint32_t *state, const uint16_t *t
     out[d] = bf16_to_f32(table[(size_t)row * hidden + d]);
 }
 
-// State block for prompt token t of a token-by-token prefill.
-__global__ void prefill_state_kernel(uint32_t *state, const uint32_t *ids, uint32_t t, uint32_t start) {
-    state[ST_TOKEN] = ids[t];
-    state[ST_POS] = start + t;
-    state[ST_SEQ] = start + t + 1;
-    state[ST_STEP] = 0;
-    state[ST_DONE] = 0;
-}
-
 __global__ void embed_ids_q1_kernel(const uint32_t *ids, const uint8_t *bits, const uint16_t *scales,
                                     float *out, uint32_t hidden, uint32_t ntok, uint32_t gs,
                                     uint32_t vocab) {
@@ -667,30 +658,33 @@ int nnz_model_prefill(nnz_model *m, const uint32_t *tokens_host, uint32_t n, uin
         NNZ_REQUIRE(ctx, tokens_host[i] < c.vocab_size, NNZ_EINVAL, "prefill: token id out of range");
     RC(ensure_prefill_buffers(m, n, start));
     NNZ_HIP(ctx, hipMemcpyAsync(m->p_ids, tokens_host, (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream));
-    if (is_q4(m)) {
-        // chunkedPrefill (transformer.zig:4032-4068): one decode step per
-        // prompt token; the last one leaves its logits.
-        for (uint32_t t = 0; t < n; ++t) {
-            prefill_state_kernel<<<1, 1, 0, ctx->stream>>>(m->state, m->p_ids, t, start);
-            NNZ_LAUNCHED(ctx);
-            RC(enqueue_decode_step(m, start + t + 1));
-        }
-        return NNZ_OK;
-    }
     const uint32_t H = c.hidden_size;
-    if (c.embed_kind == NNZ_EMBED_Q1)
-        embed_ids_q1_kernel<<<ceil_div(n * H, 256), 256, 0, ctx->stream>>>(
-            m->p_ids, (const uint8_t *)m->emb, (const uint16_t *)m->emb_scales, m->p_res, H, n,
-            c.group_size, c.vocab_size);
-    else
-        embed_ids_bf16_kernel<<<ceil_div(n * H, 256), 256, 0, ctx->stream>>>(
-            m->p_ids, (const uint16_t *)m->emb, m->p_res, H, n, c.vocab_size);
-    NNZ_LAUNCHED(ctx);
+    // q4_mlx models take the Q4 rounding points (transformer.zig:2646, :2977,
+    // :3100): BF16-truncated embedding rows and norm outputs; the 4-bit GEMMs
+    // truncate their results like the Q4 decode kernels.
+    const int tr = is_q4(m) ? 1 : 0;
+    if (c.embed_kind == NNZ_EMBED_Q4) {
+        RC(nnz_dispatch_embedding_lookup_q4(ctx, m->p_ids, m->emb, m->emb_scales, m->emb_biases,
+                                            m->p_res, {c.vocab_size, H, n, c.group_size}));
+    } else {
+        if (c.embed_kind == NNZ_EMBED_Q1)
+            embed_ids_q1_kernel<<<ceil_div(n * H, 256), 256, 0, ctx->stream>>>(
+                m->p_ids, (const uint8_t *)m->emb, (const uint16_t *)m->emb_scales, m->p_res, H, n,
+                c.group_size, c.vocab_size);
+        else
+            embed_ids_bf16_kernel<<<ceil_div(n * H, 256), 256, 0, ctx->stream>>>(
+                m->p_ids, (const uint16_t *)m->emb, m->p_res, H, n, c.vocab_size);
+        NNZ_LAUNCHED(ctx);
+    }
     const uint32_t nch = ceil_div(start + n, 512);
     for (uint32_t l = 0; l < c.num_layers; ++l) {
         Layer &Ly = m->L[l];
-        RC(nnz_dispatch_rms_norm(ctx, m->p_res, Ly.attn_norm, m->p_xn, NNZ_F16, 0, {H, n, c.rms_eps}));
-        {   // Q, K and V in one launch (row segments of one grid)
+        RC(nnz_dispatch_rms_norm(ctx, m->p_res, Ly.attn_norm, m->p_xn, NNZ_F16, tr, {H, n, c.rms_eps}));
+        if (is_q4(m)) {
+            RC(nnz_gemm_launch(ctx, &Ly.q.w, nullptr, m->p_xn, n, m->p_q, NNZ_GEMM_STORE_F16, dims_of(m, Ly.q)));
+            RC(nnz_gemm_launch(ctx, &Ly.k.w, nullptr, m->p_xn, n, m->p_k, NNZ_GEMM_STORE_F16, dims_of(m, Ly.k)));
+            RC(nnz_gemm_launch(ctx, &Ly.v.w, nullptr, m->p_xn, n, m->p_v, NNZ_GEMM_STORE_F16, dims_of(m, Ly.v)));
+        } else {   // Q, K and V in one launch (row segments of one grid)
             const nnz_qweight *ws[3] = {&Ly.q.w, &Ly.k.w, &Ly.v.w};
             void *outs[3] = {m->p_q, m->p_k, m->p_v};
             RC(nnz_gemm_segments_launch(ctx, ws, outs, 3, m->p_xn, n, H, c.group_size));
@@ -722,13 +716,13 @@ int nnz_model_prefill(nnz_model *m, const uint32_t *tokens_host, uint32_t n, uin
         RC(nnz_attn_launch_ex(ctx, ac));
         }
         RC(nnz_gemm_launch(ctx, &Ly.o.w, nullptr, m->p_att, n, m->p_res, NNZ_GEMM_RESADD, dims_of(m, Ly.o)));
-        RC(nnz_dispatch_rms_norm(ctx, m->p_res, Ly.ffn_norm, m->p_xn, NNZ_F16, 0, {H, n, c.rms_eps}));
+        RC(nnz_dispatch_rms_norm(ctx, m->p_res, Ly.ffn_norm, m->p_xn, NNZ_F16, tr, {H, n, c.rms_eps}));
         RC(nnz_gemm_launch(ctx, &Ly.gate.w, &Ly.up.w, m->p_xn, n, m->p_h, NNZ_GEMM_SILU_PAIR,
                            dims_of(m, Ly.gate)));
         RC(nnz_gemm_launch(ctx, &Ly.down.w, nullptr, m->p_h, n, m->p_res, NNZ_GEMM_RESADD,
                            dims_of(m, Ly.down)));
     }
-    RC(nnz_dispatch_rms_norm(ctx, m->p_res + (size_t)(n - 1) * H, m->final_norm, m->xn, NNZ_F16, 0,
+    RC(nnz_dispatch_rms_norm(ctx, m->p_res + (size_t)(n - 1) * H, m->final_norm, m->xn, NNZ_F16, tr,
                              {H, 1, c.rms_eps}));
     NNZ_HIP(ctx, hipMemcpyAsync(m->residual, m->p_res + (size_t)(n - 1) * H, (size_t)H * 4,
                                 hipMemcpyDeviceToDevice, ctx->stream));

@@ -195,8 +195,8 @@ def tiny_q4():
 
 
 def test_tiny_q4_prefill_and_decode_logits(mdev, tiny_q4):
-    """Q4 prefill (token by token through the decode step, as the reference's
-    chunkedPrefill) and single decode steps against the oracle."""
+    """Q4 prefill (batched, 4-bit GEMMs with the Q4 rounding points) and
+    single decode steps against the oracle."""
     cfg, w = tiny_q4
     m = DecoderModel(mdev, cfg)
     try:
@@ -229,6 +229,24 @@ def test_tiny_q4_generate_matches_oracle(mdev, tiny_q4, use_graph):
         assert np.max(np.abs(margins - ref_margins)) < 2e-2   # two logit errors, logits O(1)
     finally:
         m.close()
+
+
+def test_tiny_q4_prefill_chunks_match_single_prefill(mdev, tiny_q4):
+    """Two Q4 prefill calls (start 0, start 30) equal one over the same tokens."""
+    cfg, w = tiny_q4
+    ids = cf.prompt_ids(cfg, 60)
+    a = DecoderModel(mdev, cfg)
+    b = DecoderModel(mdev, cfg)
+    try:
+        a.load(w)
+        la = a.prefill(ids, 0)
+        b.load(w)
+        b.prefill(ids[:30], 0)
+        lb = b.prefill(ids[30:], 30)
+        assert_close_normwise(lb, la, rtol=Q4_RTOL, what="q4 chunked prefill")
+    finally:
+        a.close()
+        b.close()
 
 
 def test_q4_checkpoint_model_matches_oracle(mdev, tmp_path):

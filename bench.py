@@ -229,6 +229,7 @@ def _kernel_cases():
     import torch
     from nnzap_amd import _lib as L
     from nnzap_amd import configs as cf
+    from nnzap_amd import formats as fm
     from nnzap_amd import ops
 
     f32, f16 = torch.float32, torch.float16
@@ -395,15 +396,21 @@ def _kernel_cases():
             return us, 4096 * L_ + 12288, None
         return run
 
-    def prefill_gemm(M_, K_, mode, pair=False):
+    def prefill_gemm(M_, K_, mode, pair=False, q4=False):
         # one prefill dequant-GEMM of the decoder at a 512-token prompt:
-        # C[512 x M] = A[512 x K] . W^T (1-bit W, f16 A), reported as MFMA
-        # throughput; weights rotated like the QMV cases
+        # C[512 x M] = A[512 x K] . W^T (1-bit W, or q4_mlx gs64 with bf16
+        # scales/biases; f16 A), reported as MFMA throughput; weights rotated
+        # like the QMV cases
+        def mat(seed):
+            if q4:
+                return cf.q4_matrix(M_, K_, 64, seed, seed + 10, seed + 20, scale_dtype=fm.DT_BF16)
+            return cf.q1_matrix(M_, K_, 128, seed, seed + 10)
+
         def run(dev, n):
             P = 512
-            wa = cf.q1_matrix(M_, K_, 128, 600, 601)
+            wa = mat(600)
             ra = Rot(dev, wa, ROTATE_BYTES // (2 if pair else 1))
-            rb = Rot(dev, cf.q1_matrix(M_, K_, 128, 602, 603), ROTATE_BYTES // 2) if pair else None
+            rb = Rot(dev, mat(602), ROTATE_BYTES // 2) if pair else None
             a16 = (torch.randn(P, K_, device="cuda") * 0.5).to(f16)
             o = torch.empty(P, M_, dtype=f16 if mode in (L.GEMM_STORE_F16, L.GEMM_SILU_PAIR) else f32,
                             device="cuda")
@@ -461,6 +468,8 @@ def _kernel_cases():
         "prefill_gemm_o_resadd": prefill_gemm(H, QD, L.GEMM_RESADD),
         "prefill_gemm_gate_up_silu": prefill_gemm(I, H, L.GEMM_SILU_PAIR, pair=True),
         "prefill_gemm_down_resadd": prefill_gemm(H, I, L.GEMM_RESADD),
+        "prefill_gemm_q4_gate_up_silu": prefill_gemm(I, H, L.GEMM_SILU_PAIR, pair=True, q4=True),
+        "prefill_gemm_q4_down_resadd": prefill_gemm(H, I, L.GEMM_RESADD, q4=True),
         "sample_topk40_topp095": sample(0.8, 40, 0.95),
         "sample_topp090": sample(1.0, 0, 0.9),
         "sample_topp090_peaked": sample(1.0, 0, 0.9, peaked=True),

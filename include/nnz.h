@@ -257,7 +257,12 @@ int nnz_dispatch_dequant(nnz_ctx *ctx, const nnz_qweight *w, float *output, nnz_
  * C[P x M] = A[P x K] (f16, row-major) . dequant(W[M x K])^T, fp32 accumulate on
  * MFMA.  Epilogue `mode`: NNZ_GEMM_STORE_F16 (C -> f16 out), NNZ_GEMM_STORE_F32,
  * NNZ_GEMM_RESADD (out_f32[p*M+m] += C), NNZ_GEMM_SILU_PAIR (wb required:
- * out f16 = silu(A.Wa^T) * (A.Wb^T)).  Q1 weights only.  `lda` = K. */
+ * out f16 = silu(A.Wa^T) * (A.Wb^T)).  `lda` = K.  Q1 weights: codes 8-byte
+ * aligned.  Q4 weights (q4_mlx, bf16 or f16 scales and biases, codes 16-byte
+ * aligned): every result is BF16-truncated before its store, += or the
+ * SiLU*mul product's store, like the Q4 decode kernels
+ * (q4mv_bf16_specialized.metal:52-57).  M, K and the group size multiples of
+ * 64, the group size a power of two. */
 #define NNZ_GEMM_STORE_F16 0
 #define NNZ_GEMM_STORE_F32 1
 #define NNZ_GEMM_RESADD    2

@@ -312,8 +312,10 @@ __global__ __launch_bounds__(64 * WN * KQ) void dq_gemm_kernel(const f16_t *A, c
 // an LDS stage holds 2 k-steps: A (swizzled as above) and, per matrix and
 // row, the 16 code words of the two steps plus their (s | b << 16) words,
 // rows padded to 20 words so a fragment read of 16 rows hits distinct banks.
-constexpr int Q4_KQ = 2, Q4_SK = BK * Q4_KQ, Q4_PIECES = Q4_SK / 8, Q4_THREADS = 256;
-constexpr int Q4_WROW = 20;   // words per W row and stage in LDS
+// KQ k-phases: 4 KQ waves (2 W-row halves x KQ), LDS stages of KQ k-steps;
+// a W row holds 8 code words per step plus one (s | b << 16) word per step,
+// padded to a stride of 4 x odd words (20 for KQ = 2, 36 for KQ = 4).
+template <int KQ> constexpr int Q4_WROW = KQ == 2 ? 20 : 36;
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float q4_param(uint32_t raw16, int sdt) {
@@ -337,8 +339,8 @@ __device__ __forceinline__ half8 expand_nibbles(uint32_t w) {
     return r;
 }
 
-template <int MODE, int NMAT>
-__global__ __launch_bounds__(Q4_THREADS) void dq4_gemm_kernel(const f16_t *A, const uint32_t *codes0,
+template <int MODE, int NMAT, int KQ>
+__global__ __launch_bounds__(128 * KQ) void dq4_gemm_kernel(const f16_t *A, const uint32_t *codes0,
                                                               const uint16_t *scales0,
                                                               const uint16_t *biases0,
                                                               const uint32_t *codes1,
@@ -346,10 +348,12 @@ __global__ __launch_bounds__(Q4_THREADS) void dq4_gemm_kernel(const f16_t *A, co
                                                               const uint16_t *biases1, void *out,
                                                               uint32_t P, uint32_t M, uint32_t K,
                                                               uint32_t gs_log2, int sdt) {
+    constexpr int Q4_KQ = KQ, Q4_SK = BK * KQ, Q4_PIECES = Q4_SK / 8, Q4_THREADS = 128 * KQ;
+    constexpr int WR = Q4_WROW<KQ>;
     constexpr int A_LOADS = BM * Q4_PIECES / Q4_THREADS;   // 4
-    static_assert(Q4_PIECES >= 16 && 64 * Q4_KQ * NMAT <= Q4_THREADS, "loader shapes");
+    static_assert(Q4_PIECES >= 16 && 64 * Q4_KQ * NMAT <= Q4_THREADS && WR >= 9 * KQ, "loader shapes");
     __shared__ __attribute__((aligned(16))) f16_t As[2][BM * Q4_SK];
-    __shared__ __attribute__((aligned(16))) uint32_t Ws[2][NMAT][BN * Q4_WROW];
+    __shared__ __attribute__((aligned(16))) uint32_t Ws[2][NMAT][BN * WR];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -382,9 +386,9 @@ __global__ __launch_bounds__(Q4_THREADS) void dq4_gemm_kernel(const f16_t *A, co
 #pragma unroll
     for (int u = 0; u < A_LOADS; ++u)
         arow[u] = A + (size_t)min(p0 + (uint32_t)(lr + A_ROW_STEP * u), P - 1) * K + (lp & 7) * 8;
-    // W loader: thread t < 128 NMAT takes step t % 2 of row (t / 2) % 64 of
-    // matrix t / 128: 8 code words (two 16-byte loads), scale and bias.
-    const int wl_m = tid >> 7, wl_row = (tid >> 1) & 63, wl_q = tid & 1;
+    // W loader: thread t < 64 KQ NMAT takes step t % KQ of row (t / KQ) % 64
+    // of matrix t / (64 KQ): 8 code words (two 16-byte loads), scale and bias.
+    const int wl_m = tid / (64 * KQ), wl_row = (tid / KQ) & 63, wl_q = tid % KQ;
     const bool wl = wl_m < NMAT;
     const uint32_t wrow_g = n0 + wl_row;
     const uint32_t *wl_codes = (NMAT == 2 && wl_m == 1 ? codes1 : codes0) + (size_t)wrow_g * words_per_row;
@@ -414,10 +418,10 @@ __global__ __launch_bounds__(Q4_THREADS) void dq4_gemm_kernel(const f16_t *A, co
             ((u32x4 *)(buf + r * Q4_SK))[lp ^ (r & 15)] = areg[u];
         }
         if (wl) {
-            uint32_t *row = Ws[st & 1][wl_m] + wl_row * Q4_WROW;
+            uint32_t *row = Ws[st & 1][wl_m] + wl_row * WR;
             *(u32x4 *)(row + 8 * wl_q) = wc0;
             *(u32x4 *)(row + 8 * wl_q + 4) = wc1;
-            row[16 + wl_q] = sbreg;
+            row[8 * KQ + wl_q] = sbreg;
         }
     };
     const half8 ones = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f,
@@ -446,8 +450,8 @@ __global__ __launch_bounds__(Q4_THREADS) void dq4_gemm_kernel(const f16_t *A, co
         for (int m = 0; m < NMAT; ++m)
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const uint32_t *row = Ws[st & 1][m] + (32 * wn + 16 * j + (lane & 15)) * Q4_WROW;
-                const uint32_t sb = row[16 + kq];
+                const uint32_t *row = Ws[st & 1][m] + (32 * wn + 16 * j + (lane & 15)) * WR;
+                const uint32_t sb = row[8 * KQ + kq];
                 const float sc = q4_param(sb & 0xFFFFu, sdt), bi = q4_param(sb >> 16, sdt);
                 const half8 b0 = expand_nibbles(row[8 * kq + gsel]);
                 const half8 b1 = expand_nibbles(row[8 * kq + 4 + gsel]);
@@ -471,26 +475,35 @@ __global__ __launch_bounds__(Q4_THREADS) void dq4_gemm_kernel(const f16_t *A, co
         step_barrier();
     }
 
-    // k-phase 1 hands its tiles to phase 0 through the (free) A buffers
+    // k-phase tree through the (free) A buffers: phases [h, 2h) hand their
+    // tiles to [0, h)
     constexpr int NF = NMAT * 8;
-    static_assert(2 * NF * 64 * 16 <= (int)sizeof(As), "reduction slots fit the stage buffers");
+    static_assert(KQ / 2 * 2 * NF * 64 * 16 <= (int)sizeof(As), "reduction slots fit the stage buffers");
     float4v *red = (float4v *)&As[0][0];
-    if (kq == 1) {
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m)
+    for (int h = KQ / 2; h >= 1; h /= 2) {
+        if (kq >= h && kq < 2 * h) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int m = 0; m < NMAT; ++m)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) red[((wn * NF) + (m * 4 + i) * 2 + j) * 64 + lane] = acc[m][i][j];
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        red[(((kq - h) * 2 + wn) * NF + (m * 4 + i) * 2 + j) * 64 + lane] = acc[m][i][j];
+        }
+        __syncthreads();
+        if (kq < h) {
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[m][i][j] += red[((kq * 2 + wn) * NF + (m * 4 + i) * 2 + j) * 64 + lane];
+        }
+        __syncthreads();
     }
-    __syncthreads();
     if (kq != 0) return;   // after the last barrier
-#pragma unroll
-    for (int m = 0; m < NMAT; ++m)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) acc[m][i][j] += red[((wn * NF) + (m * 4 + i) * 2 + j) * 64 + lane];
 
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -569,19 +582,31 @@ int gemm4_launch(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, con
     const int sdt = wa->scale_dtype;
     switch (mode) {
     case NNZ_GEMM_STORE_F16:
-        dq4_gemm_kernel<NNZ_GEMM_STORE_F16, 1><<<grid, Q4_THREADS, 0, ctx->stream>>>(
-            A, c0, s0, b0, nullptr, nullptr, nullptr, out, P, d.M, d.K, gl, sdt);
+        if (grid <= ONE_ROUND_BLOCKS)
+            dq4_gemm_kernel<NNZ_GEMM_STORE_F16, 1, 4><<<grid, 512, 0, ctx->stream>>>(
+                A, c0, s0, b0, nullptr, nullptr, nullptr, out, P, d.M, d.K, gl, sdt);
+        else
+            dq4_gemm_kernel<NNZ_GEMM_STORE_F16, 1, 2><<<grid, 256, 0, ctx->stream>>>(
+                A, c0, s0, b0, nullptr, nullptr, nullptr, out, P, d.M, d.K, gl, sdt);
         break;
     case NNZ_GEMM_STORE_F32:
-        dq4_gemm_kernel<NNZ_GEMM_STORE_F32, 1><<<grid, Q4_THREADS, 0, ctx->stream>>>(
-            A, c0, s0, b0, nullptr, nullptr, nullptr, out, P, d.M, d.K, gl, sdt);
+        if (grid <= ONE_ROUND_BLOCKS)
+            dq4_gemm_kernel<NNZ_GEMM_STORE_F32, 1, 4><<<grid, 512, 0, ctx->stream>>>(
+                A, c0, s0, b0, nullptr, nullptr, nullptr, out, P, d.M, d.K, gl, sdt);
+        else
+            dq4_gemm_kernel<NNZ_GEMM_STORE_F32, 1, 2><<<grid, 256, 0, ctx->stream>>>(
+                A, c0, s0, b0, nullptr, nullptr, nullptr, out, P, d.M, d.K, gl, sdt);
         break;
     case NNZ_GEMM_RESADD:
-        dq4_gemm_kernel<NNZ_GEMM_RESADD, 1><<<grid, Q4_THREADS, 0, ctx->stream>>>(
-            A, c0, s0, b0, nullptr, nullptr, nullptr, out, P, d.M, d.K, gl, sdt);
+        if (grid <= ONE_ROUND_BLOCKS)
+            dq4_gemm_kernel<NNZ_GEMM_RESADD, 1, 4><<<grid, 512, 0, ctx->stream>>>(
+                A, c0, s0, b0, nullptr, nullptr, nullptr, out, P, d.M, d.K, gl, sdt);
+        else
+            dq4_gemm_kernel<NNZ_GEMM_RESADD, 1, 2><<<grid, 256, 0, ctx->stream>>>(
+                A, c0, s0, b0, nullptr, nullptr, nullptr, out, P, d.M, d.K, gl, sdt);
         break;
     case NNZ_GEMM_SILU_PAIR:
-        dq4_gemm_kernel<NNZ_GEMM_SILU_PAIR, 2><<<grid, Q4_THREADS, 0, ctx->stream>>>(
+        dq4_gemm_kernel<NNZ_GEMM_SILU_PAIR, 2, 2><<<grid, 256, 0, ctx->stream>>>(
             A, c0, s0, b0, (const uint32_t *)wb->codes, (const uint16_t *)wb->scales,
             (const uint16_t *)wb->biases, out, P, d.M, d.K, gl, sdt);
         break;

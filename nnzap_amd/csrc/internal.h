@@ -43,7 +43,10 @@ int nnz_attn_fused1_launch(nnz_ctx *ctx, const void *q, const void *kr, const vo
 int nnz_qmv_norm_qkv_launch(nnz_ctx *ctx, const nnz_qweight *wq, const nnz_qweight *wk,
                             const nnz_qweight *wv, const float *residual, const float *norm_w,
                             void *q, void *k, void *v, uint32_t qrows, uint32_t kvrows, uint32_t K,
-                            uint32_t gs);
+                            uint32_t gs, float eps);
+int nnz_qmv_norm_pair_silu_launch(nnz_ctx *ctx, const nnz_qweight *wg, const nnz_qweight *wu,
+                                  const float *residual, const float *norm_w, void *out,
+                                  nnz_qmv_dims d, float eps);
 // Largest attention chunk count the merge-in-O-projection path accepts.
 constexpr uint32_t NNZ_O_MERGE_MAX_CHUNKS = 16;
 int nnz_qmv_merge_resadd_launch(nnz_ctx *ctx, const nnz_qweight *w, const float *part_o,
@@ -51,7 +54,7 @@ int nnz_qmv_merge_resadd_launch(nnz_ctx *ctx, const nnz_qweight *w, const float 
                                 uint32_t nchunks, uint32_t chunk, uint32_t head_dim,
                                 float *residual, nnz_qmv_dims d);
 int nnz_qmv_norm_f32out_launch(nnz_ctx *ctx, const nnz_qweight *w, const float *residual,
-                               const float *norm_w, float *out, nnz_qmv_dims d);
+                               const float *norm_w, float *out, nnz_qmv_dims d, float eps);
 int nnz_gemm_launch(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, const void *a,
                     uint32_t P, void *out, int mode, const nnz_qmv_dims &d);
 

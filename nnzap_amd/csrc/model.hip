@@ -350,7 +350,7 @@ int enqueue_decode_step(nnz_model *m, uint32_t max_seq) {
         // transformer.zig:3024-3083 encodeAttnProjFusedNorm: the Q and the K/V
         // dispatches share one normalised input -> one launch here.
         RC(nnz_qmv_norm_qkv_launch(ctx, &Ly.q.w, &Ly.k.w, &Ly.v.w, m->residual, Ly.attn_norm, m->q,
-                                   m->k, m->v, m->qdim, m->kvdim, H, c.group_size));
+                                   m->k, m->v, m->qdim, m->kvdim, H, c.group_size, c.rms_eps));
         // transformer.zig:3244-3370 encodeAttentionGather: Q/K norm, RoPE, KV
         // append and attention in one launch, then O-proj with residual +=.
         // Up to MERGE chunks of partials, the O-projection merges them itself.
@@ -370,21 +370,18 @@ int enqueue_decode_step(nnz_model *m, uint32_t max_seq) {
         else
             RC(nnz_dispatch_qmv_f16io_resadd(ctx, &Ly.o.w, m->att, m->residual, dims_of(m, Ly.o)));
         // transformer.zig:3372-3646 encodeMLPHalf (fused norm + gate/up + SiLU, down += )
-        if (is_q4(m)) {
-            RC(nnz_dispatch_q4_fused_norm_pair_silu_f16io(ctx, &Ly.gate.w, &Ly.up.w, m->residual, m->h,
-                                                          Ly.ffn_norm, dims_of(m, Ly.gate)));
+        RC(nnz_qmv_norm_pair_silu_launch(ctx, &Ly.gate.w, &Ly.up.w, m->residual, Ly.ffn_norm, m->h,
+                                         dims_of(m, Ly.gate), c.rms_eps));
+        if (is_q4(m))
             RC(nnz_dispatch_q4mv_f16io_resadd(ctx, &Ly.down.w, m->h, m->residual, dims_of(m, Ly.down)));
-        } else {
-            RC(nnz_dispatch_fused_norm_pair_silu_f16io(ctx, &Ly.gate.w, &Ly.up.w, m->residual, m->h,
-                                                       Ly.ffn_norm, dims_of(m, Ly.gate)));
+        else
             RC(nnz_dispatch_qmv_f16io_resadd(ctx, &Ly.down.w, m->h, m->residual, dims_of(m, Ly.down)));
-        }
     }
     // transformer.zig:2730-2785 encodeFinalNormAndLMHead (norm fused into the
     // 1-bit LM head; the tied bf16 head keeps a separate norm)
     if (c.lm_head_kind == NNZ_LMHEAD_Q1 || c.lm_head_kind == NNZ_LMHEAD_Q4)
         return nnz_qmv_norm_f32out_launch(ctx, &m->lm.w, m->residual, m->final_norm, m->logits,
-                                          dims_of(m, m->lm));
+                                          dims_of(m, m->lm), c.rms_eps);
     RC(nnz_dispatch_rms_norm(ctx, m->residual, m->final_norm, m->xn, NNZ_F16, 0,
                              {H, 1, c.rms_eps}));
     return lm_head(m, m->xn, m->logits);
@@ -639,6 +636,8 @@ int nnz_model_forward_decode(nnz_model *m, uint32_t token_id, uint32_t position)
                 "forward_decode: position %u >= max_context_length", position);
     NNZ_REQUIRE(ctx, token_id < m->c.vocab_size, NNZ_EINVAL, "forward_decode: token id out of range");
     NNZ_REQUIRE(ctx, !ctx->capturing, NNZ_ESTATE, "forward_decode: use generate() for graphs");
+    NNZ_REQUIRE(ctx, !m->step_graph, NNZ_ESTATE,
+                "forward_decode: a decode stream is active (call decode_end first)");
     const uint32_t st[ST_WORDS] = {token_id, position, position + 1, 0, 0};
     NNZ_HIP(ctx, hipMemcpyAsync(m->state, st, sizeof(st), hipMemcpyHostToDevice, ctx->stream));
     NNZ_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -654,6 +653,11 @@ int nnz_model_prefill(nnz_model *m, const uint32_t *tokens_host, uint32_t n, uin
     NNZ_REQUIRE(ctx, (uint64_t)start + n <= c.max_context_length, NNZ_EINVAL,
                 "prefill: positions exceed max_context_length");
     NNZ_REQUIRE(ctx, !ctx->capturing, NNZ_ESTATE, "prefill: not capturable");
+    // A captured decode stream replays an attention plan sized for its own
+    // sequence; rewriting the KV cache or the state block under it would
+    // make its later steps silently wrong.
+    NNZ_REQUIRE(ctx, !m->step_graph, NNZ_ESTATE,
+                "prefill: a decode stream is active (call decode_end first)");
     for (uint32_t i = 0; i < n; ++i)
         NNZ_REQUIRE(ctx, tokens_host[i] < c.vocab_size, NNZ_EINVAL, "prefill: token id out of range");
     RC(ensure_prefill_buffers(m, n, start));
@@ -756,6 +760,10 @@ int begin_decode(nnz_model *m, const uint32_t *prompt, uint32_t n_prompt, uint32
         nnz_rng_seed_words(m->sp.seed, rs);
         NNZ_HIP(ctx, hipMemcpyAsync(m->rng, rs, sizeof(rs), hipMemcpyHostToDevice, ctx->stream));
     }
+    // st and rs live on this stack frame: wait for the uploads before
+    // returning (as forward_decode does) rather than rely on the runtime
+    // staging pageable copies.
+    NNZ_HIP(ctx, hipStreamSynchronize(ctx->stream));
     RC(enqueue_argmax_advance(m));
     *max_seq = n_prompt + max_new;
     uint32_t chunk, nch;
@@ -788,6 +796,8 @@ int nnz_model_generate(nnz_model *m, const uint32_t *prompt, uint32_t n_prompt, 
     if (!m) return NNZ_EINVAL;
     nnz_ctx *ctx = m->ctx;
     NNZ_REQUIRE(ctx, out_tokens, NNZ_EINVAL, "generate: null output");
+    NNZ_REQUIRE(ctx, !m->step_graph, NNZ_ESTATE,
+                "generate: a decode stream is active (call decode_end first)");
     uint32_t max_seq;
     RC(begin_decode(m, prompt, n_prompt, n_new, &max_seq));
     std::vector<hipEvent_t> ev;
@@ -840,6 +850,8 @@ int nnz_model_set_sampling(nnz_model *m, const nnz_sampling_params *p) {
     NNZ_REQUIRE(m->ctx, p, NNZ_EINVAL, "set_sampling: null params");
     NNZ_REQUIRE(m->ctx, p->temperature >= 0.f && p->temperature <= 3.0e38f, NNZ_EINVAL,
                 "set_sampling: temperature must be >= 0");
+    NNZ_REQUIRE(m->ctx, p->top_p > 0.f, NNZ_EINVAL,
+                "set_sampling: top_p must be > 0 (>= 1 disables it)");
     NNZ_REQUIRE(m->ctx, !m->step_graph, NNZ_ESTATE, "set_sampling: a decode stream is active");
     m->sp = *p;
     return NNZ_OK;

@@ -846,7 +846,7 @@ int launch_nv(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks, bool lut) 
 template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH>
 int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg_rows, int nw,
                   const void *x, const float *norm_w, void *const *out, nnz_qmv_dims d,
-                  const char *name, const MergeIn *merge = nullptr) {
+                  const char *name, const MergeIn *merge = nullptr, float eps = 1e-6f) {
     constexpr bool NORM = XIN == XIN_NORM;
     constexpr bool MERGE = XIN == XIN_MERGE;
     NNZ_CHECK_CTX(ctx);
@@ -984,7 +984,7 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
     a.gs = d.group_size;
     a.lpr_log2 = (uint32_t)lpr_log2;
     a.sdt = w[0]->scale_dtype;
-    a.eps = 1e-6f;
+    a.eps = eps;
     switch (nv) {
     case 1: return launch_nv<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, 1>(ctx, a, R, blocks, lut);
     case 2: return launch_nv<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, 2>(ctx, a, R, blocks, lut);
@@ -995,13 +995,14 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
 
 template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH>
 int launch_qmv(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, const void *x,
-               const float *norm_w, void *out0, void *out1, nnz_qmv_dims d, const char *name) {
+               const float *norm_w, void *out0, void *out1, nnz_qmv_dims d, const char *name,
+               float eps = 1e-6f) {
     const nnz_qweight *w[2] = {wa, wb};
     void *out[2] = {out0, out1};
     const uint32_t rows[1] = {d.M};
     if (NMAT == 2) NNZ_REQUIRE(ctx, wb != nullptr, NNZ_EINVAL, "%s: null second weight", name);
     return launch_qmv_ex<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH>(ctx, w, rows, NMAT, x, norm_w, out, d,
-                                                                  name);
+                                                                  name, nullptr, eps);
 }
 
 }  // namespace
@@ -1016,19 +1017,38 @@ int launch_qmv(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, const
 // q4mv_bf16_specialized.metal:52-57, :806).
 
 // RMSNorm prologue + Q, K and V projections in one launch (f16 outputs).
+// `eps` is the model's RMSNorm epsilon (the reference's fused kernels use
+// 1e-6, qmv_specialized.metal:1158; the public dispatchers keep that value).
 int nnz_qmv_norm_qkv_launch(nnz_ctx *ctx, const nnz_qweight *wq, const nnz_qweight *wk,
                             const nnz_qweight *wv, const float *residual, const float *norm_w,
                             void *q, void *k, void *v, uint32_t qrows, uint32_t kvrows, uint32_t K,
-                            uint32_t gs) {
+                            uint32_t gs, float eps) {
     const nnz_qweight *w[3] = {wq, wk, wv};
     void *out[3] = {q, k, v};
     const uint32_t rows[3] = {qrows, kvrows, kvrows};
     NNZ_REQUIRE(ctx, wq != nullptr, NNZ_EINVAL, "norm_qkv: null weight");
     if (wq->bits == 4)
         return launch_qmv_ex<4, NNZ_F32, 1, true, EPI_STORE, NNZ_F16, true>(
-            ctx, w, rows, 3, residual, norm_w, out, {qrows + 2 * kvrows, K, gs}, "q4_norm_qkv");
+            ctx, w, rows, 3, residual, norm_w, out, {qrows + 2 * kvrows, K, gs}, "q4_norm_qkv",
+            nullptr, eps);
     return launch_qmv_ex<1, NNZ_F32, 1, true, EPI_STORE, NNZ_F16, false>(
-        ctx, w, rows, 3, residual, norm_w, out, {qrows + 2 * kvrows, K, gs}, "norm_qkv");
+        ctx, w, rows, 3, residual, norm_w, out, {qrows + 2 * kvrows, K, gs}, "norm_qkv", nullptr,
+        eps);
+}
+
+// RMSNorm prologue + gate/up pair + SiLU*mul (f16 output) with the model's
+// epsilon: the reference's qmv_spec_fused_norm_pair_silu_f16io /
+// q4mv_spec_fused_norm_pair_silu_f16io (qmv_specialized.metal:1083-1279,
+// q4mv_bf16_specialized.metal:716-865).
+int nnz_qmv_norm_pair_silu_launch(nnz_ctx *ctx, const nnz_qweight *wg, const nnz_qweight *wu,
+                                  const float *residual, const float *norm_w, void *out,
+                                  nnz_qmv_dims d, float eps) {
+    NNZ_REQUIRE(ctx, wg != nullptr, NNZ_EINVAL, "norm_pair_silu: null weight");
+    if (wg->bits == 4)
+        return launch_qmv<4, NNZ_F32, 2, true, EPI_SILU, NNZ_F16, true>(
+            ctx, wg, wu, residual, norm_w, out, nullptr, d, "q4_norm_pair_silu", eps);
+    return launch_qmv<1, NNZ_F32, 2, true, EPI_SILU, NNZ_F16, false>(
+        ctx, wg, wu, residual, norm_w, out, nullptr, d, "norm_pair_silu", eps);
 }
 
 // RMSNorm prologue (x rounded to f16 like rms_norm_f16out, or BF16-truncated
@@ -1036,14 +1056,14 @@ int nnz_qmv_norm_qkv_launch(nnz_ctx *ctx, const nnz_qweight *wq, const nnz_qweig
 // reference's final norm + qmv_spec_f16in / q4mv_spec_f16in pair
 // (transformer.zig:2730-2785) in one launch.
 int nnz_qmv_norm_f32out_launch(nnz_ctx *ctx, const nnz_qweight *w, const float *residual,
-                               const float *norm_w, float *out, nnz_qmv_dims d) {
+                               const float *norm_w, float *out, nnz_qmv_dims d, float eps) {
     NNZ_REQUIRE(ctx, w != nullptr, NNZ_EINVAL, "norm_lm_head: null weight");
     if (w->bits == 4)
         return launch_qmv<4, NNZ_F32, 1, true, EPI_STORE, NNZ_F32, true>(
-            ctx, w, nullptr, residual, norm_w, out, nullptr, d, "q4_norm_lm_head");
+            ctx, w, nullptr, residual, norm_w, out, nullptr, d, "q4_norm_lm_head", eps);
     return launch_qmv<1, NNZ_F32, 1, true, EPI_STORE, NNZ_F32, false>(ctx, w, nullptr, residual,
                                                                        norm_w, out, nullptr, d,
-                                                                       "norm_lm_head");
+                                                                       "norm_lm_head", eps);
 }
 
 // O-projection with residual += whose input is merged from split-sequence
@@ -1159,13 +1179,13 @@ int nnz_dispatch_fused_norm_qkv_f16io(nnz_ctx *ctx, const nnz_qweight *wq, const
     NNZ_REQUIRE(ctx, kv_rows > 0, NNZ_EINVAL, "fused_norm_qkv: kv_rows == 0");
     NNZ_REQUIRE(ctx, wq && wq->bits == 1, NNZ_EINVAL, "fused_norm_qkv: 1-bit weights");
     return nnz_qmv_norm_qkv_launch(ctx, wq, wk, wv, residual, norm_scale, out_q, out_k, out_v,
-                                   q_dims.M, kv_rows, q_dims.K, q_dims.group_size);
+                                   q_dims.M, kv_rows, q_dims.K, q_dims.group_size, 1e-6f);
 }
 int nnz_dispatch_fused_norm_qmv_f16in(nnz_ctx *ctx, const nnz_qweight *w, const float *residual,
                                       float *output, const float *norm_scale, nnz_qmv_dims dims) {
     NNZ_CHECK_CTX(ctx);
     NNZ_REQUIRE(ctx, w && w->bits == 1, NNZ_EINVAL, "fused_norm_qmv_f16in: 1-bit weights");
-    return nnz_qmv_norm_f32out_launch(ctx, w, residual, norm_scale, output, dims);
+    return nnz_qmv_norm_f32out_launch(ctx, w, residual, norm_scale, output, dims, 1e-6f);
 }
 
 // ---------------------------- Q4 ------------------------------------------

@@ -1066,6 +1066,9 @@ int nnz_sample_launch(nnz_ctx *ctx, const float *logits, uint32_t n, const nnz_s
                 "sample: count %u outside 1..%u", n, MAX_BLOCKS * SB);
     NNZ_REQUIRE(ctx, p.temperature > 0.f && p.temperature <= 3.0e38f, NNZ_EINVAL,
                 "sample: temperature must be > 0 (0 selects argmax)");
+    // applyTopP asserts 0 < p <= 1 (transformer.zig:3781-3790); p >= 1 is
+    // "off" at the call site (:3878).  NaN and p <= 0 are refused.
+    NNZ_REQUIRE(ctx, p.top_p > 0.f, NNZ_EINVAL, "sample: top_p must be > 0 (>= 1 disables it)");
     // applyTemperature: inv_t = 1/T in f32, then logit * inv_t (transformer.zig:3713-3718)
     const float inv_t = 1.0f / p.temperature;
     const WsLayout L = ws_layout(n);

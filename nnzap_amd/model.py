@@ -14,6 +14,7 @@ import numpy as np
 from . import _lib as L
 from . import synth as S
 from .configs import PROJS, DecoderConfig, DecoderWeights
+from . import ops
 from .ops import Device
 
 _CODES = {"q": 10, "k": 12, "v": 14, "o": 16, "gate": 18, "up": 20, "down": 22}
@@ -37,6 +38,7 @@ class DecoderModel:
         h = C.c_void_p()
         dev.call("nnz_model_create", C.byref(c), C.byref(h))
         self.h = h
+        ops.track(self)
 
     def close(self):
         if self.h:

@@ -9,8 +9,10 @@ reference asserts instead.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
 import sys
+import weakref
 
 import numpy as np
 
@@ -33,6 +35,31 @@ _DT = {"float32": L.F32, "float16": L.F16, "bfloat16": L.BF16}
 
 def dtype_code(t) -> int:
     return _DT[str(t.dtype).replace("torch.", "")]
+
+
+# Objects that own library handles (contexts, models), in creation order.
+# Teardown contract: the caller closes them (close()); whatever is still
+# open when the interpreter exits is closed here, newest first (a model
+# before the context it runs on), from an atexit hook -- atexit runs before
+# interpreter finalization, while the HIP runtime is fully alive.  Nothing
+# is released from __del__ during finalization: the runtime's own C++
+# state may already be destroyed then.
+_LIVE: list = []
+
+
+def track(obj) -> None:
+    _LIVE.append(weakref.ref(obj))
+
+
+@atexit.register
+def _close_live() -> None:
+    while _LIVE:
+        o = _LIVE.pop()()
+        if o is not None:
+            try:
+                o.close()
+            except Exception:
+                pass
 
 
 class Device:
@@ -64,6 +91,7 @@ class Device:
         if rc != 0:
             raise NnzError("nnz_ctx_create", rc, "")
         self.ctx = ctx
+        track(self)
 
     def close(self) -> None:
         if self.ctx:
@@ -71,8 +99,9 @@ class Device:
             self.ctx = None
 
     def __del__(self):
-        # During interpreter shutdown the HIP runtime may already be torn
-        # down; releasing device objects then aborts the process.
+        # During interpreter finalization the HIP runtime's C++ state may
+        # already be destroyed; the atexit hook above has closed every live
+        # object before that point.
         if sys.is_finalizing():
             return
         try:

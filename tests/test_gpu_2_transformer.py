@@ -387,10 +387,13 @@ def test_dequant_gemm_shapes(dev, P, M, K, gs):
 
 
 @pytest.mark.parametrize("P,M,K,gs,sdt", [(37, 256, 2048, 64, 2), (512, 512, 2048, 64, 2),
-                                           (100, 128, 6144, 128, 1), (64, 64, 192, 64, 2)])
+                                           (100, 128, 6144, 128, 1), (64, 64, 192, 64, 2),
+                                           (512, 2560, 2048, 64, 2)])
 def test_dequant_gemm_q4_modes(dev, P, M, K, gs, sdt):
     """4-bit (q4_mlx) weights: s * (A . n) + b * sum(A) per group on the MFMA,
-    every mode BF16-faithful like the Q4 decode kernels (one bf16 ulp bar)."""
+    every mode BF16-faithful like the Q4 decode kernels (one bf16 ulp bar).
+    The last case has 320 blocks (more than one per CU), so the single-matrix
+    modes run the two-k-phase kernel real 4-bit prefill takes at hidden 2560."""
     from nnzap_amd import formats as fm
     sd = fm.DT_BF16 if sdt == 2 else fm.DT_F16
     wa = cf.q4_matrix(M, K, gs, 520, 521, 522, scale_dtype=sd)

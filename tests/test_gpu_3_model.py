@@ -12,9 +12,10 @@ import os
 import numpy as np
 import pytest
 
+from nnzap_amd import _lib as L
 from nnzap_amd import configs as cf
 from nnzap_amd.model import DecoderModel
-from nnzap_amd.ops import Device
+from nnzap_amd.ops import Device, NnzError
 from oracle.decoder import OracleDecoder
 
 from gpu_util import assert_close, assert_close_normwise
@@ -54,6 +55,34 @@ def test_tiny_prefill_and_decode_logits(mdev, tiny):
             r = ref.forward([t], pos)[0]
             g = m.forward_decode(t, pos)
             assert_close_normwise(g, r, what=f"decode pos {pos}")
+    finally:
+        m.close()
+
+
+def test_calls_during_decode_stream_are_refused(mdev, tiny):
+    """While a captured decode stream is active (decode_begin .. decode_end),
+    generate / prefill / forward_decode would rewrite the KV cache and the
+    state block under the captured plan: each is refused with ESTATE, and the
+    stream's tokens are unaffected."""
+    cfg, w = tiny
+    prompt = cf.prompt_ids(cfg, 24)
+    ref, _ = OracleDecoder(w).generate(prompt, 9)
+    m = DecoderModel(mdev, cfg)
+    try:
+        m.load(w)
+        m.decode_begin(prompt, 8)
+        m.decode_steps(4)
+        for call in (lambda: m.generate(prompt, 4), lambda: m.prefill(prompt[:8], 0),
+                     lambda: m.forward_decode(5, 30)):
+            with pytest.raises(NnzError) as e:
+                call()
+            assert e.value.code == L.ESTATE
+        m.decode_steps(4)
+        toks, _ = m.decode_read(9)
+        m.decode_end()
+        assert np.array_equal(toks, ref)
+        toks2, _, _ = m.generate(prompt, 9)          # allowed again after decode_end
+        assert np.array_equal(toks2, ref)
     finally:
         m.close()
 

@@ -17,10 +17,11 @@ import numpy as np
 import pytest
 import torch
 
+from nnzap_amd import _lib as L
 from nnzap_amd import configs as cf
 from nnzap_amd import ops
 from nnzap_amd.model import DecoderModel
-from nnzap_amd.ops import Device
+from nnzap_amd.ops import Device, NnzError
 from oracle import sampling as SM
 from oracle.decoder import OracleDecoder
 
@@ -202,3 +203,24 @@ def test_generate_stops_at_eos(sdev, tiny, use_graph):
         assert np.array_equal(toks, ref)
     finally:
         m.close()
+
+
+@pytest.mark.parametrize("top_p", [float("nan"), 0.0, -0.5])
+def test_bad_top_p_is_rejected(sdev, tiny, top_p):
+    """applyTopP asserts 0 < p <= 1 (transformer.zig:3781-3790): NaN and
+    p <= 0 are refused by both the model and the sampling dispatch (p >= 1
+    stays "off", :3878)."""
+    cfg, w = tiny
+    m = DecoderModel(sdev, cfg)
+    try:
+        with pytest.raises(NnzError) as e:
+            m.set_sampling(0.8, 0, top_p, 1)
+        assert e.value.code == L.EINVAL
+        m.set_sampling(0.8, 0, 1.5, 1)      # >= 1: top-p off, accepted
+    finally:
+        m.close()
+    x = _logits(1000, 3, "normal")
+    ws, rng, out, prob = _buffers(1000, 1)
+    with pytest.raises(NnzError) as e:
+        ops.dispatch_sample(sdev, torch.from_numpy(x).cuda(), out, rng, ws, 1.0, 0, top_p)
+    assert e.value.code == L.EINVAL

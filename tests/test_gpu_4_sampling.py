@@ -77,7 +77,7 @@ CASES = [
     (1000, 0.8, 50, 0.9, "normal", 200),
     (1000, 1.2, 0, 0.95, "normal", 200),
     (1000, 1.0, 1, 1.0, "normal", 50),
-    (1000, 1.0, 0, 0.0, "normal", 50),
+    (1000, 1.0, 0, 1e-6, "normal", 50),     # smallest nucleus: the first candidate
     (1000, 1.0, 20, 0.7, "ties", 200),
     (1000, 1.0, 0, 0.6, "ties", 200),
     (777, 0.9, 2000, 0.5, "peaked", 100),

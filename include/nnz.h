@@ -325,6 +325,22 @@ int nnz_dispatch_gqa_attention(nnz_ctx *ctx, const void *q, int q_dtype, const v
                                const void *v_cache, int kv_dtype, int v_transposed,
                                void *output, int out_dtype, void *scratch, size_t scratch_bytes,
                                int32_t rope_position, float rope_theta, nnz_gqa_dims dims);
+/* Allocation-free variant of nnz_dispatch_gqa_attention.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments and results as nnz_dispatch_gqa_attention minus
+ * the workspace: the split-sequence partials live in a fixed array of
+ * NNZ_GQA_NOALLOC_MAX_BYTES compiled into the library, one per GPU, held until
+ * the process ends.  Shapes needing more (nnz_gqa_scratch_bytes(dims) >
+ * NNZ_GQA_NOALLOC_MAX_BYTES: 16 query heads x D 128 up to seq_len 64,448)
+ * return NNZ_EUNSUPPORTED.  Calls no allocator.  Calls that overlap on one
+ * GPU share the array and race: serialise them (one stream per GPU). */
+#define NNZ_GQA_NOALLOC_MAX_BYTES ((size_t)8 << 20)
+int nnz_dispatch_gqa_attention_noalloc(nnz_ctx *ctx, const void *q, int q_dtype,
+                                       const void *k_cache, const void *v_cache, int kv_dtype,
+                                       int v_transposed, void *output, int out_dtype,
+                                       int32_t rope_position, float rope_theta,
+                                       nnz_gqa_dims dims);
 /* transformer.zig:962 dispatchGQAAttentionFusedTG: Q/K per-head RMSNorm +
  * RoPE, K/V append at `position`, attention over seq_len = position+1 tokens.
  * f16 q/k_raw/v_raw/output, f16 caches (V transposed), f32 norm scales.

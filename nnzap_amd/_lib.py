@@ -16,6 +16,7 @@ HEADER = HERE.parent / "include" / "nnz.h"
 OK, EINVAL, EUNSUPPORTED, EHIP, ENOMEM, ETIMEOUT, ESTATE = 0, -1, -2, -3, -4, -5, -6
 F32, F16, BF16 = 0, 1, 2
 GEMM_STORE_F16, GEMM_STORE_F32, GEMM_RESADD, GEMM_SILU_PAIR = 0, 1, 2, 3
+GQA_NOALLOC_MAX_BYTES = 8 << 20   # NNZ_GQA_NOALLOC_MAX_BYTES
 EMBED_Q1, EMBED_BF16, EMBED_Q4 = 0, 1, 2
 LMHEAD_Q1, LMHEAD_TIED_BF16, LMHEAD_Q4 = 0, 1, 2
 QUANT_FORMAT_Q1, QUANT_FORMAT_Q4 = 0, 1
@@ -153,6 +154,8 @@ PROTOS = {
     "nnz_gqa_scratch_bytes": (sz, [GQADims]),
     "nnz_dispatch_gqa_attention": (C.c_int, [vp, vp, C.c_int, vp, vp, C.c_int, C.c_int, vp,
                                              C.c_int, vp, sz, i32, f32, GQADims]),
+    "nnz_dispatch_gqa_attention_noalloc": (C.c_int, [vp, vp, C.c_int, vp, vp, C.c_int, C.c_int,
+                                                     vp, C.c_int, i32, f32, GQADims]),
     "nnz_dispatch_gqa_attention_fused": (C.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz,
                                                    GQAFusedDims]),
     "nnz_dispatch_gqa_attention_fused_1pass": (C.c_int, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,

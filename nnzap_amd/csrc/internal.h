@@ -28,6 +28,15 @@ uint32_t nnz_attn_chunk(uint32_t seq_len, uint32_t hkv);
 uint32_t nnz_attn_fused_chunk(uint32_t max_seq, uint32_t hkv);
 int nnz_rope_table_launch(nnz_ctx *ctx, float *out, uint32_t head_dim, float theta);
 int nnz_attn_launch_ex(nnz_ctx *ctx, const NnzAttnCall &c);
+// Single-query attention with the partials carved out of `scratch`
+// (nnz_dispatch_gqa_attention's body).
+int nnz_attn_launch(nnz_ctx *ctx, const void *q, int qdt, const void *kc, const void *vc, int kvdt,
+                    bool vt, void *out, int odt, void *scratch, size_t scratch_bytes,
+                    int32_t rope_pos, float theta, const nnz_gqa_dims &d);
+// Fixed partials buffer of nnz_dispatch_gqa_attention_noalloc (noalloc.hip):
+// looks up its device address for ctx->device (called by nnz_ctx_create).
+constexpr size_t NNZ_NOALLOC_SCRATCH_BYTES = NNZ_GQA_NOALLOC_MAX_BYTES;
+int nnz_noalloc_init(nnz_ctx *ctx);
 int nnz_attn_prep_launch(nnz_ctx *ctx, const void *q, const void *kr, const void *vr,
                          const float *qn, const float *kn, float *qout, void *kc, void *vc,
                          uint32_t hq, uint32_t hkv, uint32_t head_dim, uint32_t pos,

@@ -4,7 +4,7 @@
 // Device.init (:959-1020) -> nnz_ctx_create, shared MTLBuffers (:80-469) ->
 // explicit hipMalloc'd buffers uploaded once, commitAndWait / the unbounded
 // commitAndSpinOnFlag (:1293-1352) -> nnz_stream_sync with a timeout.
-#include "common.h"
+#include "internal.h"
 
 #include <chrono>
 #include <thread>
@@ -42,6 +42,11 @@ int nnz_ctx_create(int device, void *hip_stream, nnz_ctx **out) {
             return NNZ_EHIP;
         }
         c->own_stream = true;
+    }
+    if (int rc = nnz_noalloc_init(c)) {
+        if (c->own_stream) hipStreamDestroy(c->stream);
+        delete c;
+        return rc;
     }
     *out = c;
     return NNZ_OK;

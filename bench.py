@@ -17,9 +17,15 @@ Also reported (same JSON line):
                 per-dispatch device durations from rocprofv3 are in profiles/;
   qmv           configs 1-4 (4-bit QMV, 1-bit QMV, fused gate/up+SiLU, GQA
                 decode attention at L = 512/4096/32768) in the same way;
-  cpu_baseline  the numpy oracle's decode step on this host, bounded sample;
-  cpu_configs   configs 1-4 through the numpy oracle on this host (median of
-                7 after 2 warm-ups; --cpu-full: median of 30 after 5).
+  decode        also prefill tok/s and p50/p99 per-token latency of a host
+                loop that waits for each token (the reference bench's outputs);
+  decode_tied_lm_head  the same decoder with the tied bf16 embedding table
+                as LM head (622 MB per token), and that GEMV's HBM fraction;
+  cpu_baseline  the full 28-layer decode step in PyTorch float32 on this
+                host's cores (pre-dequantised weights: 5 warm-ups, median of
+                30; dequantising every step: a shorter sample);
+  cpu_configs   configs 1-4 in PyTorch float32 on this host (median of 7
+                after 2 warm-ups; --cpu-full: median of 30 after 5).
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--lm-head q1|tied] [--quick]
                 [--cpu-full]
@@ -62,17 +68,29 @@ def log(*a):
 
 
 # ---------------------------------------------------------------- decode ----
-def bench_decode(args, dev):
+def bench_decode(args, dev, lm_head=None, latency=True):
+    """Headline decode tok/s (see the module docstring), plus the
+    reference bench's other outputs (bonsai_bench.zig:255-320): prefill tok/s
+    (512 prompt tokens / prefill wall time, median of 3 after a warm-up) and
+    the p50 / p99 per-token latency of a host loop that waits for every token
+    before asking for the next (8 warm-up + 64 measured tokens; p50 =
+    sorted[n/2], p99 = sorted[n*99/100])."""
     from nnzap_amd import configs as cf
     from nnzap_amd.model import DecoderModel
 
+    lm_head = lm_head or args.lm_head
     cfg = cf.DecoderConfig(**{**cf.BONSAI_1_7B.__dict__,
-                              "lm_head_kind": 1 if args.lm_head == "tied" else 0})
+                              "lm_head_kind": 1 if lm_head == "tied" else 0})
     t = time.time()
-    w = cf.decoder_weights(cfg, norm_mode="small", host_embed=False)
+    # the tied model's table is generated on the device: build the host
+    # weights without it
+    w = cf.decoder_weights(cf.DecoderConfig(**{**cfg.__dict__, "lm_head_kind": 0}),
+                           norm_mode="small", host_embed=False)
+    if lm_head == "tied":
+        w.lm_head = None
     m = DecoderModel(dev, cfg)
     m.load(w, embed_on_device=True)
-    log(f"model ready in {time.time() - t:.1f}s")
+    log(f"model ({lm_head} LM head) ready in {time.time() - t:.1f}s")
     prompt = cf.prompt_ids(cfg, args.prompt)
     # warm-up pass (separate prefill)
     m.decode_begin(prompt, max(args.warmup, 1))
@@ -98,8 +116,33 @@ def bench_decode(args, dev):
         "min_margin": float(np.min(margins)),
         "tokens_head": toks[:8].tolist(),
     }
+    if latency:
+        pf = []
+        for i in range(4):
+            dev.sync()
+            a = time.perf_counter()
+            m.prefill(prompt, 0)
+            pf.append(time.perf_counter() - a)
+        t_pf = float(np.median(pf[1:]))
+        out["prefill_ms"] = round(1000.0 * t_pf, 3)
+        out["prefill_tok_s"] = round(len(prompt) / t_pf, 1)
+        n_warm, n_lat = 8, 64
+        m.decode_begin(prompt, n_warm + n_lat)
+        lat = []
+        for i in range(n_warm + n_lat):
+            a = time.perf_counter()
+            m.decode_steps(1)
+            m.decode_read(i + 2)          # waits for this token, copies it to the host
+            if i >= n_warm:
+                lat.append(time.perf_counter() - a)
+        m.decode_end()
+        srt = sorted(lat)
+        out["latency_us"] = {"p50": round(1e6 * srt[len(srt) // 2], 1),
+                             "p99": round(1e6 * srt[len(srt) * 99 // 100], 1),
+                             "tokens": n_lat, "warmup": n_warm,
+                             "mode": "one graph replay + bounded sync + token read per token"}
     gold = os.path.join(ROOT, "tests", "golden", "config5_tokens.json")
-    if os.path.exists(gold) and args.lm_head == "q1" and args.prompt == 512:
+    if os.path.exists(gold) and lm_head == "q1" and args.prompt == 512:
         g = json.load(open(gold))
         n = min(len(g["tokens"]), args.steps)
         out["tokens_match_golden"] = bool(np.array_equal(toks[:n], np.array(g["tokens"][:n])))
@@ -373,6 +416,20 @@ def _kernel_cases():
                            max(16, n // 8))
         return us, wl.nbytes + H * 2 + V * 4, None
 
+    def dec_lm_head_tied(dev, n):
+        # the tied bf16 LM head (622 MB per token): two tables alternate, each
+        # larger than the 256 MB Infinity Cache, so every launch streams HBM
+        g = torch.Generator(device="cuda")
+        g.manual_seed(516)
+        tabs = [(torch.randn(V, H, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+                for _ in range(2)]
+        x16 = torch.randn(H, dtype=f16, device="cuda") * 0.05
+        logits = torch.empty(V, dtype=f32, device="cuda")
+        us = time_launches(dev, lambda i: ops.dispatch_lm_head_bf16(dev, tabs[i % 2], x16, logits),
+                           max(8, n // 16))
+        del tabs
+        return us, V * H * 2 + H * 2 + V * 4, None
+
     def floor_small(dev, n):
         # launch floor: one tiny kernel (residual += addition over 2048 f32)
         a = torch.zeros(H, dtype=f32, device="cuda")
@@ -460,7 +517,8 @@ def _kernel_cases():
         "dec_o_merge_resadd": dec_o_merge, "dec_gate_up_norm_silu": dec_gate_up,
         "attention_fused_seq640": dec_attention, "o_resadd": dec_o,
         "dec_down_resadd": dec_down, "dec_lm_head_norm": dec_lm_head,
-        "dec_lm_head_f16in": dec_lm_head_f16in, "floor_residual_add": floor_small,
+        "dec_lm_head_f16in": dec_lm_head_f16in, "dec_lm_head_tied": dec_lm_head_tied,
+        "floor_residual_add": floor_small,
         "config4_attention_L512": config4(512), "config4_attention_L4096": config4(4096),
         "config4_attention_L32768": config4(32768), "copy_256MiB": copy_calib,
         "prefill_gemm_q": prefill_gemm(QD, H, L.GEMM_STORE_F16),
@@ -503,6 +561,24 @@ def bench_kernels(dev, quick=False, only=None):
     return res
 
 
+def load_trace_us():
+    """Mean per-dispatch device duration (us) of every kernel case from the
+    committed rocprofv3 kernel-trace summary (profiles/kernel_case_traces.md,
+    first table: the case's kernels summed)."""
+    path = os.path.join(ROOT, "profiles", "kernel_case_traces.md")
+    out = {}
+    if not os.path.exists(path):
+        return out
+    for line in open(path):
+        f = [x.strip() for x in line.strip().strip("|").split("|")]
+        if len(f) >= 10 and f[0] and f[0] not in out:
+            try:
+                out[f[0]] = float(f[3])
+            except ValueError:
+                pass
+    return out
+
+
 def load_traffic():
     """HBM bytes per launch of the decode kernel cases, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/pmc_traffic.md):
@@ -520,35 +596,10 @@ def load_traffic():
 
 
 # ------------------------------------------------------------ CPU baseline --
-def cpu_baseline(sample_layers=2, tokens=3):
-    """The numpy oracle's decode step on this host: `sample_layers` of the 28
-    layers (full shapes) + the full 1-bit LM head, `tokens` single-token
-    forwards after a 64-token prefill; tok/s extrapolated to 28 layers."""
-    from nnzap_amd import configs as cf
-    from oracle.decoder import OracleDecoder
-
-    cfg = cf.DecoderConfig(**{**cf.BONSAI_1_7B.__dict__, "num_layers": sample_layers,
-                              "max_context_length": 1024})
-    w = cf.decoder_weights(cfg, norm_mode="small", host_embed=False)
-    od = OracleDecoder(w)
-    prompt = cf.prompt_ids(cfg, 64)
-    od.forward(list(prompt), 0)
-    xf = np.zeros((1, cfg.hidden_size))
-    t0 = time.perf_counter()
-    for _ in range(tokens):
-        od.lm_head(xf)
-    t_lm = (time.perf_counter() - t0) / tokens
-    t0 = time.perf_counter()
-    for i in range(tokens):
-        od.forward([int(prompt[i])], 64 + i)
-    t_tok = (time.perf_counter() - t0) / tokens
-    t_layer = max(t_tok - t_lm, 1e-9) / sample_layers
-    per_token = t_lm + 28 * t_layer
-    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
-    return {"value": round(1.0 / per_token, 4), "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": (f"numpy float64 oracle (OracleDecoder), {tokens} single-token decode steps "
-                       f"through {sample_layers} full-size layers + 1-bit LM head at position 64+; "
-                       f"per-token time = LM head + 28 x measured per-layer time")}
+def cpu_threads() -> int:
+    """Threads the CPU legs use: OMP_NUM_THREADS (the GPU box sets it to its
+    CPU share, 16 per GPU) or every core os.cpu_count() reports."""
+    return int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
 
 
 def _median_time(fn, warmup=5, runs=30):
@@ -572,52 +623,111 @@ def cpu_model():
     return "unknown"
 
 
-def cpu_configs(full=False):
-    """Configs 1-4 through the numpy oracle on this host: 2 warm-up calls,
-    then the median of 7 (with full=True: 5 and the median of 30).  Two
-    variants per config: dequantise (or widen the bf16 caches) on every
-    call, and the same product on pre-dequantised float64 operands."""
+def cpu_baseline(pos=512, warmup=5, runs=30, dq_warmup=1, dq_runs=3):
+    """The config-5 decoder's decode step in PyTorch float32 on this host's
+    cores (oracle/torch_cpu.py): all 28 layers + the 1-bit LM head, KV cache
+    holding `pos` tokens.  Pre-dequantised float32 weights: `warmup` steps
+    then the median of `runs` (the headline value).  Dequantised from the
+    packed codes on every step: `dq_warmup` then the median of `dq_runs`
+    (several seconds per step, so a shorter sample)."""
+    import torch
     from nnzap_amd import configs as cf
-    from nnzap_amd import synth as S
-    from oracle import oracle as O
+    from oracle.torch_cpu import TorchDecoder
 
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    cfg = cf.BONSAI_1_7B
+    w = cf.decoder_weights(cfg, norm_mode="small", host_embed=False)
+    t0 = time.perf_counter()
+    td = TorchDecoder(w, pos + 8, predequantise=True)
+    t_deq = time.perf_counter() - t0
+    td.fill_cache(pos)
+    x = torch.randn(cfg.hidden_size, generator=torch.Generator().manual_seed(1)) * 0.02
+    t_pre = _median_time(lambda: td.step(x, pos), warmup, runs)
+    del td
+    tq = TorchDecoder(w, pos + 8, predequantise=False)
+    tq.fill_cache(pos)
+    t_dq = _median_time(lambda: tq.step(x, pos), dq_warmup, dq_runs)
+    del tq
+    log(f"cpu decode (torch f32, {threads} threads): {1 / t_pre:.2f} tok/s pre-dequantised, "
+        f"{1 / t_dq:.3f} tok/s dequantising every step (one-time dequant {t_deq:.1f}s)")
+    return {"value": round(1.0 / t_pre, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+            "impl": "PyTorch CPU float32 (oracle/torch_cpu.py)", "cpu_model": cpu_model(),
+            "cpu_count": os.cpu_count(),
+            "ms_per_token_predequantised": round(1000 * t_pre, 2),
+            "ms_per_token_dequant_each_call": round(1000 * t_dq, 1),
+            "tok_s_dequant_each_call": round(1.0 / t_dq, 4),
+            "sample": (f"one decode step of the full config-5 decoder (28 layers + 1-bit LM head, "
+                       f"KV cache of {pos} tokens) in torch float32 on {threads} threads; "
+                       f"value: weights pre-dequantised, {warmup} warm-up steps then the median "
+                       f"of {runs}; dequantising every step: {dq_warmup} warm-up then the median "
+                       f"of {dq_runs}")}
+
+
+def cpu_configs(full=False):
+    """Configs 1-4 in PyTorch float32 on this host (oracle/torch_cpu.py), 5
+    warm-up calls then the median of 30 (without --cpu-full: 2 and 7).  Two
+    variants per config: dequantise (or widen the bf16 caches) on every
+    call, and the same product on pre-dequantised float32 operands."""
+    import torch
+    from nnzap_amd import configs as cf
+    from nnzap_amd import formats as fm
+    from oracle import torch_cpu as T
+
+    torch.set_num_threads(cpu_threads())
     wu, nr = (5, 30) if full else (2, 7)
     out = {}
     w1, x1 = cf.config1()
-    d1 = O.dequant(w1)
-    out["config1_q4mv"] = (lambda: O.qmv(w1, x1), lambda: O.qmv(w1, x1, d1), w1.nbytes + 8192 + 24576)
+    x1t = torch.from_numpy(x1)
+    deq1 = lambda: T.dequant_q4(w1.codes, w1.scales, w1.biases, w1.M, w1.K, w1.group_size,  # noqa: E731
+                                w1.scale_dtype == fm.DT_BF16)
+    d1 = deq1()
+    out["config1_q4mv"] = (lambda: deq1() @ x1t, lambda: d1 @ x1t, w1.nbytes + 8192 + 24576)
     w2, x2 = cf.config2()
-    d2 = O.dequant(w2)
-    out["config2_qmv"] = (lambda: O.qmv(w2, x2), lambda: O.qmv(w2, x2, d2), w2.nbytes + 24576 + 8192)
+    x2t = torch.from_numpy(x2)
+    deq2 = lambda: T.dequant_q1(w2.codes, w2.scales, w2.M, w2.K, w2.group_size)  # noqa: E731
+    d2 = deq2()
+    out["config2_qmv"] = (lambda: deq2() @ x2t, lambda: d2 @ x2t, w2.nbytes + 24576 + 8192)
     wg, wup, x3 = cf.config3()
-    dg, du = O.dequant(wg), O.dequant(wup)
-    x3d = np.asarray(x3, np.float64)
-    out["config3_gate_up_silu"] = (lambda: O.qmv_pair_silu(wg, wup, x3),
-                                   lambda: O.silu(dg @ x3d) * (du @ x3d),
+    x3t = torch.from_numpy(x3)
+    dq = lambda q: T.dequant_q1(q.codes, q.scales, q.M, q.K, q.group_size)  # noqa: E731
+    dg, du = dq(wg), dq(wup)
+    silu = torch.nn.functional.silu
+    out["config3_gate_up_silu"] = (lambda: silu(dq(wg) @ x3t) * (dq(wup) @ x3t),
+                                   lambda: silu(dg @ x3t) * (du @ x3t),
                                    wg.nbytes + wup.nbytes + 8192 + 24576)
+    p = torch.arange(64, dtype=torch.float64)
+    inv = torch.exp2(-(2.0 * p / 128) * np.log2(1e6)).float()
+
+    def attn(q, k, v, L_):
+        qr = T.rope(q, L_, inv).view(8, 2, 128)
+        s = torch.matmul(qr, k.transpose(1, 2)) / np.sqrt(128)
+        return torch.matmul(torch.softmax(s, dim=-1), v).reshape(16, 128)
+
+    def bf16(bits, shape):
+        return (torch.from_numpy(bits.view(np.int16)).to(torch.int32) << 16).view(torch.float32) \
+            .reshape(shape)
     for L_ in (512, 4096, 32768):
         q, k, v = cf.config4(L_)
-
-        def widen(q=q, k=k, v=v, L_=L_):
-            qf = O.rope(S.bf16_bits_to_f32(q).astype(np.float64), L_, 1e6)
-            return O.attention_decode(qf, S.bf16_bits_to_f32(k), S.bf16_bits_to_f32(v), L_, False)
-
-        qf = O.rope(S.bf16_bits_to_f32(q).astype(np.float64), L_, 1e6)
-        kf, vf = S.bf16_bits_to_f32(k).astype(np.float64), S.bf16_bits_to_f32(v).astype(np.float64)
-        out[f"config4_attention_L{L_}"] = (widen, lambda qf=qf, kf=kf, vf=vf, L_=L_:
-                                           O.attention_decode(qf, kf, vf, L_, False),
-                                           4096 * L_ + 12288)
+        qf, kf, vf = bf16(q, (16, 128)), bf16(k, (8, L_, 128)), bf16(v, (8, L_, 128))
+        out[f"config4_attention_L{L_}"] = (
+            lambda q=q, k=k, v=v, L_=L_: attn(bf16(q, (16, 128)), bf16(k, (8, L_, 128)),
+                                              bf16(v, (8, L_, 128)), L_),
+            lambda qf=qf, kf=kf, vf=vf, L_=L_: attn(qf, kf, vf, L_),
+            4096 * L_ + 12288)
     res = {}
-    for name, (f_dq, f_pre, nbytes) in out.items():
-        t_dq = _median_time(f_dq, wu, nr)
-        t_pre = _median_time(f_pre, wu, nr)
-        res[name] = {"us_dequant_each_call": round(t_dq * 1e6, 1),
-                     "us_predequantised": round(t_pre * 1e6, 1),
-                     "GBs_dequant_each_call": round(nbytes / t_dq / 1e9, 3)}
-        log(f"cpu {name:26s} {t_dq * 1e6:12.1f} us (dequant each call) {t_pre * 1e6:12.1f} us (pre-dequantised)")
-    return {"kind": "port", "impl": "numpy float64 oracle", "warmup": wu, "runs": nr,
-            "stat": "median", "threads": int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)),
-            "cpu_model": cpu_model(), "cpu_count": os.cpu_count(), "configs": res}
+    with torch.no_grad():
+        for name, (f_dq, f_pre, nbytes) in out.items():
+            t_dq = _median_time(f_dq, wu, nr)
+            t_pre = _median_time(f_pre, wu, nr)
+            res[name] = {"us_dequant_each_call": round(t_dq * 1e6, 1),
+                         "us_predequantised": round(t_pre * 1e6, 1),
+                         "GBs_dequant_each_call": round(nbytes / t_dq / 1e9, 3)}
+            log(f"cpu {name:26s} {t_dq * 1e6:12.1f} us (dequant each call) "
+                f"{t_pre * 1e6:12.1f} us (pre-dequantised)")
+    return {"kind": "port", "impl": "PyTorch CPU float32 (oracle/torch_cpu.py)", "warmup": wu,
+            "runs": nr, "stat": "median", "threads": cpu_threads(), "cpu_model": cpu_model(),
+            "cpu_count": os.cpu_count(), "configs": res}
 
 
 def main():
@@ -633,6 +743,8 @@ def main():
                     help="per-config CPU timings with 5 warm-ups and the median of 30")
     ap.add_argument("--skip-kernels", action="store_true")
     ap.add_argument("--skip-q4", action="store_true", help="leave out the 4-bit decode figure")
+    ap.add_argument("--skip-tied", action="store_true",
+                    help="leave out the tied bf16 LM head decode figure")
     ap.add_argument("--skip-decode", action="store_true",
                     help="kernel timings only (profiling runs); no JSON line")
     ap.add_argument("--only", default=None,
@@ -655,6 +767,10 @@ def main():
         bench_kernels(dev, quick=args.quick, only=args.only)
         return
     dec = bench_decode(args, dev)
+    dec_tied = None if args.skip_tied or args.lm_head == "tied" else \
+        bench_decode(args, dev, lm_head="tied", latency=False)
+    if dec_tied:
+        log(f"tied bf16 LM head decode: {dec_tied['tok_s']:.1f} tok/s")
     dec_q4 = None if args.skip_q4 else bench_decode_q4(args, dev)
     if dec_q4:
         log(f"q4 decode: {dec_q4['tok_s']} tok/s")
@@ -670,7 +786,15 @@ def main():
         roofline = {"kernel": dom, "bound": "hbm", "achieved": d["GBs"], "peak": PEAK_HBM_GBS,
                     "unit": "GB/s", "frac": round(d["GBs"] / PEAK_HBM_GBS, 4), "traffic": traffic,
                     "avg_launch_us": d["us"], "algorithmic_bytes": d["bytes"],
+                    "timing": "live: launches back to back in one hipGraph, HIP events on the "
+                              "library stream / launches",
                     "traffic_source": "profiles/pmc_traffic.md" if traffic else None}
+        tr = load_trace_us().get(dom)
+        if tr:   # the committed rocprofv3 per-dispatch mean of the same case
+            roofline.update({"trace_us": tr,
+                             "achieved_trace": round(d["bytes"] / (tr * 1e-6) / 1e9, 1),
+                             "frac_trace": round(d["bytes"] / (tr * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                             "trace_source": "profiles/kernel_case_traces.md"})
     cpu = None if args.skip_cpu else cpu_baseline()
     cpu_cfg = None if args.skip_cpu else cpu_configs(full=args.cpu_full)
 
@@ -697,6 +821,10 @@ def main():
         "cpu_configs": cpu_cfg,
         "decode": dec,
         "decode_q4": dec_q4,
+        "decode_tied_lm_head": dec_tied and {
+            "tok_s": round(dec_tied["tok_s"], 2), "ms_per_step": round(dec_tied["ms_per_step"], 4),
+            "lm_head_kernel": kern.get("dec_lm_head_tied"),
+            "workload": "config 5 with the tied bf16 embedding table as LM head (622 MB/token)"},
         "qmv": {k: v for k, v in kern.items() if k.startswith("config")},
         "prefill_gemm": {k: v for k, v in kern.items() if k.startswith("prefill_gemm")},
         "decode_kernels": dec_k,

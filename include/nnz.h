@@ -436,6 +436,15 @@ int nnz_dispatch_sample(nnz_ctx *ctx, const float *logits, uint32_t count,
                         const nnz_sampling_params *params, uint64_t *d_rng, void *workspace,
                         size_t workspace_bytes, uint32_t *out_index, float *out_prob);
 
+/* Tied bf16 LM head: the LM-head half of encodeFinalNormAndLMHead
+ * (transformer.zig:2730-2785) when the head is the bf16 embedding table
+ * (tie_word_embeddings, :297; BASELINE config 5 read literally):
+ * logits[v] = sum_k table[v][k] * x[k]; table bf16 [vocab][hidden]
+ * row-major, x f16 [hidden] (the final norm's output), logits f32 [vocab],
+ * f32 accumulation.  table and x 16-byte aligned. */
+int nnz_dispatch_lm_head_bf16(nnz_ctx *ctx, const void *table, const void *x, float *logits,
+                              uint32_t vocab, uint32_t hidden);
+
 /* ---- decoder model: forwardDecode / generate (transformer.zig:2389-4135) -- */
 
 typedef struct {

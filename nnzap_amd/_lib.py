@@ -172,6 +172,7 @@ PROTOS = {
     "nnz_sample_workspace_bytes": (sz, [u32]),
     "nnz_rng_seed": (C.c_int, [vp, C.c_uint64, vp]),
     "nnz_dispatch_sample": (C.c_int, [vp, vp, u32, vp, vp, vp, sz, vp, vp]),
+    "nnz_dispatch_lm_head_bf16": (C.c_int, [vp, vp, vp, vp, u32, u32]),
     # model
     "nnz_model_create": (C.c_int, [vp, P(ModelConfig), P(vp)]),
     "nnz_model_destroy": (C.c_int, [vp]),

@@ -22,6 +22,7 @@
 //     the decode step: f16 activations and KV cache, f32 residual stream.
 #include "internal.h"
 
+#include <algorithm>
 #include <vector>
 
 // Public launchers implemented in qmv.hip / transformer.hip.
@@ -134,6 +135,90 @@ __global__ __launch_bounds__(256) void dense_bf16_gemv_kernel(const uint16_t *E,
         }
         acc = group_sum(acc, LPR);
         if (ok && ll == 0) y[row] = acc;
+    }
+}
+
+// Tied bf16 LM head for hidden = 2048 * NV: a lane owns NV 32-column units
+// of every row (64 bytes each: four 16-byte loads), its x slice stays in
+// registers, and a wave takes R rows per step.  Two register sets alternate:
+// the next step's rows are loading while the current step computes, so each
+// wave keeps R * NV * 256 bytes of the table in flight.  The table is read
+// once per token and streams past the caches (non-temporal loads), leaving
+// the Infinity Cache to the layer weights and the KV cache.
+template <int NV, int R>
+__global__ __launch_bounds__(256) void lm_head_bf16_kernel(const uint16_t *__restrict__ E,
+                                                           const f16_t *__restrict__ x,
+                                                           float *__restrict__ y, uint32_t M) {
+    constexpr uint32_t K = 2048 * NV;
+    const int lane = threadIdx.x & 63;
+    float xr[NV][32];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const uint4 *xp = (const uint4 *)(x + (size_t)(lane + 64 * j) * 32);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint4 q = xp[v];
+            const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                xr[j][8 * v + 2 * e] = (float)__builtin_bit_cast(f16_t, (uint16_t)(w4[e] & 0xFFFFu));
+                xr[j][8 * v + 2 * e + 1] = (float)__builtin_bit_cast(f16_t, (uint16_t)(w4[e] >> 16));
+            }
+        }
+    }
+    const uint32_t wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint32_t stride = gridDim.x * 4 * R;
+    typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+    typedef v4u Rows[R][NV][4];
+    auto load = [&](uint32_t b, Rows &dst) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t row = b + r < M ? b + r : M - 1;
+            const v4u *p = (const v4u *)(E + (size_t)row * K);
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    dst[r][j][v] = __builtin_nontemporal_load(p + (lane + 64 * j) * 4 + v);
+        }
+    };
+    auto consume = [&](const Rows &src, uint32_t b) {
+        float rt[R];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float acc = 0.f;
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const uint32_t w4[4] = {src[r][j][v].x, src[r][j][v].y, src[r][j][v].z,
+                                            src[r][j][v].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        acc = fmaf(__uint_as_float(w4[e] << 16), xr[j][8 * v + 2 * e], acc);
+                        acc = fmaf(__uint_as_float(w4[e] & 0xFFFF0000u), xr[j][8 * v + 2 * e + 1], acc);
+                    }
+                }
+            rt[r] = lane63(wave_sum_to_last(acc));
+        }
+        float t = rt[0];
+#pragma unroll
+        for (int k = 1; k < R; ++k) t = lane == k ? rt[k] : t;
+        if (lane < R && b + (uint32_t)lane < M) y[b + lane] = t;
+    };
+    uint32_t base = wave * R;
+    Rows ra, rb;
+    load(base < M ? base : 0u, ra);
+    while (base < M) {
+        uint32_t nb = base + stride;
+        load(nb < M ? nb : base, rb);
+        consume(ra, base);
+        base = nb;
+        if (base >= M) break;
+        nb = base + stride;
+        load(nb < M ? nb : base, ra);
+        consume(rb, base);
+        base = nb;
     }
 }
 
@@ -289,30 +374,47 @@ nnz_gqa_dims gqa_dims(const nnz_model *m, uint32_t seq) {
             m->G};
 }
 
-int lm_head(nnz_model *m, const f16_t *x, float *logits) {
-    if (m->c.lm_head_kind == NNZ_LMHEAD_Q4)
-        return nnz_dispatch_q4mv_f16in(m->ctx, &m->lm.w, x, logits, dims_of(m, m->lm));
-    if (m->c.lm_head_kind == NNZ_LMHEAD_Q1)
-        return nnz_dispatch_qmv_f16in(m->ctx, &m->lm.w, x, logits, dims_of(m, m->lm));
-    const uint32_t K = m->c.hidden_size, units = K / 32;
+// Rows per wave step and blocks of the tied bf16 LM head (measured).
+constexpr int LMH_R = 2;
+constexpr uint32_t LMH_BLOCKS = 1024;
+
+// Dense bf16 LM head: the pipelined kernel for hidden 2048 / 4096, the
+// lane-group kernel otherwise.
+int lm_head_bf16_launch(nnz_ctx *ctx, const uint16_t *E, const f16_t *x, float *logits, uint32_t V,
+                        uint32_t K) {
+    if (K == 2048 || K == 4096) {
+        const uint32_t blocks = std::min<uint32_t>(LMH_BLOCKS, ceil_div(V, 4u * LMH_R));
+        if (K == 2048) lm_head_bf16_kernel<1, LMH_R><<<blocks, 256, 0, ctx->stream>>>(E, x, logits, V);
+        else lm_head_bf16_kernel<2, LMH_R><<<blocks, 256, 0, ctx->stream>>>(E, x, logits, V);
+        NNZ_LAUNCHED(ctx);
+        return NNZ_OK;
+    }
+    const uint32_t units = K / 32;
     uint32_t lpr = 1;
     while (lpr < units && lpr < 64) lpr <<= 1;
     int lg = 0;
     while ((1u << lg) < lpr) ++lg;
     const uint32_t nv = ceil_div(units, lpr);
     const uint32_t rows_per_block = 4 * (64 / lpr);
-    uint32_t blocks = ceil_div(m->c.vocab_size, rows_per_block);
+    uint32_t blocks = ceil_div(V, rows_per_block);
     if (blocks > 4096) blocks = 4096;
     if (nv == 1)
-        dense_bf16_gemv_kernel<1><<<blocks, 256, 0, m->ctx->stream>>>(
-            (const uint16_t *)m->emb, x, logits, m->c.vocab_size, K, lg);
+        dense_bf16_gemv_kernel<1><<<blocks, 256, 0, ctx->stream>>>(E, x, logits, V, K, lg);
     else if (nv == 2)
-        dense_bf16_gemv_kernel<2><<<blocks, 256, 0, m->ctx->stream>>>(
-            (const uint16_t *)m->emb, x, logits, m->c.vocab_size, K, lg);
+        dense_bf16_gemv_kernel<2><<<blocks, 256, 0, ctx->stream>>>(E, x, logits, V, K, lg);
     else
-        return nnz_fail(m->ctx, NNZ_EUNSUPPORTED, "tied bf16 LM head: hidden %u > 4096", K);
-    NNZ_LAUNCHED(m->ctx);
+        return nnz_fail(ctx, NNZ_EUNSUPPORTED, "bf16 LM head: hidden %u > 4096", K);
+    NNZ_LAUNCHED(ctx);
     return NNZ_OK;
+}
+
+int lm_head(nnz_model *m, const f16_t *x, float *logits) {
+    if (m->c.lm_head_kind == NNZ_LMHEAD_Q4)
+        return nnz_dispatch_q4mv_f16in(m->ctx, &m->lm.w, x, logits, dims_of(m, m->lm));
+    if (m->c.lm_head_kind == NNZ_LMHEAD_Q1)
+        return nnz_dispatch_qmv_f16in(m->ctx, &m->lm.w, x, logits, dims_of(m, m->lm));
+    return lm_head_bf16_launch(m->ctx, (const uint16_t *)m->emb, x, logits, m->c.vocab_size,
+                               m->c.hidden_size);
 }
 
 #define RC(x)                  \
@@ -447,6 +549,17 @@ int ensure_prefill_buffers(nnz_model *m, uint32_t n, uint32_t start) {
 }  // namespace
 
 extern "C" {
+
+int nnz_dispatch_lm_head_bf16(nnz_ctx *ctx, const void *table, const void *x, float *logits,
+                              uint32_t vocab, uint32_t hidden) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, table && x && logits, NNZ_EINVAL, "lm_head_bf16: null buffer");
+    NNZ_REQUIRE(ctx, vocab > 0 && hidden > 0 && hidden % 32 == 0, NNZ_EINVAL,
+                "lm_head_bf16: vocab > 0 and hidden a multiple of 32 required");
+    NNZ_REQUIRE(ctx, ((uintptr_t)table & 15) == 0 && ((uintptr_t)x & 15) == 0, NNZ_EINVAL,
+                "lm_head_bf16: table and x must be 16-byte aligned");
+    return lm_head_bf16_launch(ctx, (const uint16_t *)table, (const f16_t *)x, logits, vocab, hidden);
+}
 
 int nnz_model_create(nnz_ctx *ctx, const nnz_model_config *cfg, nnz_model **out) {
     NNZ_CHECK_CTX(ctx);

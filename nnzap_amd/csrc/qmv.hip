@@ -294,12 +294,114 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                                                         uvalid, units, G);
     };
 
-    // ---- x slice for the owned units, kept in registers -------------------
-    // A unit past the row end holds unit 0's (finite) values; its scale is
-    // zero, so it adds nothing and needs no masking here.
+    // ---- 1-bit signed nibble tables (LUT, full-wave rows only) --------------
+    // For each unit j of a lane and nibble n (columns 4n..4n+3 of the unit)
+    // the 16 signed sums T[e] = sum_k (bit k of e ? +x : -x)[4n + k], so a
+    // row's +-x sum over 32 weights is 8 table reads (no mask-and-add per
+    // weight, no separate sum of x).  The tables are built straight from the
+    // prologue's own loads: thread (lane l, wave w) loads the float4 of
+    // nibbles n = 2w, 2w+1 of units u = l + 64 j, normalises it (RMSNorm
+    // input) and writes its 2 x 16 entries at [j][n][e][l] -- the lane that
+    // reads a unit's tables is the one that owns it, so the 64 reads (and
+    // writes) of a wave hit 64 distinct banks.  One barrier after the norm's
+    // sum of squares, one after the tables.
+    __shared__ float lut[LUT ? NV * 8 * 16 * 64 : 1];
     float xr[NV][32];
     float xsum[NV];
-    if constexpr (NORM) {
+    if constexpr (LUT) {
+        static_assert(!MERGE, "tables are built from x or the normalised residual");
+        const int wid = threadIdx.x >> 6;
+        float v[NV][2][4];
+        if constexpr (NORM) {
+            __shared__ float red[4];
+            const float4 *res4 = (const float4 *)a.x;
+            const float4 *nw4 = (const float4 *)a.norm_w;
+            float4 rv[NV][2], wv[NV][2];
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb) {
+                    const uint32_t i4 = uvalid[j] ? (uint32_t)(lane + 64 * j) * 8u + 2u * wid + sb : 0u;
+                    rv[j][sb] = res4[i4];
+                    wv[j][sb] = nw4[i4];
+                }
+            first_weights();
+            float ss = 0.f;
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb) {
+                    if (!uvalid[j]) rv[j][sb] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    ss = fmaf(rv[j][sb].x, rv[j][sb].x, ss);
+                    ss = fmaf(rv[j][sb].y, rv[j][sb].y, ss);
+                    ss = fmaf(rv[j][sb].z, rv[j][sb].z, ss);
+                    ss = fmaf(rv[j][sb].w, rv[j][sb].w, ss);
+                }
+            ss = wave_sum(ss);
+            if (lane == 0) red[wid] = ss;
+            __syncthreads();
+            ss = (red[0] + red[1]) + (red[2] + red[3]);
+            const float rms = rsqrtf(ss / (float)K + a.eps);
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb) {
+                    float t[4] = {rv[j][sb].x * rms * wv[j][sb].x, rv[j][sb].y * rms * wv[j][sb].y,
+                                  rv[j][sb].z * rms * wv[j][sb].z, rv[j][sb].w * rms * wv[j][sb].w};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if constexpr (FAITH) t[e] = bf16_trunc(t[e]);
+                        v[j][sb][e] = (float)(f16_t)t[e];
+                    }
+                }
+        } else {
+            // x as given: 4 columns = one float4 (f32) or 8 bytes (f16 / bf16)
+            float4 xf[NV][2];
+            uint2 xh[NV][2];
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb) {
+                    const uint32_t i4 = uvalid[j] ? (uint32_t)(lane + 64 * j) * 8u + 2u * wid + sb : 0u;
+                    if constexpr (XDT == NNZ_F32) xf[j][sb] = ((const float4 *)a.x)[i4];
+                    else xh[j][sb] = ((const uint2 *)a.x)[i4];
+                }
+            first_weights();
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+#pragma unroll
+                for (int sb = 0; sb < 2; ++sb) {
+                    if constexpr (XDT == NNZ_F32) {
+                        v[j][sb][0] = xf[j][sb].x; v[j][sb][1] = xf[j][sb].y;
+                        v[j][sb][2] = xf[j][sb].z; v[j][sb][3] = xf[j][sb].w;
+                    } else {
+                        const uint32_t h[4] = {xh[j][sb].x & 0xFFFFu, xh[j][sb].x >> 16,
+                                               xh[j][sb].y & 0xFFFFu, xh[j][sb].y >> 16};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            v[j][sb][e] = XDT == NNZ_F16 ? (float)__builtin_bit_cast(f16_t, (uint16_t)h[e])
+                                                         : bf16_to_f32((uint16_t)h[e]);
+                    }
+                    if (!uvalid[j]) v[j][sb][0] = v[j][sb][1] = v[j][sb][2] = v[j][sb][3] = 0.f;
+                }
+        }
+        float *const dst = lut + lane;
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+#pragma unroll
+            for (int sb = 0; sb < 2; ++sb) {
+                const int n = 2 * wid + sb;
+                const float *x4 = v[j][sb];
+                // bit 0 of e signs x0, bit 1 x1, bit 2 x2, bit 3 x3
+                const float p1 = x4[0] - x4[1], p3 = x4[0] + x4[1];
+                const float q1 = x4[2] - x4[3], q3 = x4[2] + x4[3];
+                const float p[4] = {-p3, p1, -p1, p3};
+                const float q[4] = {-q3, q1, -q1, q3};
+#pragma unroll
+                for (int e = 0; e < 16; ++e) dst[((j * 8 + n) * 16 + e) * 64] = p[e & 3] + q[e >> 2];
+            }
+        __syncthreads();
+    } else if constexpr (NORM) {
         // The block normalises x once: each thread loads K/256 residual and
         // norm-weight values (K <= 2048*NV, so at most 2*NV float4 each),
         // the sum of squares is reduced through LDS, and the f16-rounded
@@ -514,42 +616,14 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
             }
         }
     }
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        float s = 0.f;
-#pragma unroll
-        for (int i = 0; i < 32; ++i) s += xr[j][i];
-        xsum[j] = s;
-    }
-
-    // ---- 1-bit nibble tables (LUT, full-wave rows only) --------------------
-    // For each owned unit j and nibble n (columns 4n..4n+3 of the unit), the
-    // 16 subset sums T[e] = sum_{k in e} x[4n+k], so a row's sum over its set
-    // bits is 8 table reads per 32 weights instead of 32 mask-and-adds.  All
-    // waves of a block own the same columns: wave w builds nibbles 2w, 2w+1
-    // of every unit and the block shares the tables through LDS, laid out
-    // [unit][nibble][entry][lane] so a wave's 64 reads hit 64 distinct banks.
-    __shared__ float lut[LUT ? NV * 8 * 16 * 64 : 1];
-    if constexpr (LUT) {
-        const int wid = threadIdx.x >> 6;
+    if constexpr (!LUT) {
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
+            float s = 0.f;
 #pragma unroll
-            for (int n = 0; n < 8; ++n) {
-                if ((n >> 1) != wid) continue;   // wave-uniform
-                const float x0 = xr[j][4 * n], x1 = xr[j][4 * n + 1];
-                const float x2 = xr[j][4 * n + 2], x3 = xr[j][4 * n + 3];
-                float t[16];
-                t[0] = 0.f; t[1] = x0; t[2] = x1; t[3] = x0 + x1;
-                t[4] = x2; t[5] = x2 + x0; t[6] = x2 + x1; t[7] = x2 + t[3];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) t[8 + e] = e == 0 ? x3 : x3 + t[e];
-                float *dst = lut + ((j * 8 + n) * 16) * 64 + lane;
-#pragma unroll
-                for (int e = 0; e < 16; ++e) dst[e * 64] = t[e];
-            }
+            for (int i = 0; i < 32; ++i) s += xr[j][i];
+            xsum[j] = s;
         }
-        __syncthreads();
     }
 
     // ---- software-pipelined row loop ---------------------------------------
@@ -574,7 +648,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                         float sb = 0.f;
 #pragma unroll
                         for (int n = 0; n < 8; ++n) sb += tb[(n * 16 + ((w >> (4 * n)) & 15u)) * 64];
-                        accv = fmaf(s, 2.f * sb - xsum[j], accv);
+                        accv = fmaf(s, sb, accv);
                     } else if constexpr (BITS == 1) {
                         const uint32_t w = cur.cw[m][r][j][0];
                         float sb = 0.f;
@@ -830,7 +904,7 @@ int launch_nv(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks, bool lut) 
         // the merge prologue keeps every chunk's partials in registers
         return nnz_fail(ctx, NNZ_EUNSUPPORTED, "merge_o_resadd: K > 4096");
     } else {
-        if constexpr (BITS == 1 && NV <= LUT_MAX_NV) {
+        if constexpr (BITS == 1 && NV <= LUT_MAX_NV && XIN != XIN_MERGE) {
             if (lut) launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, true>(ctx, a, R, blocks);
             else launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false>(ctx, a, R, blocks);
         } else {

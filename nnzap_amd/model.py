@@ -46,11 +46,11 @@ class DecoderModel:
             self.h = None
 
     def __del__(self):
-        if sys.is_finalizing():  # HIP runtime may be gone; see ops.Device
-            return
         try:
+            if sys.is_finalizing():  # HIP runtime may be gone; see ops.Device
+                return
             self.close()
-        except Exception:
+        except Exception:   # module globals may already be gone at teardown
             pass
 
     def _mcall(self, name, *args):

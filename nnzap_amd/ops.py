@@ -102,11 +102,11 @@ class Device:
         # During interpreter finalization the HIP runtime's C++ state may
         # already be destroyed; the atexit hook above has closed every live
         # object before that point.
-        if sys.is_finalizing():
-            return
         try:
+            if sys.is_finalizing():
+                return
             self.close()
-        except Exception:
+        except Exception:   # module globals may already be gone at teardown
             pass
 
     def call(self, name: str, *args) -> None:
@@ -436,6 +436,13 @@ def dispatch_sample(dev, logits, out_index, rng, workspace, temperature: float,
     dev.call("nnz_dispatch_sample", _v(logits), logits.numel(), C.byref(p), _v(rng),
              _v(workspace), workspace.numel() * workspace.element_size() if workspace is not None
              else 0, _v(out_index), _v(out_prob))
+
+
+def dispatch_lm_head_bf16(dev, table, x, logits):
+    """LM head of transformer.zig:2730-2785 with the tied bf16 embedding
+    table (:297): logits = table . x, table bf16 [V, H], x f16 [H]."""
+    V, H = table.shape
+    dev.call("nnz_dispatch_lm_head_bf16", _v(table), _v(x), _v(logits), V, H)
 
 
 __all__ = [n for n in dir() if n.startswith("dispatch_")] + ["Device", "DeviceQWeight",

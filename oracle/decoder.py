@@ -39,12 +39,28 @@ def _f32(x):
 
 
 class OracleDecoder:
-    def __init__(self, w: DecoderWeights, max_ctx: int | None = None):
+    def __init__(self, w: DecoderWeights, max_ctx: int | None = None, round16: bool = True,
+                 matmul_dtype=np.float64):
+        """``round16=False`` drops the float16 storage roundings of the
+        activations (normalised inputs, q/k/v, attention output, SiLU*mul,
+        final norm) and keeps the float16 KV cache and the float32 residual:
+        the precision of the reference's own CPU test references
+        (transformer_test.zig:364-716), against which the composition is
+        pinned.
+
+        ``matmul_dtype=np.float32`` evaluates every weight product in float32
+        (the precision of the GPU's accumulators) with the same rounding
+        points: the spread between that and the float64 oracle is the
+        rounding noise any float32 implementation carries, which sets the
+        end-to-end bar at full size."""
         cfg = w.cfg
         self.cfg, self.w = cfg, w
+        self.mdt = matmul_dtype
+        self.r16 = O.f16 if round16 else (lambda x: np.asarray(x, dtype=np.float64))
         self.q4 = getattr(cfg, "quant_format", 0) == 1
-        self.W = [{n: O.dequant(layer[n]) for n in PROJS} for layer in w.layers]
-        self.lm = O.dequant(w.lm_head) if w.lm_head is not None else None
+        self.W = [{n: O.dequant(layer[n]).astype(matmul_dtype) for n in PROJS}
+                  for layer in w.layers]
+        self.lm = O.dequant(w.lm_head).astype(matmul_dtype) if w.lm_head is not None else None
         T = max_ctx or cfg.max_context_length
         self.kc = np.zeros((cfg.num_layers, cfg.num_kv_heads, T, cfg.head_dim))
         self.vc = np.zeros((cfg.num_layers, cfg.num_kv_heads, T, cfg.head_dim))
@@ -80,11 +96,11 @@ class OracleDecoder:
         return O.bf16_trunc(_f32(x)) if self.q4 else x
 
     def _norm16(self, x, w):
-        return O.f16(self._t(O.rmsnorm(x, w, self.cfg.rms_eps)))
+        return self.r16(self._t(O.rmsnorm(x, w, self.cfg.rms_eps)))
 
     def lm_head(self, xf: np.ndarray) -> np.ndarray:
         if self.lm is not None:
-            return _f32(self._t(xf @ self.lm.T))
+            return _f32(self._t((xf.astype(self.mdt) @ self.lm.T).astype(np.float64)))
         table = S.bf16_bits_to_f32(self.w.embed_bf16).astype(np.float64)
         return _f32(xf @ table.T)
 
@@ -92,44 +108,52 @@ class OracleDecoder:
     def forward(self, ids, start: int) -> np.ndarray:
         """Run tokens ``ids`` at positions start..start+P-1; returns the logits
         of every token [P, vocab] (float32 values as float64)."""
-        cfg = self.cfg
-        P = len(ids)
-        D, Hq, Hkv = cfg.head_dim, cfg.num_query_heads, cfg.num_kv_heads
-        g = Hq // Hkv
         res = _f32(self.embed_rows(ids))
-        positions = np.arange(start, start + P)
-        for l, layer in enumerate(self.w.layers):
-            W = self.W[l]
-            xn = self._norm16(res, layer["attn_norm"])
-            q = O.f16(self._t(xn @ W["q"].T))
-            k = O.f16(self._t(xn @ W["k"].T))
-            v = O.f16(self._t(xn @ W["v"].T))
-            qn = np.stack([O.head_norm_rope(q[p].reshape(Hq, D), layer["q_norm"], int(positions[p]),
-                                            cfg.rope_theta, cfg.rms_eps) for p in range(P)])
-            kn = np.stack([O.f16(O.head_norm_rope(k[p].reshape(Hkv, D), layer["k_norm"],
-                                                  int(positions[p]), cfg.rope_theta, cfg.rms_eps))
-                           for p in range(P)])
-            self.kc[l, :, start:start + P, :] = kn.transpose(1, 0, 2)
-            self.vc[l, :, start:start + P, :] = v.reshape(P, Hkv, D).transpose(1, 0, 2)
-            att = np.empty((P, Hq, D))
-            scale = 1.0 / np.sqrt(D)
-            T = start + P
-            K = self.kc[l, :, :T, :]
-            V = self.vc[l, :, :T, :]
-            mask = np.arange(T)[None, :] <= positions[:, None]  # [P, T]
-            for h in range(Hq):
-                s = qn[:, h, :] @ K[h // g].T * scale  # [P, T]
-                s = np.where(mask, s, -np.inf)
-                s = np.exp(s - s.max(axis=1, keepdims=True))
-                s /= s.sum(axis=1, keepdims=True)
-                att[:, h, :] = s @ V[h // g]
-            att = O.f16(att.reshape(P, Hq * D))
-            res = _f32(res + self._t(att @ W["o"].T))
-            xn2 = self._norm16(res, layer["ffn_norm"])
-            hmid = O.f16(self._t(O.silu(xn2 @ W["gate"].T) * (xn2 @ W["up"].T)))
-            res = _f32(res + self._t(hmid @ W["down"].T))
+        for l in range(self.cfg.num_layers):
+            res = self.layer(l, res, start)
         xf = self._norm16(res, self.w.final_norm)
         return self.lm_head(xf)
+
+    def layer(self, l: int, res: np.ndarray, start: int) -> np.ndarray:
+        """One decoder block (forwardBlock, transformer.zig:2452-2564) for the
+        residual rows ``res`` [P, H] of tokens at positions start..start+P-1:
+        attention half then MLP half; appends the block's K/V rows to its
+        cache.  Returns the new residual (float32 values)."""
+        cfg = self.cfg
+        P = res.shape[0]
+        D, Hq, Hkv = cfg.head_dim, cfg.num_query_heads, cfg.num_kv_heads
+        g = Hq // Hkv
+        positions = np.arange(start, start + P)
+        layer, W, r16 = self.w.layers[l], self.W[l], self.r16
+        mm = lambda a, b: (a.astype(self.mdt) @ b.T).astype(np.float64)  # noqa: E731
+        xn = self._norm16(res, layer["attn_norm"])
+        q = r16(self._t(mm(xn, W["q"])))
+        k = r16(self._t(mm(xn, W["k"])))
+        v = r16(self._t(mm(xn, W["v"])))
+        qn = np.stack([O.head_norm_rope(q[p].reshape(Hq, D), layer["q_norm"], int(positions[p]),
+                                        cfg.rope_theta, cfg.rms_eps) for p in range(P)])
+        kn = np.stack([O.f16(O.head_norm_rope(k[p].reshape(Hkv, D), layer["k_norm"],
+                                              int(positions[p]), cfg.rope_theta, cfg.rms_eps))
+                       for p in range(P)])
+        self.kc[l, :, start:start + P, :] = kn.transpose(1, 0, 2)
+        self.vc[l, :, start:start + P, :] = O.f16(v).reshape(P, Hkv, D).transpose(1, 0, 2)
+        att = np.empty((P, Hq, D))
+        scale = 1.0 / np.sqrt(D)
+        T = start + P
+        K = self.kc[l, :, :T, :]
+        V = self.vc[l, :, :T, :]
+        mask = np.arange(T)[None, :] <= positions[:, None]  # [P, T]
+        for h in range(Hq):
+            s = qn[:, h, :] @ K[h // g].T * scale  # [P, T]
+            s = np.where(mask, s, -np.inf)
+            s = np.exp(s - s.max(axis=1, keepdims=True))
+            s /= s.sum(axis=1, keepdims=True)
+            att[:, h, :] = s @ V[h // g]
+        att = r16(att.reshape(P, Hq * D))
+        res = _f32(res + self._t(mm(att, W["o"])))
+        xn2 = self._norm16(res, layer["ffn_norm"])
+        hmid = r16(self._t(O.silu(mm(xn2, W["gate"])) * mm(xn2, W["up"])))
+        return _f32(res + self._t(mm(hmid, W["down"])))
 
     def generate(self, prompt, n_new: int, eos=()):
         """Greedy generate with the reference's loop (transformer.zig:3942-4030):

@@ -6,7 +6,8 @@ checkpoints), so these fixtures are produced by the oracle from seeded
 synthetic inputs -- the seeds make the inputs reproducible on any host.
 
   python tests/golden/make_golden.py small     # kernel-level vectors (seconds)
-  python tests/golden/make_golden.py config5   # 28-layer greedy tokens (minutes, ~20 GB RAM)
+  python tests/golden/make_golden.py config5        # 28-layer greedy tokens + logits (minutes, ~20 GB RAM)
+  python tests/golden/make_golden.py config5_unit   # the same with norm weights 1 + N(0, 0.02)
 """
 from __future__ import annotations
 
@@ -72,7 +73,46 @@ def small():
     print("wrote small_vectors.json")
 
 
-def config5(n_prompt=512, n_new=256, norm_mode="small"):
+LOGIT_STEPS = 16     # decode steps whose logits are recorded
+LOGIT_STRIDE = 512   # every 512th logit is recorded besides the top 8
+
+
+def logit_summary(logits):
+    """What the GPU test compares at full size: the top 8 (index, value), a
+    strided sample of the whole vector, max |logit|, and a sha256 of the
+    float32 values (identifies the vector; not compared on the GPU)."""
+    lg = np.asarray(logits, dtype=np.float64)
+    top = np.argsort(-lg, kind="stable")[:8]
+    return {"top8_idx": top.tolist(), "top8_val": lg[top].tolist(),
+            "sample": lg[::LOGIT_STRIDE].tolist(), "max_abs": float(np.max(np.abs(lg))),
+            "sha256": sha(lg.astype(np.float32))}
+
+
+def fp32_noise(w, prompt, summary) -> float:
+    """Normwise spread (max |err| / max |logit| over the recorded entries)
+    between the float64 oracle's last-prompt-token logits and the same
+    algorithm with every weight product in float32 -- the rounding noise any
+    float32 implementation carries end to end at this size (float16
+    activation roundings flip and propagate through the 28 layers)."""
+    od = OracleDecoder(w, max_ctx=len(prompt) + 8, matmul_dtype=np.float32)
+    lg = od.forward(list(prompt), 0)[-1]
+    idx = np.concatenate([np.array(summary["top8_idx"]), np.arange(0, len(lg), LOGIT_STRIDE)])
+    want = np.concatenate([np.array(summary["top8_val"]), np.array(summary["sample"])])
+    return float(np.max(np.abs(lg[idx] - want)) / summary["max_abs"])
+
+
+def add_noise(name: str):
+    path = os.path.join(HERE, name)
+    g = json.load(open(path))
+    cfg = cf.BONSAI_1_7B
+    w = cf.decoder_weights(cfg, norm_mode=g["norm_mode"], host_embed=False)
+    g["fp32_noise"] = fp32_noise(w, cf.prompt_ids(cfg, g["n_prompt"]), g["logits"][0])
+    with open(path, "w") as f:
+        json.dump(g, f)
+    print(f"{name}: fp32 noise {g['fp32_noise']:.3e}")
+
+
+def config5(n_prompt=512, n_new=256, norm_mode="small", out_name="config5_tokens.json"):
     t0 = time.time()
     cfg = cf.BONSAI_1_7B
     w = cf.decoder_weights(cfg, norm_mode=norm_mode, host_embed=False)  # rows on demand
@@ -82,6 +122,7 @@ def config5(n_prompt=512, n_new=256, norm_mode="small"):
     prompt = cf.prompt_ids(cfg, n_prompt)
     logits = od.forward(list(prompt), 0)[-1]
     print(f"prefill {time.time() - t0:.0f}s", flush=True)
+    summaries = [logit_summary(logits)]      # last prefill token, then decode steps
     pos = n_prompt
     toks, margins = [], []
     for i in range(n_new):
@@ -90,15 +131,23 @@ def config5(n_prompt=512, n_new=256, norm_mode="small"):
         toks.append(int(t))
         margins.append(float(srt[-1] - srt[-2]))
         logits = od.forward([t], pos)[0]
+        if i < LOGIT_STEPS:
+            summaries.append(logit_summary(logits))
         pos += 1
         if i % 16 == 0:
             print(f"step {i} token {t} margin {margins[-1]:.3e} ({time.time() - t0:.0f}s)", flush=True)
+    del od
+    noise = fp32_noise(w, prompt, summaries[0])
     res = {"n_prompt": n_prompt, "n_new": n_new, "norm_mode": norm_mode, "lm_head": "q1",
+           "fp32_noise": noise,
            "prompt_sha256": sha(prompt), "tokens": toks, "margins": margins,
-           "min_margin": min(margins)}
-    with open(os.path.join(HERE, "config5_tokens.json"), "w") as f:
+           "min_margin": min(margins), "distinct_tokens": len(set(toks)),
+           "logit_stride": LOGIT_STRIDE,
+           "logits": summaries}
+    with open(os.path.join(HERE, out_name), "w") as f:
         json.dump(res, f)
-    print(f"wrote config5_tokens.json in {time.time() - t0:.0f}s; min margin {min(margins):.3e}")
+    print(f"wrote {out_name} in {time.time() - t0:.0f}s; min margin {min(margins):.3e}; "
+          f"{len(set(toks))} distinct tokens")
 
 
 if __name__ == "__main__":
@@ -107,5 +156,13 @@ if __name__ == "__main__":
         small()
     elif what == "config5":
         config5()
+    elif what == "noise":
+        # record the float32 noise in existing config-5 fixtures
+        add_noise("config5_tokens.json")
+        add_noise("config5_unit_tokens.json")
+    elif what == "config5_unit":
+        # norm weights 1 + N(0, 0.02): the fallback of the norm-weight
+        # decision, whose token stream is not periodic
+        config5(norm_mode="unit", out_name="config5_unit_tokens.json")
     else:
         raise SystemExit(f"unknown fixture set {what}")

@@ -53,3 +53,34 @@ def test_dims_structs_match_reference_layout():
     assert C.sizeof(L.GQAFusedDims) == 36
     assert C.sizeof(L.EmbedDims) == 16
     assert C.sizeof(L.FusedKNormRoPEKVDims) == 24
+
+
+def _c_check_lib():
+    """tests/c/abi_check.c compiled against include/nnz.h (gcc, -Werror):
+    its static_asserts pin every dims struct's size and field offsets to the
+    reference's extern structs (transformer.zig:389-479)."""
+    import importlib.util
+    from pathlib import Path
+    here = Path(__file__).resolve().parent / "c"
+    spec = importlib.util.spec_from_file_location("nnz_c_tests_build", here / "build.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return C.CDLL(str(mod.build()))
+
+
+def test_c_translation_unit_compiles_and_checks_error_paths():
+    lib = _c_check_lib()
+    assert lib.nnz_abi_check_host() == 0
+
+
+def test_ctypes_argument_counts_match_header():
+    """Every ctypes prototype takes as many arguments as the header
+    declaration (a drifted signature would pass the name check)."""
+    import re
+    text = re.sub(r"/\*.*?\*/", "", L.HEADER.read_text(), flags=re.S)
+    decls = dict(re.findall(r"\b(nnz_[a-z0-9_]+)\s*\(([^()]*)\)\s*;", text))
+    assert set(decls) == set(L.PROTOS)
+    for name, params in decls.items():
+        params = params.strip()
+        n = 0 if params in ("", "void") else params.count(",") + 1
+        assert n == len(L.PROTOS[name][1]), f"{name}: header {n} args, ctypes {len(L.PROTOS[name][1])}"

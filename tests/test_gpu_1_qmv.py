@@ -310,3 +310,51 @@ def test_qmv_rejects_bad_dims(dev):
     assert e.value.code == -1
     with pytest.raises(ops.NnzError):
         ops.dispatch_q4mv(dev, dw, x, y)  # Q1 weight into a Q4 entry point
+
+
+def test_c_abi_config2_from_c(dev):
+    """BASELINE config 2 through the C ABI from a C translation unit
+    (tests/c/abi_check.c: nnz_ctx_create, nnz_alloc, nnz_upload,
+    nnz_dispatch_qmv, nnz_stream_sync, nnz_download), against the oracle and
+    the committed golden vector."""
+    import ctypes as C
+    import json
+    import os
+    from pathlib import Path
+    print("config2 QMV from C", flush=True)
+    so = Path(__file__).resolve().parent / "c" / "libnnz_abi_check.so"
+    if not so.exists():
+        import importlib.util
+        spec = importlib.util.spec_from_file_location("nnz_c_tests_build", so.parent / "build.py")
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        mod.build()
+    lib = C.CDLL(str(so))
+    w, x = cf.config2()
+    y = np.zeros(w.M, dtype=np.float32)
+    codes = np.ascontiguousarray(w.codes, dtype=np.uint32)
+    scales = np.ascontiguousarray(w.scales, dtype=np.uint16)
+    xc = np.ascontiguousarray(x, dtype=np.float32)
+    err = C.create_string_buffer(256)
+    rc = lib.nnz_abi_qmv_config(codes.ctypes.data_as(C.c_void_p), scales.ctypes.data_as(C.c_void_p),
+                                xc.ctypes.data_as(C.c_void_p), y.ctypes.data_as(C.c_void_p),
+                                C.c_uint32(w.M), C.c_uint32(w.K), C.c_uint32(w.group_size), err)
+    assert rc == 0, err.value.decode()
+    assert_close(y, O.qmv(w, x), what="config2 from C")
+    gold = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "small_vectors.json")))
+    assert_close(y[:64], np.array(gold["config2"]["y64"]), what="config2 golden")
+
+
+@pytest.mark.parametrize("V,H", [(5003, 2048), (1000, 4096), (777, 2560)])
+def test_lm_head_bf16(dev, V, H):
+    """Tied bf16 LM head (nnz_dispatch_lm_head_bf16): logits = table . x with
+    f32 accumulation; the pipelined kernel (hidden 2048 / 4096, ragged row
+    count) and the lane-group kernel (hidden 2560)."""
+    table = S.f64_to_bf16_bits(0.02 * S.normal(600 + H, V * H)).reshape(V, H)
+    x = S.normal(601, H).astype(np.float16)
+    tb = torch.from_numpy(table.view(np.int16)).cuda().view(torch.bfloat16)
+    y = torch.full((V,), float("nan"), dtype=torch.float32, device="cuda")
+    ops.dispatch_lm_head_bf16(dev, tb, tdev(x), y)
+    dev.sync()
+    ref = S.bf16_bits_to_f32(table).astype(np.float64) @ x.astype(np.float64)
+    assert_close(host(y), ref, what=f"lm_head_bf16 V={V} H={H}")

@@ -148,28 +148,76 @@ def test_device_embedding_generator_matches_host(mdev):
     assert np.array_equal(host, ref)
 
 
-def test_config5_golden_tokens(mdev):
-    """BASELINE config 5 at full size: 512 prompt ids, 256 greedy steps; tokens
-    must equal the oracle's golden list (committed fixture)."""
-    path = os.path.join(GOLDEN, "config5_tokens.json")
+def _check_logit_summary(got, ref, what, rel=1e-3):
+    """Full-size logits against the golden summary (top 8 and a strided
+    sample of the whole vector): max |err| <= rel * max |logit| on every
+    recorded entry, and the same argmax wherever the oracle's top-2 margin
+    exceeds that bar."""
+    got = np.asarray(got, dtype=np.float64)
+    idx = np.concatenate([np.array(ref["top8_idx"]),
+                          np.arange(0, len(got), ref.get("stride", 512))])
+    want = np.concatenate([np.array(ref["top8_val"]), np.array(ref["sample"])])
+    bar = rel * ref["max_abs"]
+    err = np.max(np.abs(got[idx] - want))
+    assert err <= bar, f"{what}: max |err| {err:.3e} > {bar:.3e}"
+    assert abs(np.max(np.abs(got)) - ref["max_abs"]) <= bar, f"{what}: max |logit|"
+    if ref["top8_val"][0] - ref["top8_val"][1] > 2 * bar:
+        assert int(np.argmax(got)) == ref["top8_idx"][0], f"{what}: argmax"
+
+
+@pytest.mark.parametrize("name", ["config5_tokens.json", "config5_unit_tokens.json"])
+def test_config5_golden(mdev, name):
+    """BASELINE config 5 at full size: 512 prompt ids, 256 greedy steps;
+    tokens must equal the oracle's golden list, and the logits of the last
+    prompt token and of the first 16 decode steps (teacher-forced with the
+    golden tokens) must match the golden summaries.  Two fixtures: the
+    literal norm weights ~N(0, 0.02), and 1 + N(0, 0.02), whose token stream
+    is not periodic."""
+    path = os.path.join(GOLDEN, name)
     if not os.path.exists(path):
         pytest.skip("golden fixture not generated yet")
     gold = json.load(open(path))
     cfg = cf.BONSAI_1_7B
-    print("config5: building weights", flush=True)
+    print(f"{name}: building weights", flush=True)
     w = cf.decoder_weights(cfg, norm_mode=gold["norm_mode"], host_embed=False)
     m = DecoderModel(mdev, cfg)
     try:
         m.load(w, embed_on_device=True)
         prompt = cf.prompt_ids(cfg, gold["n_prompt"])
-        print("config5: generating", flush=True)
+        print(f"{name}: generating", flush=True)
         toks, margins, _ = m.generate(prompt, gold["n_new"], use_graph=True)
+        ref = np.array(gold["tokens"], dtype=np.uint32)
+        # Greedy tokens are identical up to a step whose top-2 oracle margin
+        # is within twice the logit bar below: there the decision belongs to
+        # fp32-vs-fp64 rounding and the streams may part.
+        near = (2 * max(1e-3, 4 * gold.get("fp32_noise", 0.0)) * gold["logits"][0]["max_abs"]
+                if gold.get("logits") else 0.0)
+        first_bad = int(np.argmax(toks != ref)) if np.any(toks != ref) else -1
+        if first_bad >= 0:
+            mg = gold["margins"][first_bad]
+            assert mg < near, (f"first mismatch at step {first_bad}: got {toks[first_bad]}, "
+                               f"want {ref[first_bad]} (oracle margin {mg:.3e}, bar {near:.3e})")
+            print(f"{name}: streams part at near-tie step {first_bad} (margin {mg:.2e})")
+        ties = [i for i, mg in enumerate(gold["margins"]) if mg < near]
+        assert first_bad == -1 or first_bad >= (ties[0] if ties else 0)
+        sums = gold.get("logits", [])
+        # Bar: normwise 1e-3, or 4x the spread between the float64 oracle and
+        # the same algorithm with float32 products where that is larger
+        # (fp32_noise, recorded by make_golden.py): with norm weights near 1
+        # every layer passes meaningful activations on, float16 roundings
+        # flip between any two float32 evaluations and the flips propagate
+        # through 28 layers (7.6e-4 of max |logit| for that fixture).
+        rel = max(1e-3, 4 * gold.get("fp32_noise", 0.0))
+        if sums:
+            print(f"{name}: logits", flush=True)
+            for s_ in sums:
+                s_["stride"] = gold.get("logit_stride", 512)
+            _check_logit_summary(m.prefill(prompt, 0), sums[0], "last prompt token", rel)
+            for i, s_ in enumerate(sums[1:]):
+                got = m.forward_decode(int(ref[i]), gold["n_prompt"] + i)
+                _check_logit_summary(got, s_, f"decode step {i}", rel)
     finally:
         m.close()
-    ref = np.array(gold["tokens"], dtype=np.uint32)
-    first_bad = int(np.argmax(toks != ref)) if np.any(toks != ref) else -1
-    assert first_bad == -1, (f"first mismatch at step {first_bad}: got {toks[first_bad]}, "
-                            f"want {ref[first_bad]} (oracle margin {gold['margins'][first_bad]:.3e})")
 
 
 # -- MLX checkpoint -> device (loadWeights, model.zig:196-242) ------------------

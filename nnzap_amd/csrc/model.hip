@@ -138,48 +138,42 @@ __global__ __launch_bounds__(256) void dense_bf16_gemv_kernel(const uint16_t *E,
     }
 }
 
-// Tied bf16 LM head for hidden = 2048 * NV: a lane owns NV 32-column units
-// of every row (64 bytes each: four 16-byte loads), its x slice stays in
-// registers, and a wave takes R rows per step.  Two register sets alternate:
-// the next step's rows are loading while the current step computes, so each
-// wave keeps R * NV * 256 bytes of the table in flight.  The table is read
-// once per token and streams past the caches (non-temporal loads), leaving
-// the Infinity Cache to the layer weights and the KV cache.
-template <int NV, int R>
+// Tied bf16 LM head for hidden = 512 * NU: a row is NU segments of 512
+// columns (1 KB); lane l owns the 16-byte piece l of every segment, so each
+// load instruction of a wave reads one contiguous kilobyte.  The lane's x
+// slice (8 * NU values) stays in registers, and a wave takes R rows per
+// step.  Two register sets alternate: the next step's rows are loading
+// while the current step computes.  The table is read once per token and
+// streams past the caches (non-temporal loads), leaving the Infinity Cache
+// to the layer weights and the KV cache.
+template <int NU, int R>
 __global__ __launch_bounds__(256) void lm_head_bf16_kernel(const uint16_t *__restrict__ E,
                                                            const f16_t *__restrict__ x,
                                                            float *__restrict__ y, uint32_t M) {
-    constexpr uint32_t K = 2048 * NV;
+    constexpr uint32_t K = 512 * NU;
     const int lane = threadIdx.x & 63;
-    float xr[NV][32];
+    float xr[NU][8];
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        const uint4 *xp = (const uint4 *)(x + (size_t)(lane + 64 * j) * 32);
+    for (int v = 0; v < NU; ++v) {
+        const uint4 q = ((const uint4 *)x)[v * 64 + lane];
+        const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const uint4 q = xp[v];
-            const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                xr[j][8 * v + 2 * e] = (float)__builtin_bit_cast(f16_t, (uint16_t)(w4[e] & 0xFFFFu));
-                xr[j][8 * v + 2 * e + 1] = (float)__builtin_bit_cast(f16_t, (uint16_t)(w4[e] >> 16));
-            }
+        for (int e = 0; e < 4; ++e) {
+            xr[v][2 * e] = (float)__builtin_bit_cast(f16_t, (uint16_t)(w4[e] & 0xFFFFu));
+            xr[v][2 * e + 1] = (float)__builtin_bit_cast(f16_t, (uint16_t)(w4[e] >> 16));
         }
     }
     const uint32_t wave = blockIdx.x * 4 + (threadIdx.x >> 6);
     const uint32_t stride = gridDim.x * 4 * R;
     typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-    typedef v4u Rows[R][NV][4];
+    typedef v4u Rows[R][NU];
     auto load = [&](uint32_t b, Rows &dst) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const uint32_t row = b + r < M ? b + r : M - 1;
-            const v4u *p = (const v4u *)(E + (size_t)row * K);
+            const v4u *p = (const v4u *)(E + (size_t)row * K) + lane;
 #pragma unroll
-            for (int j = 0; j < NV; ++j)
-#pragma unroll
-                for (int v = 0; v < 4; ++v)
-                    dst[r][j][v] = __builtin_nontemporal_load(p + (lane + 64 * j) * 4 + v);
+            for (int v = 0; v < NU; ++v) dst[r][v] = __builtin_nontemporal_load(p + v * 64);
         }
     };
     auto consume = [&](const Rows &src, uint32_t b) {
@@ -188,17 +182,14 @@ __global__ __launch_bounds__(256) void lm_head_bf16_kernel(const uint16_t *__res
         for (int r = 0; r < R; ++r) {
             float acc = 0.f;
 #pragma unroll
-            for (int j = 0; j < NV; ++j)
+            for (int v = 0; v < NU; ++v) {
+                const uint32_t w4[4] = {src[r][v].x, src[r][v].y, src[r][v].z, src[r][v].w};
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const uint32_t w4[4] = {src[r][j][v].x, src[r][j][v].y, src[r][j][v].z,
-                                            src[r][j][v].w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        acc = fmaf(__uint_as_float(w4[e] << 16), xr[j][8 * v + 2 * e], acc);
-                        acc = fmaf(__uint_as_float(w4[e] & 0xFFFF0000u), xr[j][8 * v + 2 * e + 1], acc);
-                    }
+                for (int e = 0; e < 4; ++e) {
+                    acc = fmaf(__uint_as_float(w4[e] << 16), xr[v][2 * e], acc);
+                    acc = fmaf(__uint_as_float(w4[e] & 0xFFFF0000u), xr[v][2 * e + 1], acc);
                 }
+            }
             rt[r] = lane63(wave_sum_to_last(acc));
         }
         float t = rt[0];
@@ -376,7 +367,7 @@ nnz_gqa_dims gqa_dims(const nnz_model *m, uint32_t seq) {
 
 // Rows per wave step and blocks of the tied bf16 LM head (measured).
 constexpr int LMH_R = 2;
-constexpr uint32_t LMH_BLOCKS = 1024;
+constexpr uint32_t LMH_BLOCKS = 256;
 
 // Dense bf16 LM head: the pipelined kernel for hidden 2048 / 4096, the
 // lane-group kernel otherwise.
@@ -384,8 +375,8 @@ int lm_head_bf16_launch(nnz_ctx *ctx, const uint16_t *E, const f16_t *x, float *
                         uint32_t K) {
     if (K == 2048 || K == 4096) {
         const uint32_t blocks = std::min<uint32_t>(LMH_BLOCKS, ceil_div(V, 4u * LMH_R));
-        if (K == 2048) lm_head_bf16_kernel<1, LMH_R><<<blocks, 256, 0, ctx->stream>>>(E, x, logits, V);
-        else lm_head_bf16_kernel<2, LMH_R><<<blocks, 256, 0, ctx->stream>>>(E, x, logits, V);
+        if (K == 2048) lm_head_bf16_kernel<4, LMH_R><<<blocks, 256, 0, ctx->stream>>>(E, x, logits, V);
+        else lm_head_bf16_kernel<8, LMH_R><<<blocks, 256, 0, ctx->stream>>>(E, x, logits, V);
         NNZ_LAUNCHED(ctx);
         return NNZ_OK;
     }

@@ -156,10 +156,20 @@ __device__ __forceinline__ SegPtrs seg_mat(const QmvArgs &a, int seg) {
     return r;
 }
 
+// Per-lane unit offsets, fixed for the whole kernel: word offset of unit j
+// within a row (0 for a unit past the row end, whose scale is zeroed) and
+// its group index within the row's scales.
+template <int NV>
+struct LaneUnits {
+    uint32_t uoff[NV];   // units (32-column pieces) from the row start
+    uint32_t ugrp[NV];   // scale groups from the row start
+    bool ok[NV];         // the unit exists
+};
+
 template <int BITS, int NMAT, int R, int NV, bool RES>
 __device__ __forceinline__ void load_step(const QmvArgs &a, StepRegs<NMAT, R, NV, (BITS == 1 ? 1 : 4)> &s,
-                                          uint32_t base, int RPW, int rr, int ll, int LPR,
-                                          const bool (&uvalid)[NV], uint32_t units, uint32_t G) {
+                                          uint32_t base, int RPW, int rr, const LaneUnits<NV> &lu,
+                                          uint32_t units, uint32_t G) {
     constexpr int VEC = (BITS == 1) ? 1 : 4;
     const uint32_t words_per_row = units * VEC;
     // Matrix pointers of this step, chosen with a wave-uniform segment index
@@ -182,44 +192,42 @@ __device__ __forceinline__ void load_step(const QmvArgs &a, StepRegs<NMAT, R, NV
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
+        // With whole-wave rows (rr == 0) the row and its offsets are
+        // wave-uniform: scalar arithmetic, one vector add per address.
         const uint32_t row = base + (uint32_t)(r * RPW + rr);
         const bool rv = row < a.M;
-        const uint32_t lrow = row - seg_start;
+        // Unconditional loads from a clamped address (row 0 stands in for a
+        // row past the end, unit 0 for a unit past the row end); the dead
+        // lane's scale and bias are zeroed so its weights contribute 0.
+        const uint32_t lr = rv ? row - seg_start : 0u;
         if constexpr (RES) {  // residual rows this step will add to, read early
             static_assert(NMAT == 1, "residual add has one matrix");
-            s.res[r] = ((gptr<const float>)outp)[rv ? lrow : 0u];
+            s.res[r] = ((gptr<const float>)outp)[lr];
         }
+        const size_t rw = (size_t)lr * words_per_row, rg = (size_t)lr * G;
 #pragma unroll
         for (int m = 0; m < NMAT; ++m) {
-            const gptr<const uint32_t> codes = cp[m];
-            const gptr<const uint16_t> scales = sp[m];
-            const gptr<const uint16_t> biases = bp[m];
+            const gptr<const uint32_t> codes = cp[m] + rw;
+            const gptr<const uint16_t> scales = sp[m] + rg;
+            const gptr<const uint16_t> biases = bp[m] + rg;
 #pragma unroll
             for (int j = 0; j < NV; ++j) {
-                // Unconditional loads from a clamped address (word 0 of the
-                // matrix stands in for a lane past the end); the dead lane's
-                // scale and bias are zeroed so its weights contribute 0.
-                const bool ok = rv && uvalid[j];
-                const uint32_t u = ok ? (uint32_t)ll + (uint32_t)(LPR * j) : 0u;
-                const uint32_t lr = ok ? lrow : 0u;
-                const size_t wofs = (size_t)lr * words_per_row + (size_t)u * VEC;
                 // R == 8 is chosen only for vocabulary-sized matrices (the LM
                 // head), read once per token: load those weights
                 // non-temporally so they do not evict the layer weights and
                 // the KV cache (measured: +0.8% decode tok/s)
                 if constexpr (VEC == 1) {
-                    if constexpr (R == 8) s.cw[m][r][j][0] = __builtin_nontemporal_load(&codes[wofs]);
-                    else s.cw[m][r][j][0] = codes[wofs];
+                    if constexpr (R == 8) s.cw[m][r][j][0] = __builtin_nontemporal_load(&codes[lu.uoff[j]]);
+                    else s.cw[m][r][j][0] = codes[lu.uoff[j]];
                 } else {
-                    const u32x4 q = *(gptr<const u32x4>)(codes + wofs);
+                    const u32x4 q = *(gptr<const u32x4>)(codes + (size_t)lu.uoff[j] * VEC);
                     s.cw[m][r][j][0] = q.x; s.cw[m][r][j][1] = q.y;
                     s.cw[m][r][j][2] = q.z; s.cw[m][r][j][3] = q.w;
                 }
-                const size_t gidx = (size_t)lr * G + (u * 32u) / a.gs;
-                if constexpr (R == 8) s.sc[m][r][j] = __builtin_nontemporal_load(&scales[gidx]);
-                else s.sc[m][r][j] = scales[gidx];
-                if constexpr (BITS == 4) s.bi[m][r][j] = biases[gidx];
-                s.ok[m][r][j] = ok;
+                if constexpr (R == 8) s.sc[m][r][j] = __builtin_nontemporal_load(&scales[lu.ugrp[j]]);
+                else s.sc[m][r][j] = scales[lu.ugrp[j]];
+                if constexpr (BITS == 4) s.bi[m][r][j] = biases[lu.ugrp[j]];
+                s.ok[m][r][j] = rv && lu.ok[j];
             }
         }
     }
@@ -255,14 +263,18 @@ __device__ __forceinline__ void qmv_epilogue(const QmvArgs &a, void *out0, uint3
     }
 }
 
-template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH, int NV, int R, bool LUT>
+// FULL: whole-wave rows (LPR == 64, every K >= 2048) fixed at compile time,
+// so that row indices, offsets and the row reductions are wave-uniform.
+template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH, int NV, int R, bool LUT,
+          bool FULL>
 __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
     static_assert(!LUT || BITS == 1, "nibble tables are for 1-bit weights");
+    static_assert(!LUT || FULL, "nibble tables need whole-wave rows");
     constexpr bool NORM = XIN == XIN_NORM;
     constexpr bool MERGE = XIN == XIN_MERGE;
     constexpr int VEC = (BITS == 1) ? 1 : 4;  // u32 words per 32-column unit
     const int lane = threadIdx.x & 63;
-    const int lpr_log2 = (int)a.lpr_log2;
+    const int lpr_log2 = FULL ? 6 : (int)a.lpr_log2;
     const int LPR = 1 << lpr_log2;
     const int RPW = 64 >> lpr_log2;
     const int rr = lane >> lpr_log2;       // sub-row within the wave step
@@ -272,8 +284,14 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
     const uint32_t G = K / a.gs;            // groups per row
 
     bool uvalid[NV];
+    LaneUnits<NV> lu;
 #pragma unroll
-    for (int j = 0; j < NV; ++j) uvalid[j] = (uint32_t)ll + (uint32_t)(LPR * j) < units;
+    for (int j = 0; j < NV; ++j) {
+        uvalid[j] = (uint32_t)ll + (uint32_t)(LPR * j) < units;
+        lu.ok[j] = uvalid[j];
+        lu.uoff[j] = uvalid[j] ? (uint32_t)ll + (uint32_t)(LPR * j) : 0u;
+        lu.ugrp[j] = (lu.uoff[j] * 32u) / a.gs;
+    }
 
     const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
     const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
@@ -290,8 +308,8 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
     // re-reads rows that are valid, and their values go unused.
     StepRegs<NMAT, R, NV, VEC> cur;
     auto first_weights = [&]() {
-        load_step<BITS, NMAT, R, NV, EPI == EPI_RESADD>(a, cur, base < a.M ? base : 0u, RPW, rr, ll, LPR,
-                                                        uvalid, units, G);
+        load_step<BITS, NMAT, R, NV, EPI == EPI_RESADD>(a, cur, base < a.M ? base : 0u, RPW, rr, lu,
+                                                        units, G);
     };
 
     // ---- 1-bit signed nibble tables (LUT, full-wave rows only) --------------
@@ -630,8 +648,8 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
     for (; base < a.M; base += nwaves * rows_per_iter) {
         const uint32_t next = base + nwaves * rows_per_iter;
         StepRegs<NMAT, R, NV, VEC> nxt;
-        load_step<BITS, NMAT, R, NV, EPI == EPI_RESADD>(a, nxt, next < a.M ? next : base, RPW, rr, ll, LPR,
-                                                        uvalid, units, G);
+        load_step<BITS, NMAT, R, NV, EPI == EPI_RESADD>(a, nxt, next < a.M ? next : base, RPW, rr, lu,
+                                                        units, G);
 
         float acc[NMAT][R];
 #pragma unroll
@@ -876,26 +894,24 @@ constexpr int LUT_MAX_NV = 3;
 // Weight words a lane holds for one row-step; the host keeps it <= 32.
 constexpr int step_words(int BITS, int NMAT, int NV, int R) { return NMAT * R * NV * (BITS == 1 ? 1 : 4); }
 
-template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH, int NV, bool LUT>
+template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH, int NV, bool LUT, bool FULL>
 void launch_r(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks) {
     dim3 grid(blocks), block(256);
+#define QK(RR) qmv_kernel<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, RR, LUT, FULL><<<grid, block, 0, ctx->stream>>>(a)
     if (R == 8) {
         // long matrices only (the 1-bit LM head): more rows in flight per wave
-        if constexpr (LUT && step_words(BITS, NMAT, NV, 8) <= 32)
-            qmv_kernel<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, 8, LUT><<<grid, block, 0, ctx->stream>>>(a);
+        if constexpr (LUT && step_words(BITS, NMAT, NV, 8) <= 32) QK(8);
         else R = 4;
     }
     if (R == 4) {
-        if constexpr (step_words(BITS, NMAT, NV, 4) <= 32)
-            qmv_kernel<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, 4, LUT><<<grid, block, 0, ctx->stream>>>(a);
+        if constexpr (step_words(BITS, NMAT, NV, 4) <= 32) QK(4);
         else R = 1;
     } else if (R == 2) {
-        if constexpr (step_words(BITS, NMAT, NV, 2) <= 32)
-            qmv_kernel<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, 2, LUT><<<grid, block, 0, ctx->stream>>>(a);
+        if constexpr (step_words(BITS, NMAT, NV, 2) <= 32) QK(2);
         else R = 1;
     }
-    if (R == 1)
-        qmv_kernel<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, 1, LUT><<<grid, block, 0, ctx->stream>>>(a);
+    if (R == 1) QK(1);
+#undef QK
 }
 
 template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH, int NV>
@@ -904,11 +920,16 @@ int launch_nv(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks, bool lut) 
         // the merge prologue keeps every chunk's partials in registers
         return nnz_fail(ctx, NNZ_EUNSUPPORTED, "merge_o_resadd: K > 4096");
     } else {
+        // rows narrower than a wave (K < 2048) occur only with one unit per lane
+        const bool full = a.lpr_log2 == 6;
         if constexpr (BITS == 1 && NV <= LUT_MAX_NV && XIN != XIN_MERGE) {
-            if (lut) launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, true>(ctx, a, R, blocks);
-            else launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false>(ctx, a, R, blocks);
-        } else {
-            launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false>(ctx, a, R, blocks);
+            if (lut) launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, true, true>(ctx, a, R, blocks);
+            else if (full) launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false, true>(ctx, a, R, blocks);
+            else if constexpr (NV == 1) launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false, false>(ctx, a, R, blocks);
+        } else if (full) {
+            launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false, true>(ctx, a, R, blocks);
+        } else if constexpr (NV == 1) {
+            launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false, false>(ctx, a, R, blocks);
         }
         NNZ_LAUNCHED(ctx);
         return NNZ_OK;

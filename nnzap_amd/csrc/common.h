@@ -138,6 +138,74 @@ __device__ __forceinline__ float wave_sum_to_last(float v) {
     return v;
 }
 
+// Totals of V = 1, 2, 4 or 8 per-lane partial sums, each summed over the
+// whole wave, by exchange-halving: v_permlane32_swap pairs the values two
+// at a time across the wave halves, v_permlane16_swap across 16-lane rows,
+// a row mirror across 8-lane halves, then DPP within 8 lanes -- log2(V)
+// swaps+adds per level instead of a full 64-lane reduction per value.
+// Returns, in every lane, the total of value slot(lane) =
+// bit-reverse (log2 V bits) of lane >> (6 - log2 V); lanes 0, 64/V, 2*64/V...
+// each hold a different slot.
+__device__ __forceinline__ float2 swap32(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(a), __float_as_int(b), false, false);
+    return make_float2(__int_as_float(r[0]), __int_as_float(r[1]));
+}
+__device__ __forceinline__ float2 swap16(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_int(a), __float_as_int(b), false, false);
+    return make_float2(__int_as_float(r[0]), __int_as_float(r[1]));
+}
+
+template <int V>
+__device__ __forceinline__ float multi_row_sum(const float (&v)[V]) {
+    static_assert(V == 1 || V == 2 || V == 4 || V == 8, "1, 2, 4 or 8 values");
+    const int lane = threadIdx.x & 63;
+    float c[V > 1 ? V / 2 : 1];
+    if constexpr (V == 1) {
+        const float2 p = swap32(v[0], v[0]);
+        c[0] = p.x + p.y;
+    } else {
+#pragma unroll
+        for (int k = 0; k < V / 2; ++k) {      // [slot 2k | slot 2k+1] by wave half
+            const float2 p = swap32(v[2 * k], v[2 * k + 1]);
+            c[k] = p.x + p.y;
+        }
+    }
+    constexpr int C = V > 1 ? V / 2 : 1;
+    float d[C > 1 ? C / 2 : 1];
+    if constexpr (C == 1) {
+        const float2 p = swap16(c[0], c[0]);
+        d[0] = p.x + p.y;
+    } else {
+#pragma unroll
+        for (int k = 0; k < C / 2; ++k) {      // 16-lane rows: slots 4k, 4k+2, 4k+1, 4k+3
+            const float2 p = swap16(c[2 * k], c[2 * k + 1]);
+            d[k] = p.x + p.y;
+        }
+    }
+    float e;
+    if constexpr (V == 8) {                    // 8-lane halves: d[0] low, d[1] high
+        const bool hi = lane & 8;
+        const float mine = hi ? d[1] : d[0], other = hi ? d[0] : d[1];
+        e = mine + dpp_move<DPP_ROW_MIRROR>(other, 0.f);
+    } else {
+        e = d[0] + dpp_move<DPP_ROW_MIRROR>(d[0], 0.f);
+    }
+    e += dpp_move<DPP_ROW_HALF_MIRROR>(e, 0.f);
+    e += dpp_move<DPP_XOR2>(e, 0.f);
+    e += dpp_move<DPP_XOR1>(e, 0.f);
+    return e;
+}
+
+// The slot multi_row_sum<V> leaves in this lane.
+template <int V>
+__device__ __forceinline__ int multi_row_slot() {
+    const int lane = threadIdx.x & 63;
+    if constexpr (V == 1) return 0;
+    else if constexpr (V == 2) return lane >> 5;
+    else if constexpr (V == 4) return ((lane >> 4) & 1) * 2 + (lane >> 5);
+    else return ((lane >> 3) & 1) * 4 + ((lane >> 4) & 1) * 2 + (lane >> 5);
+}
+
 __device__ __forceinline__ float lane63(float v) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }

@@ -705,27 +705,31 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
         int seg = 0;
         if constexpr (NMAT == 1) seg = step_segment(a, base, seg_start);
         void *out0 = NMAT == 1 ? (void *)seg_mat(a, seg).out : a.m0.out;
-        if (LPR == 64) {
-            // Each row's total by a DPP reduction (lands in lane 63, read
-            // back as a wave-uniform value); lane r then stores row base+r.
-            float rt[NMAT][R];
+        if constexpr (FULL) {
+            // The NMAT x R row totals in one exchange-halving reduction
+            // (slot r * NMAT + m); the lanes heading each slot's lane group
+            // store.  A pair's two totals of a row sit in lanes l and l ^ 32.
+            constexpr int V = NMAT * R;
+            float vals[V];
 #pragma unroll
-            for (int m = 0; m < NMAT; ++m)
+            for (int r = 0; r < R; ++r)
 #pragma unroll
-                for (int r = 0; r < R; ++r) rt[m][r] = lane63(wave_sum_to_last(acc[m][r]));
+                for (int m = 0; m < NMAT; ++m) vals[r * NMAT + m] = acc[m][r];
+            const float t = multi_row_sum<V>(vals);
+            const int slot = multi_row_slot<V>();
+            const int r = slot / NMAT;
             float tot[NMAT];
-#pragma unroll
-            for (int m = 0; m < NMAT; ++m) {
-                float t = rt[m][0];
-#pragma unroll
-                for (int k = 1; k < R; ++k) t = lane == k ? rt[m][k] : t;
-                tot[m] = t;
+            tot[0] = t;
+            if constexpr (NMAT == 2) {
+                const float2 p = swap32(t, t);   // the partner half's total
+                tot[1] = p.y;                    // lanes < 32 hold m = 0 and read m = 1
             }
             float prev = cur.res[0];
 #pragma unroll
-            for (int k = 1; k < R; ++k) prev = lane == k ? cur.res[k] : prev;
-            const uint32_t row = base + (uint32_t)lane;  // RPW == 1
-            if (lane < R && row < a.M)
+            for (int k = 1; k < R; ++k) prev = r == k ? cur.res[k] : prev;
+            const uint32_t row = base + (uint32_t)r;
+            const bool head = (lane & ((64 / V) - 1)) == 0 && (NMAT == 1 || lane < 32);
+            if (head && row < a.M)
                 qmv_epilogue<EPI, ODT, FAITH, NMAT>(a, out0, row, row - seg_start, tot, prev);
         } else {
 #pragma unroll
@@ -900,7 +904,7 @@ void launch_r(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks) {
 #define QK(RR) qmv_kernel<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, RR, LUT, FULL><<<grid, block, 0, ctx->stream>>>(a)
     if (R == 8) {
         // long matrices only (the 1-bit LM head): more rows in flight per wave
-        if constexpr (LUT && step_words(BITS, NMAT, NV, 8) <= 32) QK(8);
+        if constexpr (LUT && NMAT == 1 && step_words(BITS, NMAT, NV, 8) <= 32) QK(8);
         else R = 4;
     }
     if (R == 4) {

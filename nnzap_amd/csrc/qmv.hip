@@ -828,6 +828,7 @@ __global__ __launch_bounds__(64 * KS) void qmv1_splitk_kernel(QmvArgs a) {
         Step nxt;
         load(base + stride < M ? base + stride : base, nxt);
         const int buf = it & 1;
+        float pr[R];
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const uint32_t w = cur.cw[r];
@@ -838,9 +839,11 @@ __global__ __launch_bounds__(64 * KS) void qmv1_splitk_kernel(QmvArgs a) {
                 sb += __int_as_float(mask & __float_as_int(xr[i]));
             }
             const float sc = uv ? (float)__builtin_bit_cast(f16_t, cur.sc[r]) : 0.f;
-            const float p = lane63(wave_sum_to_last(sc * (2.f * sb - xsum)));
-            if (lane == 0) part[buf][kp][r] = p;
+            pr[r] = sc * (2.f * sb - xsum);
         }
+        // the R row partials of this wave in one exchange-halving reduction
+        const float p = multi_row_sum<R>(pr);
+        if ((lane & (64 / R - 1)) == 0) part[buf][kp][multi_row_slot<R>()] = p;
         __syncthreads();
         if (kp == 0 && lane < R) {
             float t = 0.f;

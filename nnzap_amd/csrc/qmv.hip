@@ -98,8 +98,7 @@ __device__ __forceinline__ int step_segment(const QmvArgs &a, uint32_t base, uin
     seg_start = 0;
     if (a.nseg > 1 && base >= a.m0.seg_end) { seg = 1; seg_start = a.m0.seg_end; }
     if (a.nseg > 2 && base >= a.m1.seg_end) { seg = 2; seg_start = a.m1.seg_end; }
-    seg_start = __builtin_amdgcn_readfirstlane(seg_start);
-    return __builtin_amdgcn_readfirstlane(seg);
+    return seg;   // uniform: a.nseg, the segment ends and `base` are
 }
 
 // Matrix `m` of a pair (compile-time index).
@@ -162,7 +161,7 @@ __device__ __forceinline__ SegPtrs seg_mat(const QmvArgs &a, int seg) {
 template <int NV>
 struct LaneUnits {
     uint32_t uoff[NV];   // units (32-column pieces) from the row start
-    uint32_t ugrp[NV];   // scale groups from the row start
+    uint32_t ugrp[NV];   // byte offset of the unit's scale (and bias) from the row's first
     bool ok[NV];         // the unit exists
 };
 
@@ -224,13 +223,88 @@ __device__ __forceinline__ void load_step(const QmvArgs &a, StepRegs<NMAT, R, NV
                     s.cw[m][r][j][0] = q.x; s.cw[m][r][j][1] = q.y;
                     s.cw[m][r][j][2] = q.z; s.cw[m][r][j][3] = q.w;
                 }
-                if constexpr (R == 8) s.sc[m][r][j] = __builtin_nontemporal_load(&scales[lu.ugrp[j]]);
-                else s.sc[m][r][j] = scales[lu.ugrp[j]];
-                if constexpr (BITS == 4) s.bi[m][r][j] = biases[lu.ugrp[j]];
+                // 32-bit byte offsets: scalar base + vector offset addressing
+                const gptr<const uint16_t> sj = (gptr<const uint16_t>)((gptr<const char>)scales + lu.ugrp[j]);
+                if constexpr (R == 8) s.sc[m][r][j] = __builtin_nontemporal_load(sj);
+                else s.sc[m][r][j] = *sj;
+                if constexpr (BITS == 4)
+                    s.bi[m][r][j] = *(gptr<const uint16_t>)((gptr<const char>)biases + lu.ugrp[j]);
                 s.ok[m][r][j] = rv && lu.ok[j];
             }
         }
     }
+}
+
+// Whole-wave rows (FULL): per-lane byte offsets of row r's unit j from the
+// first row of a step, fixed for the whole kernel, so a step's loads need
+// one scalar base per matrix and no per-row address arithmetic.
+template <int R, int NV>
+struct FullOffsets {
+    uint32_t code[R][NV];    // codes
+    uint32_t scale[R][NV];   // scales and biases
+    uint32_t res;            // the residual of this lane's output row
+};
+
+// Raw buffer resource over a weight array: stride 0, no range limit (the
+// offsets below are in bounds by construction), gfx9 dword3 (32-bit data
+// format).  A load through it adds a 32-bit scalar offset (the step's first
+// row) to a 32-bit per-lane offset (fixed for the kernel): no 64-bit
+// address arithmetic per row or per step.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t weight_rsrc(const void *p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, (int)0xFFFFFFFF, 0x00020000);
+}
+
+// Loads of one step of R consecutive whole-wave rows starting at `rb`
+// (wave-uniform, rb + R <= M: the caller clamps the last step back onto
+// valid rows instead of clamping each row).
+template <int BITS, int NMAT, int R, int NV, bool RES>
+__device__ __forceinline__ void load_step_full(const QmvArgs &a, StepRegs<NMAT, R, NV, (BITS == 1 ? 1 : 4)> &s,
+                                               uint32_t rb, const FullOffsets<R, NV> &fo,
+                                               uint32_t words_per_row, uint32_t G) {
+    // R == 8 is chosen only for vocabulary-sized matrices (the LM head), read
+    // once per token: non-temporal loads keep them from evicting the layer
+    // weights and the KV cache
+    constexpr int AUX = (R == 8) ? 2 : 0;
+    __amdgpu_buffer_rsrc_t cr[NMAT], sr[NMAT], br[NMAT];
+    uint32_t seg_start = 0;
+    if constexpr (NMAT == 1) {
+        // plain selects of the argument values (already scalar): no
+        // per-step moves of the pointers through vector registers
+        const int seg = step_segment(a, rb, seg_start);
+        auto sel = [&](const void *p0, const void *p1, const void *p2) {
+            return seg == 0 ? p0 : (seg == 1 ? p1 : p2);
+        };
+        cr[0] = weight_rsrc(sel(a.m0.codes, a.m1.codes, a.m2.codes));
+        sr[0] = weight_rsrc(sel(a.m0.scales, a.m1.scales, a.m2.scales));
+        br[0] = weight_rsrc(sel(a.m0.biases, a.m1.biases, a.m2.biases));
+    } else {
+        cr[0] = weight_rsrc(a.m0.codes); sr[0] = weight_rsrc(a.m0.scales); br[0] = weight_rsrc(a.m0.biases);
+        cr[NMAT - 1] = weight_rsrc(mat_of<NMAT - 1>(a).codes);
+        sr[NMAT - 1] = weight_rsrc(mat_of<NMAT - 1>(a).scales);
+        br[NMAT - 1] = weight_rsrc(mat_of<NMAT - 1>(a).biases);
+    }
+    const uint32_t lr = rb - seg_start;
+    const uint32_t co = lr * words_per_row * 4u, so = lr * G * 2u;
+    if constexpr (RES) {
+        static_assert(NMAT == 1, "residual add has one matrix");
+        s.res[0] = *(gptr<const float>)((gptr<const char>)uniform_ptr(a.m0.out) + (size_t)rb * 4u + fo.res);
+    }
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                if constexpr (BITS == 1) {
+                    s.cw[m][r][j][0] = __builtin_amdgcn_raw_buffer_load_b32(cr[m], fo.code[r][j], co, AUX);
+                } else {
+                    const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(cr[m], fo.code[r][j], co, AUX);
+                    s.cw[m][r][j][0] = q.x; s.cw[m][r][j][1] = q.y;
+                    s.cw[m][r][j][2] = q.z; s.cw[m][r][j][3] = q.w;
+                    s.bi[m][r][j] = __builtin_amdgcn_raw_buffer_load_b16(br[m], fo.scale[r][j], so, AUX);
+                }
+                s.sc[m][r][j] = __builtin_amdgcn_raw_buffer_load_b16(sr[m], fo.scale[r][j], so, AUX);
+            }
 }
 
 // Store / residual-add / SiLU epilogue of one row.  `row` indexes the pair
@@ -290,7 +364,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
         uvalid[j] = (uint32_t)ll + (uint32_t)(LPR * j) < units;
         lu.ok[j] = uvalid[j];
         lu.uoff[j] = uvalid[j] ? (uint32_t)ll + (uint32_t)(LPR * j) : 0u;
-        lu.ugrp[j] = (lu.uoff[j] * 32u) / a.gs;
+        lu.ugrp[j] = (lu.uoff[j] * 32u) / a.gs * 2u;
     }
 
     const uint32_t wave = __builtin_amdgcn_readfirstlane(blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6));
@@ -307,9 +381,32 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
     // at its join cover every load issued before it): past the end, a step
     // re-reads rows that are valid, and their values go unused.
     StepRegs<NMAT, R, NV, VEC> cur;
+    // FULL: a step reads rows [rb, rb + R) with rb = min(base, M - R) (the
+    // host keeps M >= R), so every load is in bounds and the last step's
+    // rows below `base` are computed but not stored.
+    FullOffsets<R, NV> fo;
+    if constexpr (FULL) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                fo.code[r][j] = ((uint32_t)r * units * VEC + lu.uoff[j] * VEC) * 4u;
+                fo.scale[r][j] = (uint32_t)r * G * 2u + lu.ugrp[j];
+            }
+        fo.res = (uint32_t)(multi_row_slot<NMAT * R>() / NMAT) * 4u;
+    }
+    auto step_base = [&](uint32_t b) { return b < a.M - (uint32_t)R ? b : a.M - (uint32_t)R; };
+    auto load_rows = [&](StepRegs<NMAT, R, NV, VEC> &dst, uint32_t b) {
+        if constexpr (FULL)
+            load_step_full<BITS, NMAT, R, NV, EPI == EPI_RESADD>(a, dst, step_base(b), fo, units * VEC, G);
+        else
+            load_step<BITS, NMAT, R, NV, EPI == EPI_RESADD>(a, dst, b < a.M ? b : 0u, RPW, rr, lu, units, G);
+    };
     auto first_weights = [&]() {
-        load_step<BITS, NMAT, R, NV, EPI == EPI_RESADD>(a, cur, base < a.M ? base : 0u, RPW, rr, lu,
-                                                        units, G);
+        // the prologue's own loads go out first (nothing of the weight
+        // addressing may be scheduled ahead of them)
+        __builtin_amdgcn_sched_barrier(0);
+        load_rows(cur, base);
     };
 
     // ---- 1-bit signed nibble tables (LUT, full-wave rows only) --------------
@@ -499,7 +596,16 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
         const MergeIn &mg = a.mg;
         const uint32_t D = mg.head_dim;
         const uint32_t heads = K / D;
-        const uint32_t seq = mg.d_seq ? *mg.d_seq : mg.seq_len;
+        // The device sequence length as a vector load issued ahead of the
+        // partials' loads, without a branch: a null d_seq gets an empty range,
+        // so the load returns 0 without touching memory and seq_len is used.
+        // (A scalar load here is hoisted above the vector loads with its wait,
+        // and a flat load's completion is not ordered with them.)
+        const uint32_t seq_dev = __builtin_amdgcn_raw_buffer_load_b32(
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(mg.d_seq), (short)0,
+                                              mg.d_seq ? 4 : 0, 0x00020000),
+            0, 0, 0);
+
         // (m, l) of this thread's (head, chunk) pairs p = tid + 256 i, then
         // the partial outputs, then the weights
         constexpr int PI = 2 * NV;   // heads x 16 <= 512 NV pairs
@@ -529,6 +635,11 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
             }
         }
         first_weights();
+        // the length is used from here on only (an empty asm pins the point:
+        // hoisted above the loads, its wait would be theirs too)
+        uint32_t seq_v = seq_dev;
+        asm volatile("" : "+v"(seq_v));
+        const uint32_t seq = mg.d_seq ? __builtin_amdgcn_readfirstlane(seq_v) : mg.seq_len;
         const uint32_t nch = min(mg.nchunks, ceil_div(seq, mg.chunk));
 #pragma unroll
         for (int i = 0; i < PI; ++i) {
@@ -645,11 +756,18 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
     }
 
     // ---- software-pipelined row loop ---------------------------------------
-    for (; base < a.M; base += nwaves * rows_per_iter) {
-        const uint32_t next = base + nwaves * rows_per_iter;
-        StepRegs<NMAT, R, NV, VEC> nxt;
-        load_step<BITS, NMAT, R, NV, EPI == EPI_RESADD>(a, nxt, next < a.M ? next : base, RPW, rr, lu,
-                                                        units, G);
+    // Two register sets used alternately (the loop body appears twice), so
+    // the next step's weights land in the set not being read and nothing is
+    // copied at the back edge.
+    const uint32_t stride = nwaves * rows_per_iter;
+    // nibble-table addresses: byte 0 = lane * 4, byte 1 = the nibble (the
+    // table of one (unit, nibble) pair is 16 entries x 64 lanes x 4 bytes)
+    const uint32_t lane4 = (uint32_t)lane * 4u;
+    auto row_step = [&](StepRegs<NMAT, R, NV, VEC> &c, StepRegs<NMAT, R, NV, VEC> &n) {
+        // Past the last step a wave re-reads its own rows (cache hits): the
+        // clamped rows [M - R, M) would be one hot spot for every wave.
+        const uint32_t next = base + stride;
+        load_rows(n, next < a.M ? next : base);
 
         float acc[NMAT][R];
 #pragma unroll
@@ -659,16 +777,30 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                 float accv = 0.f;
 #pragma unroll
                 for (int j = 0; j < NV; ++j) {
-                    const float s = cur.ok[m][r][j] ? scale_to_f32(cur.sc[m][r][j], (int)a.sdt) : 0.f;
                     if constexpr (BITS == 1 && LUT) {
-                        const uint32_t w = cur.cw[m][r][j][0];
-                        const float *tb = lut + (j * 8 * 16) * 64 + lane;
-                        float sb = 0.f;
+                        // A unit past the row end has all-zero tables, and a
+                        // row past M is never stored: no validity select.
+                        // Q1 scales are f16.
+                        const float s = (float)__builtin_bit_cast(f16_t, c.sc[m][r][j]);
+                        const uint32_t w = c.cw[m][r][j][0];
+                        const uint32_t wl = w & 0x0F0F0F0Fu, wh = (w >> 4) & 0x0F0F0F0Fu;
+                        const char *tb = (const char *)(lut + (j * 8 * 16) * 64);
+                        float t[8];
 #pragma unroll
-                        for (int n = 0; n < 8; ++n) sb += tb[(n * 16 + ((w >> (4 * n)) & 15u)) * 64];
+                        for (int n = 0; n < 8; ++n) {
+                            // nibble n is byte n/2 of wl (n even) or wh (n odd)
+                            const uint32_t sel = 0x0C0C0000u | ((4u + (uint32_t)(n >> 1)) << 8);
+                            const uint32_t off = __builtin_amdgcn_perm((n & 1) ? wh : wl, lane4, sel);
+                            t[n] = *(const float *)(tb + n * 16 * 64 * 4 + off);
+                        }
+                        float sb = t[0];
+#pragma unroll
+                        for (int n = 1; n < 8; ++n) sb += t[n];
                         accv = fmaf(s, sb, accv);
                     } else if constexpr (BITS == 1) {
-                        const uint32_t w = cur.cw[m][r][j][0];
+                        const bool ok = FULL ? lu.ok[j] : c.ok[m][r][j];
+                        const float s = ok ? (float)__builtin_bit_cast(f16_t, c.sc[m][r][j]) : 0.f;
+                        const uint32_t w = c.cw[m][r][j][0];
                         float sb = 0.f;
 #pragma unroll
                         for (int i = 0; i < 32; ++i) {
@@ -677,10 +809,12 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                         }
                         accv = fmaf(s, 2.f * sb - xsum[j], accv);
                     } else {
+                        const bool ok = FULL ? lu.ok[j] : c.ok[m][r][j];
+                        const float s = ok ? scale_to_f32(c.sc[m][r][j], (int)a.sdt) : 0.f;
                         float nd = 0.f;
 #pragma unroll
                         for (int k = 0; k < 4; ++k) {
-                            const uint32_t w = cur.cw[m][r][j][k];
+                            const uint32_t w = c.cw[m][r][j][k];
                             const uint32_t lo = w & 0x0F0F0F0Fu;
                             const uint32_t hi = (w >> 4) & 0x0F0F0F0Fu;
                             nd = fmaf((float)(lo & 0xFFu), xr[j][8 * k + 0], nd);
@@ -692,7 +826,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                             nd = fmaf((float)(lo >> 24), xr[j][8 * k + 6], nd);
                             nd = fmaf((float)(hi >> 24), xr[j][8 * k + 7], nd);
                         }
-                        const float b = cur.ok[m][r][j] ? scale_to_f32(cur.bi[m][r][j], (int)a.sdt) : 0.f;
+                        const float b = ok ? scale_to_f32(c.bi[m][r][j], (int)a.sdt) : 0.f;
                         accv = fmaf(s, nd, fmaf(b, xsum[j], accv));
                     }
                 }
@@ -701,10 +835,11 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
 
         // Row sums: DPP reductions for full-wave rows, lane-group
         // shuffles for narrow ones.
+        const uint32_t rb = FULL ? step_base(base) : base;
         uint32_t seg_start = 0;
         int seg = 0;
-        if constexpr (NMAT == 1) seg = step_segment(a, base, seg_start);
-        void *out0 = NMAT == 1 ? (void *)seg_mat(a, seg).out : a.m0.out;
+        if constexpr (NMAT == 1) seg = step_segment(a, rb, seg_start);
+        void *out0 = NMAT == 1 ? (seg == 0 ? a.m0.out : (seg == 1 ? a.m1.out : a.m2.out)) : a.m0.out;
         if constexpr (FULL) {
             // The NMAT x R row totals in one exchange-halving reduction
             // (slot r * NMAT + m); the lanes heading each slot's lane group
@@ -724,13 +859,10 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                 const float2 p = swap32(t, t);   // the partner half's total
                 tot[1] = p.y;                    // lanes < 32 hold m = 0 and read m = 1
             }
-            float prev = cur.res[0];
-#pragma unroll
-            for (int k = 1; k < R; ++k) prev = r == k ? cur.res[k] : prev;
-            const uint32_t row = base + (uint32_t)r;
+            const uint32_t row = rb + (uint32_t)r;   // < M
             const bool head = (lane & ((64 / V) - 1)) == 0 && (NMAT == 1 || lane < 32);
-            if (head && row < a.M)
-                qmv_epilogue<EPI, ODT, FAITH, NMAT>(a, out0, row, row - seg_start, tot, prev);
+            if (head && row >= base)
+                qmv_epilogue<EPI, ODT, FAITH, NMAT>(a, out0, row, row - seg_start, tot, c.res[0]);
         } else {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
@@ -739,10 +871,17 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                 for (int m = 0; m < NMAT; ++m) tot[m] = group_sum(acc[m][r], LPR);
                 const uint32_t row = base + (uint32_t)(r * RPW + rr);
                 if (ll == 0 && row < a.M)
-                    qmv_epilogue<EPI, ODT, FAITH, NMAT>(a, out0, row, row - seg_start, tot, cur.res[r]);
+                    qmv_epilogue<EPI, ODT, FAITH, NMAT>(a, out0, row, row - seg_start, tot, c.res[r]);
             }
         }
-        cur = nxt;
+    };
+    StepRegs<NMAT, R, NV, VEC> nxt;
+    while (base < a.M) {
+        row_step(cur, nxt);
+        base += stride;
+        if (base >= a.M) break;
+        row_step(nxt, cur);
+        base += stride;
     }
 }
 
@@ -966,6 +1105,7 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
         total += rows;
     }
     if (NMAT == 1) NNZ_REQUIRE(ctx, total == d.M, NNZ_EINVAL, "%s: segments do not add up to M", name);
+    NNZ_REQUIRE(ctx, EPI != EPI_RESADD || nw == 1, NNZ_EINVAL, "%s: residual add takes one matrix", name);
     if (MERGE) {
         NNZ_REQUIRE(ctx, merge && merge->part_o && merge->part_ml, NNZ_EINVAL, "%s: null partials", name);
         NNZ_REQUIRE(ctx, merge->nchunks >= 1 && merge->nchunks <= (uint32_t)MERGE_MAX_CHUNKS &&
@@ -1034,8 +1174,7 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
     while (R > 1 && (ceil_div(d.M, 4u * R * rpw) < min_blocks || NMAT * R * (int)nv * vec > 32)) R >>= 1;
     // 1-bit full-wave rows may use the nibble tables.  Building them is a
     // fixed cost per block that pays off from about four matrix rows per
-    // wave: pairs take two rows per wave; single matrices only when the
-    // grid cap below leaves each wave many rows.
+    // wave: pairs take two rows per wave.
     bool lut = BITS == 1 && lpr == 64 && nv <= (uint32_t)LUT_MAX_NV;
     if (lut && NMAT == 2 && R < 2 && 2 * 2 * (int)nv * vec <= 32) R = 2;
     if (lut && NMAT == 1 && d.M >= 4u * 2048u * 8u) R = 8;   // e.g. a vocabulary-sized LM head
@@ -1060,9 +1199,15 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
         while (R < 4 && NMAT * 2 * R * (int)nv * vec <= 32 && ceil_div(d.M, 4u * R * rpw) > 256) R <<= 1;
         blocks = ceil_div(d.M, 4u * R * rpw);
     }
-    // measured: tables pay off from 4 row-units per wave for pairs, from 8
-    // rows per wave for single matrices
-    if (lut && ceil_div(d.M, blocks * 4u) * NMAT < (NMAT == 2 ? 4u : 8u)) lut = false;
+    if (lpr == 64 && d.M < (uint32_t)R) {
+        // whole-wave rows: a step's R rows must exist (the last step is
+        // clamped back onto rows [M - R, M))
+        while (R > 1 && d.M < (uint32_t)R) R >>= 1;
+        blocks = ceil_div(d.M, 4u * R * rpw);
+    }
+    // measured: tables pay off from 4 row-units per wave (fused Q/K/V, 4
+    // rows per wave: 3.55 us without, 3.16 us with)
+    if (lut && ceil_div(d.M, blocks * 4u) * NMAT < 4u) lut = false;
 
     QmvArgs a{};
     for (int i = 0; i < nw; ++i) {

@@ -196,6 +196,47 @@ __device__ __forceinline__ float multi_row_sum(const float (&v)[V]) {
     return e;
 }
 
+// Totals over each aligned group of L = 8 or 16 lanes (half or whole DPP
+// row) of V per-lane values, by exchange-halving inside the group: at each
+// level a lane keeps one half of its values and adds its partner's copy of
+// that half (the row mirror pairs the 8-lane halves for L = 16, then the
+// half-row mirror, xor 2, xor 1; once one value is left the levels are
+// plain pairwise sums).  Afterwards lane l (its index within the group)
+// holds in a[0..N) the totals of values prefix * N + j, N = max(V / L, 1),
+// prefix = the top log2(V / N) bits of l; with V < L the lanes sharing a
+// prefix hold the same totals.
+template <int CTRL, int N>
+__device__ __forceinline__ void halving_level(float *a, bool upper) {
+    if constexpr (N >= 2) {
+#pragma unroll
+        for (int k = 0; k < N / 2; ++k) {
+            const float keep = upper ? a[k + N / 2] : a[k];
+            const float send = upper ? a[k] : a[k + N / 2];
+            a[k] = keep + dpp_move<CTRL>(send, 0.f);
+        }
+    } else {
+        a[0] += dpp_move<CTRL>(a[0], 0.f);
+    }
+}
+
+template <int V, int L>
+__device__ __forceinline__ void group_multi_sum(float (&a)[V]) {
+    static_assert(L == 8 || L == 16, "8 or 16 lanes");
+    static_assert(V >= 1 && (V & (V - 1)) == 0, "a power of two of values");
+    constexpr int N0 = V, N1 = N0 > 1 ? N0 / 2 : 1, N2 = N1 > 1 ? N1 / 2 : 1, N3 = N2 > 1 ? N2 / 2 : 1;
+    const int l = threadIdx.x & (L - 1);
+    if constexpr (L == 16) {
+        halving_level<DPP_ROW_MIRROR, N0>(a, l & 8);
+        halving_level<DPP_ROW_HALF_MIRROR, N1>(a, l & 4);
+        halving_level<DPP_XOR2, N2>(a, l & 2);
+        halving_level<DPP_XOR1, N3>(a, l & 1);
+    } else {
+        halving_level<DPP_ROW_HALF_MIRROR, N0>(a, l & 4);
+        halving_level<DPP_XOR2, N1>(a, l & 2);
+        halving_level<DPP_XOR1, N2>(a, l & 1);
+    }
+}
+
 // The slot multi_row_sum<V> leaves in this lane.
 template <int V>
 __device__ __forceinline__ int multi_row_slot() {

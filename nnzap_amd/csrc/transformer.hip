@@ -337,6 +337,9 @@ struct AttnArgs {
 };
 
 constexpr int ATT_MAX_CHUNK = 512;
+#ifndef ATTN_STREAM_OFF
+#define ATTN_STREAM_OFF 0
+#endif
 #ifndef NNZ_DEC_TARGET_BLOCKS
 #define NNZ_DEC_TARGET_BLOCKS 1024u
 #endif
@@ -552,16 +555,18 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
 // and masked by selection (never multiplied), so stale partials cannot
 // leak in.  part_o rows are 16-byte aligned (checked by the launcher); the
 // launcher picks PRE to cover the chunk count (launch_combine).
-template <int D, int PRE>
+template <int D, int PRE, int DS>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
-    constexpr int NV = D / 4, PARTS = 256 / NV;
+    // DS blocks per query head, block ds taking dims [ds D / DS, (ds + 1) D / DS)
+    // (every one of them folds the chunks' (m, l) pairs itself)
+    constexpr int NV = D / 4 / DS, PARTS = 256 / NV;
     __shared__ float red[4];
     __shared__ float4 acc[256];
-    const uint32_t qh = blockIdx.x, z = blockIdx.y, tid = threadIdx.x;
+    const uint32_t qh = blockIdx.x, z = blockIdx.y / DS, ds = blockIdx.y % DS, tid = threadIdx.x;
     const uint32_t dv = tid % NV, p = tid / NV;
     const size_t base = ((size_t)z * a.hq + qh) * a.nchunks;
     const float2 *ml = (const float2 *)(a.part_ml + base * 2);
-    const float4 *po = (const float4 *)(a.part_o + base * D) + dv;
+    const float4 *po = (const float4 *)(a.part_o + base * D) + ds * NV + dv;
     const uint32_t last = a.nchunks - 1;
     const float2 mine = ml[min(tid, last)];
     float2 mlk[PRE];
@@ -570,7 +575,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     for (int k = 0; k < PRE; ++k) {
         const uint32_t c = min(p + (uint32_t)(PARTS * k), last);
         mlk[k] = ml[c];
-        ok[k] = po[(size_t)c * NV];
+        ok[k] = po[(size_t)c * (D / 4)];
     }
     const uint32_t seq = (a.d_seq ? *a.d_seq : a.seq_len) + z;
     const uint32_t nch = min(a.nchunks, ceil_div(seq, a.chunk));
@@ -598,7 +603,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 #pragma unroll 4
     for (uint32_t c = p + PARTS * PRE; c < nch; c += PARTS) {
         const float w = expf(ml[c].x - M);
-        const float4 o = po[(size_t)c * NV];
+        const float4 o = po[(size_t)c * (D / 4)];
         s.x = fmaf(w, o.x, s.x);
         s.y = fmaf(w, o.y, s.y);
         s.z = fmaf(w, o.z, s.z);
@@ -615,7 +620,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
             s.z += o.z;
             s.w += o.w;
         }
-        const size_t ob = (size_t)z * a.o_stride + (size_t)qh * D + 4 * tid;
+        const size_t ob = (size_t)z * a.o_stride + (size_t)qh * D + 4 * (ds * NV + tid);
         store_dt(a.out, ob + 0, s.x / den, a.odt);
         store_dt(a.out, ob + 1, s.y / den, a.odt);
         store_dt(a.out, ob + 2, s.z / den, a.odt);
@@ -983,14 +988,14 @@ struct DecAttnArgs {
 template <int D, int G, int KVDT, bool VT>
 __global__ __launch_bounds__(256) void attn_decode_kernel(DecAttnArgs a) {
     constexpr int NQ = (G * D + 255) / 256;
-    constexpr int TPT = 256 / FCHUNK;            // lanes per token (scores)
-    constexpr int KV4 = D / 8 / TPT;             // K: 16-byte vectors per lane
     constexpr int PARTS = 256 / D;               // VT: token parts per d
     constexpr int VTOK = FCHUNK / PARTS;         // VT: tokens per thread
-    constexpr int DP = D / 8, TG = 256 / DP;     // !VT: lanes per row, token groups
+    constexpr int DP = D / 8, TG = 256 / DP;     // lanes per K/V row, token groups
+    constexpr int KT = FCHUNK / TG;              // K: tokens (16-byte pieces) per lane
     constexpr int VV4 = VT ? VTOK / 8 : FCHUNK / TG;
     constexpr int NRED = VT ? PARTS : 4;
-    static_assert(KV4 >= 1 && VV4 >= 1 && TPT <= 4 && FCHUNK == 64, "chunk/head_dim");
+    constexpr bool QREG = G <= 2;                // this lane's q slice in registers
+    static_assert(KT >= 1 && VV4 >= 1 && (DP == 8 || DP == 16) && FCHUNK == 64, "chunk/head_dim");
     __shared__ float qs[G][D];
     __shared__ float ps[G][FCHUNK];
     __shared__ float pe[G][FCHUNK];
@@ -1016,16 +1021,20 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecAttnArgs a) {
 
     const size_t kv_stride = (size_t)a.max_ctx * D;
     const uint16_t *kb = a.kc + h * kv_stride, *vb = a.vc + h * kv_stride;
-    const int kt = tid / TPT, ksub = tid % TPT;
     const int vd = tid % D, vpart = tid / D;      // VT roles
-    const int dp = tid % DP, tg = tid / DP;       // !VT roles
+    const int dp = tid % DP, tg = tid / DP;       // K (and !VT V) roles
     // Loads of sub-chunk s (s < ns): tokens past the end read an in-range
-    // token (K: the last one; V: group 0 or the last row) and are masked.
-    auto load = [&](uint4 (&kr)[KV4], uint4 (&vr)[VV4], uint32_t s) {
+    // token (the last one, or V group 0) and are masked.  K and the
+    // row-major V: lane (dp, tg) reads the 16 bytes at dims 8 dp.. of tokens
+    // v TG + tg, so one wave instruction reads 64 / DP whole consecutive rows
+    // (1 KB at D = 128).
+    auto load = [&](uint4 (&kr)[KT], uint4 (&vr)[VV4], uint32_t s) {
         const uint32_t t0 = c0 + s * FCHUNK, len = min((uint32_t)FCHUNK, seq - t0);
-        const uint4 *kp = (const uint4 *)(kb + (size_t)(t0 + min((uint32_t)kt, len - 1)) * D) + ksub * KV4;
 #pragma unroll
-        for (int v = 0; v < KV4; ++v) kr[v] = kp[v];
+        for (int v = 0; v < KT; ++v) {
+            const uint32_t t = min((uint32_t)(v * TG + tg), len - 1);
+            kr[v] = *((const uint4 *)(kb + (size_t)(t0 + t) * D) + dp);
+        }
         if constexpr (VT) {
             const uint16_t *row = vb + (size_t)vd * a.max_ctx + t0;
 #pragma unroll
@@ -1041,7 +1050,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecAttnArgs a) {
             }
         }
     };
-    uint4 kA[KV4], vA[VV4], kB[KV4], vB[VV4];
+    uint4 kA[KT], vA[VV4], kB[KT], vB[VV4];
     load(kA, vA, 0);
 
     // q (optionally RoPE-rotated at rope_pos) -> LDS
@@ -1057,6 +1066,13 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecAttnArgs a) {
     }
     __syncthreads();
 
+    float qr[QREG ? G : 1][8];   // q at this lane's 8 dims (G <= 2)
+    if constexpr (QREG) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) qr[g][i] = qs[g][dp * 8 + i];
+    }
     float m_run[G], l_run[G];
     float o[G][VT ? 1 : 8];
 #pragma unroll
@@ -1069,32 +1085,42 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecAttnArgs a) {
 
     // One sub-chunk from (kr, vr); the caller has already issued the next
     // sub-chunk's loads into the other register set.
-    auto compute = [&](const uint4 (&kr)[KV4], const uint4 (&vr)[VV4], uint32_t s) {
+    auto compute = [&](const uint4 (&kr)[KT], const uint4 (&vr)[VV4], uint32_t s) {
         const uint32_t t0 = c0 + s * FCHUNK, len = min((uint32_t)FCHUNK, seq - t0);
         {
-            float dot[G];
+            // partial q.k over this lane's 8 dims for its KT tokens, value
+            // v G + g; then the totals over the DP lanes of each row
+            constexpr int NV = KT * G;
+            float dot[NV];
 #pragma unroll
-            for (int g = 0; g < G; ++g) dot[g] = 0.f;
+            for (int i = 0; i < NV; ++i) dot[i] = 0.f;
 #pragma unroll
-            for (int v = 0; v < KV4; ++v) {
+            for (int v = 0; v < KT; ++v) {
                 const uint32_t wv[4] = {kr[v].x, kr[v].y, kr[v].z, kr[v].w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int d = (ksub * KV4 + v) * 8 + 2 * e;
                     float k0, k1;
                     unpack2<KVDT>(wv[e], k0, k1);
 #pragma unroll
-                    for (int g = 0; g < G; ++g) dot[g] = fmaf(qs[g][d + 1], k1, fmaf(qs[g][d], k0, dot[g]));
+                    for (int g = 0; g < G; ++g) {
+                        const float q0 = QREG ? qr[QREG ? g : 0][2 * e] : qs[g][dp * 8 + 2 * e];
+                        const float q1 = QREG ? qr[QREG ? g : 0][2 * e + 1] : qs[g][dp * 8 + 2 * e + 1];
+                        dot[v * G + g] = fmaf(q1, k1, fmaf(q0, k0, dot[v * G + g]));
+                    }
                 }
             }
+            group_multi_sum<NV, DP>(dot);
+            constexpr int NF = NV >= DP ? NV / DP : 1;          // totals per lane
+            constexpr int LB = DP == 16 ? 4 : 3;
+            constexpr int H = NV >= DP ? LB : (NV == 1 ? 0 : (NV == 2 ? 1 : (NV == 4 ? 2 : 3)));
+            const int prefix = dp >> (LB - H);
+            if ((dp & ((DP >> H) - 1)) == 0) {
 #pragma unroll
-            for (int g = 0; g < G; ++g) {
-                if constexpr (TPT >= 2) dot[g] += dpp_move<DPP_XOR1>(dot[g], 0.f);
-                if constexpr (TPT >= 4) dot[g] += dpp_move<DPP_XOR2>(dot[g], 0.f);
-            }
-            if (ksub == 0) {
-#pragma unroll
-                for (int g = 0; g < G; ++g) ps[g][kt] = (uint32_t)kt < len ? dot[g] * a.scale : -INFINITY;
+                for (int jj = 0; jj < NF; ++jj) {
+                    const int k = prefix * NF + jj, v = k / G, g = k % G;
+                    const uint32_t t = (uint32_t)(v * TG + tg);
+                    ps[g][t] = t < len ? dot[jj] * a.scale : -INFINITY;
+                }
             }
         }
         __syncthreads();
@@ -1198,6 +1224,274 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecAttnArgs a) {
             if (d == 0) {
                 a.part_ml[slot * 2] = m_run[g];
                 a.part_ml[slot * 2 + 1] = l_run[g];
+            }
+        }
+    }
+}
+
+// ------------------------------------ single-query attention, streaming --
+// The single-query attention of attn_decode_kernel for head_dim 128 and 1 or
+// 2 query heads per block, with every wave streaming its own tokens:
+//   * the block's chunk is cut into 16-token groups; wave w takes groups
+//     w, w + 4, ... and keeps its own online softmax (m, l, o), so the loop
+//     has no block barrier;
+//   * lane (row r = lane / 16, dp = lane % 16) reads the 16 bytes at dims
+//     8 dp.. of tokens 4 v + r (v < 4) of a group: each wave instruction
+//     reads 4 whole consecutive K (or row-major V) rows, 1 KB;
+//   * q.k over the lane's 8 dims, the totals over the 16 lanes of a row by
+//     exchange-halving; scores and probabilities go through a per-wave LDS
+//     row (one 16-lane row per head for the max and the sum);
+//   * P.V from registers (row-major V: the lane's 8 dims over its 4 tokens;
+//     V transposed: dims lane and lane + 64 over the group's 16 tokens);
+//   * the next group's loads are issued before the current one is used;
+//   * the 4 waves' (m, l, o) are merged once at the end: the output (one
+//     chunk) or the chunk's partials for attn_combine_kernel.
+template <int G, int KVDT, bool VT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))   // <= 128 VGPRs: 4 blocks per CU
+void attn_stream_kernel(DecAttnArgs a) {
+    constexpr int D = 128, DP = 16, KT = 4, TPI = 16, NR = VT ? 1 : 4;
+    static_assert(G == 1 || G == 2, "one or two query heads per block");
+    __shared__ float qs[G][D];
+    __shared__ float pw[4][G][TPI];
+    __shared__ float wml[4][G][2];
+    __shared__ float wo[4][NR][G][D];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int row = lane >> 4, dp = lane & 15;
+    const uint32_t bid = blockIdx.x, span = 8 * a.parts;
+    const uint32_t j = a.parts == 1 ? 0u : (bid % span) / 8;
+    const uint32_t u = a.parts == 1 ? bid : (bid / span) * 8 + bid % 8;
+    if (u >= a.units) return;
+    const uint32_t c = u % a.nchunks, h = u / a.nchunks, qb = h * a.gfull + j * G;
+    const uint32_t seq = a.d_seq ? *a.d_seq : a.seq_len;
+    const uint32_t c0 = c * a.sub * FCHUNK;
+    if (c0 >= seq) return;  // the combine step reads chunks < ceil(seq / chunk) only
+    const uint32_t cend = min(c0 + a.sub * FCHUNK, seq);
+    const uint32_t ngrp = ceil_div(cend - c0, (uint32_t)TPI);
+    const uint32_t nit = ngrp > (uint32_t)w ? ceil_div(ngrp - (uint32_t)w, 4u) : 0u;
+
+    float qv = 0.f;
+    if (tid < G * D) qv = load_dt(a.q, (size_t)qb * D + tid, a.qdt);
+
+    const size_t kv_stride = (size_t)a.max_ctx * D;
+    const uint16_t *kb = a.kc + h * kv_stride, *vb = a.vc + h * kv_stride;
+    // group of this wave's iteration i: past its last group it re-reads the
+    // last one (a wave without groups reads group 0), so loads stay in range
+    auto grp = [&](uint32_t i) -> uint32_t {
+        const uint32_t gi = (uint32_t)w + 4u * i;
+        return gi < ngrp ? gi : (nit ? (uint32_t)w + 4u * (nit - 1) : 0u);
+    };
+    auto load = [&](uint4 (&kr)[KT], uint4 (&vr)[4], uint32_t i) {
+        const uint32_t t0 = c0 + grp(i) * TPI, len = min((uint32_t)TPI, cend - t0);
+#pragma unroll
+        for (int v = 0; v < KT; ++v) {
+            const uint32_t t = min((uint32_t)(4 * v + row), len - 1);
+            kr[v] = *((const uint4 *)(kb + (size_t)(t0 + t) * D) + dp);
+        }
+        if constexpr (VT) {
+            // dims lane and lane + 64, tokens t0.. in two 8-token halves (a
+            // half past the end re-reads the first one; max_ctx % 8 == 0)
+            const uint32_t t1 = len > 8 ? t0 + 8 : t0;
+            const uint16_t *r0 = vb + (size_t)lane * a.max_ctx, *r1 = vb + (size_t)(lane + 64) * a.max_ctx;
+            vr[0] = *(const uint4 *)(r0 + t0);
+            vr[1] = *(const uint4 *)(r0 + t1);
+            vr[2] = *(const uint4 *)(r1 + t0);
+            vr[3] = *(const uint4 *)(r1 + t1);
+        } else {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const uint32_t t = min((uint32_t)(4 * v + row), len - 1);
+                vr[v] = *((const uint4 *)(vb + (size_t)(t0 + t) * D) + dp);
+            }
+        }
+    };
+    uint4 kA[KT], vA[4], kB[KT], vB[4];
+    load(kA, vA, 0);
+
+    // q (optionally RoPE-rotated at rope_pos) -> LDS -> this lane's 8 dims
+    {
+        float v = qv;
+        if (a.rope_pos >= 0) {
+            const float partner = __shfl_xor(v, 1, 64);  // all lanes take part
+            v = rope_rotate(v, partner, tid % D, (uint32_t)a.rope_pos, D, a.rope_theta);
+        }
+        if (tid < G * D) qs[tid / D][tid % D] = v;
+    }
+    __syncthreads();
+    float qr[G][8];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qr[g][i] = qs[g][dp * 8 + i];
+
+    float m_run[G], l_run[G];
+    float o[G][VT ? 2 : 8];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        m_run[g] = -INFINITY;
+        l_run[g] = 0.f;
+#pragma unroll
+        for (int e = 0; e < (VT ? 2 : 8); ++e) o[g][e] = 0.f;
+    }
+    const int sg = (lane >> 4) % G;   // softmax: head of this lane's row
+
+    auto compute = [&](const uint4 (&kr)[KT], const uint4 (&vr)[4], uint32_t i) {
+        const uint32_t t0 = c0 + grp(i) * TPI, len = min((uint32_t)TPI, cend - t0);
+        // scores: value v G + g = q_g . k of token 4 v + row over 8 dims
+        constexpr int NV = KT * G;
+        float dot[NV];
+#pragma unroll
+        for (int k = 0; k < NV; ++k) dot[k] = 0.f;
+#pragma unroll
+        for (int v = 0; v < KT; ++v) {
+            const uint32_t wv[4] = {kr[v].x, kr[v].y, kr[v].z, kr[v].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float k0, k1;
+                unpack2<KVDT>(wv[e], k0, k1);
+#pragma unroll
+                for (int g = 0; g < G; ++g)
+                    dot[v * G + g] = fmaf(qr[g][2 * e + 1], k1, fmaf(qr[g][2 * e], k0, dot[v * G + g]));
+            }
+        }
+        group_multi_sum<NV, DP>(dot);
+        {   // lanes whose low 4 - H bits are 0 hold the total of value dp >> (4 - H)
+            constexpr int H = NV == 4 ? 2 : 3;
+            if ((dp & ((DP >> H) - 1)) == 0) {
+                const int k = dp >> (4 - H), v = k / G, g = k % G;
+                const uint32_t tt = (uint32_t)(4 * v + row);
+                pw[w][g][tt] = tt < len ? dot[0] * a.scale : -INFINITY;
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        // online softmax, one 16-lane row per head (rows >= G repeat them)
+        float alpha[G];
+        {
+            const float sc = pw[w][sg][dp];
+            float mx = sc;
+            mx = fmaxf(mx, dpp_move<DPP_XOR1>(mx, -INFINITY));
+            mx = fmaxf(mx, dpp_move<DPP_XOR2>(mx, -INFINITY));
+            mx = fmaxf(mx, dpp_move<DPP_ROW_HALF_MIRROR>(mx, -INFINITY));
+            mx = fmaxf(mx, dpp_move<DPP_ROW_MIRROR>(mx, -INFINITY));
+            const float mo = G == 1 ? m_run[0] : (sg == 0 ? m_run[0] : m_run[G - 1]);
+            const float mn = fmaxf(mo, mx);
+            const float e = expf(sc - mn);
+            float rs = e;
+            rs += dpp_move<DPP_XOR1>(rs, 0.f);
+            rs += dpp_move<DPP_XOR2>(rs, 0.f);
+            rs += dpp_move<DPP_ROW_HALF_MIRROR>(rs, 0.f);
+            rs += dpp_move<DPP_ROW_MIRROR>(rs, 0.f);
+            if (lane < 16 * G) pw[w][sg][dp] = e;
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const float mng = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mn), 16 * g));
+                const float rsg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rs), 16 * g));
+                alpha[g] = expf(m_run[g] - mng);
+                l_run[g] = fmaf(l_run[g], alpha[g], rsg);
+                m_run[g] = mng;
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        if constexpr (VT) {
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                o[g][0] *= alpha[g];
+                o[g][1] *= alpha[g];
+            }
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const uint32_t w0[4] = {vr[hh].x, vr[hh].y, vr[hh].z, vr[hh].w};
+                const uint32_t w1[4] = {vr[2 + hh].x, vr[2 + hh].y, vr[2 + hh].z, vr[2 + hh].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int t = 8 * hh + 2 * e;
+                    float a0, a1, b0, b1;
+                    unpack2<KVDT>(w0[e], a0, a1);
+                    unpack2<KVDT>(w1[e], b0, b1);
+#pragma unroll
+                    for (int g = 0; g < G; ++g) {
+                        const float p0 = pw[w][g][t], p1 = pw[w][g][t + 1];
+                        o[g][0] = fmaf(p1, a1, fmaf(p0, a0, o[g][0]));
+                        o[g][1] = fmaf(p1, b1, fmaf(p0, b0, o[g][1]));
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) o[g][e] *= alpha[g];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const uint32_t wv[4] = {vr[v].x, vr[v].y, vr[v].z, vr[v].w};
+                float p[G];
+#pragma unroll
+                for (int g = 0; g < G; ++g) p[g] = pw[w][g][4 * v + row];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float v0, v1;
+                    unpack2<KVDT>(wv[e], v0, v1);
+#pragma unroll
+                    for (int g = 0; g < G; ++g) {
+                        o[g][2 * e] = fmaf(p[g], v0, o[g][2 * e]);
+                        o[g][2 * e + 1] = fmaf(p[g], v1, o[g][2 * e + 1]);
+                    }
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();   // the next group rewrites pw[w]
+    };
+
+    for (uint32_t i = 0; i < nit; i += 2) {
+        load(kB, vB, i + 1);
+        compute(kA, vA, i);
+        load(kA, vA, i + 2);
+        if (i + 1 < nit) compute(kB, vB, i + 1);
+    }
+
+    // the 4 waves' states -> one (m, l, o) per query head
+    if (lane == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            wml[w][g][0] = m_run[g];
+            wml[w][g][1] = l_run[g];
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        if constexpr (VT) {
+            wo[w][0][g][lane] = o[g][0];
+            wo[w][0][g][lane + 64] = o[g][1];
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) wo[w][row][g][dp * 8 + e] = o[g][e];
+        }
+    }
+    __syncthreads();
+    if (tid < G * D) {
+        const int g = tid / D, d = tid % D;
+        float M = wml[0][g][0];
+#pragma unroll
+        for (int k = 1; k < 4; ++k) M = fmaxf(M, wml[k][g][0]);
+        float s = 0.f, l = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            // a wave without tokens has m = -inf, l = 0, o = 0: weight 0
+            const float sc = expf(wml[k][g][0] - M);
+            float ok = 0.f;
+#pragma unroll
+            for (int r = 0; r < NR; ++r) ok += wo[k][r][g][d];
+            s = fmaf(sc, ok, s);
+            l = fmaf(sc, wml[k][g][1], l);
+        }
+        if (a.nchunks == 1) {
+            store_dt(a.out, (size_t)(qb + g) * D + d, s / l, a.odt);
+        } else {
+            const size_t slot = (size_t)(qb + g) * a.nchunks + c;
+            a.part_o[slot * D + d] = s;
+            if (d == 0) {
+                a.part_ml[slot * 2] = M;
+                a.part_ml[slot * 2 + 1] = l;
             }
         }
     }
@@ -1333,16 +1627,21 @@ size_t nnz_attn_scratch_bytes_impl(uint32_t hq, uint32_t head_dim, uint32_t seq_
 
 // The combine step for Hq x nq queries: the preload depth covers the chunks
 // each lane group folds (ceil(nchunks / (256 / (D/4)))), up to 16.
+template <int D, int DS>
+static void launch_combine_ds(nnz_ctx *ctx, const AttnArgs &a, uint32_t nq) {
+    constexpr uint32_t PARTS = 256 / (D / 4 / DS);
+    const uint32_t per = ceil_div(a.nchunks, PARTS);
+    const dim3 grid(a.hq, nq * DS);
+    if (per <= 1) attn_combine_kernel<D, 1, DS><<<grid, 256, 0, ctx->stream>>>(a);
+    else if (per <= 2) attn_combine_kernel<D, 2, DS><<<grid, 256, 0, ctx->stream>>>(a);
+    else if (per <= 4) attn_combine_kernel<D, 4, DS><<<grid, 256, 0, ctx->stream>>>(a);
+    else if (per <= 8) attn_combine_kernel<D, 8, DS><<<grid, 256, 0, ctx->stream>>>(a);
+    else attn_combine_kernel<D, 16, DS><<<grid, 256, 0, ctx->stream>>>(a);
+}
+
 template <int D>
 static void launch_combine(nnz_ctx *ctx, const AttnArgs &a, uint32_t nq) {
-    constexpr uint32_t PARTS = 256 / (D / 4);
-    const uint32_t per = ceil_div(a.nchunks, PARTS);
-    const dim3 grid(a.hq, nq);
-    if (per <= 1) attn_combine_kernel<D, 1><<<grid, 256, 0, ctx->stream>>>(a);
-    else if (per <= 2) attn_combine_kernel<D, 2><<<grid, 256, 0, ctx->stream>>>(a);
-    else if (per <= 4) attn_combine_kernel<D, 4><<<grid, 256, 0, ctx->stream>>>(a);
-    else if (per <= 8) attn_combine_kernel<D, 8><<<grid, 256, 0, ctx->stream>>>(a);
-    else attn_combine_kernel<D, 16><<<grid, 256, 0, ctx->stream>>>(a);
+    launch_combine_ds<D, 1>(ctx, a, nq);
 }
 
 template <int D, int G, int KVDT, bool VT>
@@ -1516,8 +1815,25 @@ int nnz_attn_launch(nnz_ctx *ctx, const void *q, int qdt, const void *kc, const 
         default: DEC_KV(DD, 8); break;                                       \
         }                                                                    \
     } while (0)
-    if (d.head_dim == 128) DEC_G(128);
-    else DEC_G(64);
+    if (d.head_dim == 128 && gb <= 2 && !ATTN_STREAM_OFF) {
+#define STR(GG)                                                                                         \
+    do {                                                                                                \
+        if (kvdt == NNZ_F16) {                                                                          \
+            if (vt) attn_stream_kernel<GG, NNZ_F16, true><<<blocks, 256, 0, ctx->stream>>>(a);          \
+            else attn_stream_kernel<GG, NNZ_F16, false><<<blocks, 256, 0, ctx->stream>>>(a);            \
+        } else {                                                                                        \
+            if (vt) attn_stream_kernel<GG, NNZ_BF16, true><<<blocks, 256, 0, ctx->stream>>>(a);         \
+            else attn_stream_kernel<GG, NNZ_BF16, false><<<blocks, 256, 0, ctx->stream>>>(a);           \
+        }                                                                                               \
+    } while (0)
+        if (gb == 1) STR(1);
+        else STR(2);
+#undef STR
+    } else if (d.head_dim == 128) {
+        DEC_G(128);
+    } else {
+        DEC_G(64);
+    }
 #undef DEC_G
 #undef DEC_KV
 #undef DEC

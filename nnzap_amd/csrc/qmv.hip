@@ -261,10 +261,10 @@ template <int BITS, int NMAT, int R, int NV, bool RES>
 __device__ __forceinline__ void load_step_full(const QmvArgs &a, StepRegs<NMAT, R, NV, (BITS == 1 ? 1 : 4)> &s,
                                                uint32_t rb, const FullOffsets<R, NV> &fo,
                                                uint32_t words_per_row, uint32_t G) {
-    // R == 8 is chosen only for vocabulary-sized matrices (the LM head), read
-    // once per token: non-temporal loads keep them from evicting the layer
-    // weights and the KV cache
-    constexpr int AUX = (R == 8) ? 2 : 0;
+    // Every weight is read once per token: non-temporal loads (measured:
+    // decode +0.6% over plain loads for the layer weights, +0.8% for the LM
+    // head) leave the caches to the activations and the KV cache.
+    constexpr int AUX = 2;
     __amdgpu_buffer_rsrc_t cr[NMAT], sr[NMAT], br[NMAT];
     uint32_t seg_start = 0;
     if constexpr (NMAT == 1) {

@@ -337,9 +337,6 @@ struct AttnArgs {
 };
 
 constexpr int ATT_MAX_CHUNK = 512;
-#ifndef ATTN_STREAM_OFF
-#define ATTN_STREAM_OFF 0
-#endif
 #ifndef NNZ_DEC_TARGET_BLOCKS
 #define NNZ_DEC_TARGET_BLOCKS 1024u
 #endif
@@ -1815,7 +1812,7 @@ int nnz_attn_launch(nnz_ctx *ctx, const void *q, int qdt, const void *kc, const 
         default: DEC_KV(DD, 8); break;                                       \
         }                                                                    \
     } while (0)
-    if (d.head_dim == 128 && gb <= 2 && !ATTN_STREAM_OFF) {
+    if (d.head_dim == 128 && gb <= 2) {
 #define STR(GG)                                                                                         \
     do {                                                                                                \
         if (kvdt == NNZ_F16) {                                                                          \

@@ -423,8 +423,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
     __shared__ float lut[LUT ? NV * 8 * 16 * 64 : 1];
     float xr[NV][32];
     float xsum[NV];
-    if constexpr (LUT) {
-        static_assert(!MERGE, "tables are built from x or the normalised residual");
+    if constexpr (LUT && !MERGE) {   // (the merge prologue builds its tables itself)
         const int wid = threadIdx.x >> 6;
         float v[NV][2][4];
         if constexpr (NORM) {
@@ -581,17 +580,20 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
             }
         }
     } else if constexpr (MERGE) {
-        // The block merges the attention partials into x once and stages it
-        // f16 in LDS for every wave -- the merge that would otherwise be a
-        // launch of its own.  Phase 1: per (head, chunk) the weight
-        // exp(m_c - M) and per head the denominator, one thread per pair
-        // (a head's 16 chunk slots are one DPP row).  Phase 2: 8 outputs per
-        // thread per 2048 columns.  All partials of the first
+        // The block merges the attention partials into x once -- the merge
+        // that would otherwise be a launch of its own -- and builds the
+        // nibble tables from it (LUT), or stages it f16 in LDS for every wave.
+        // Phase 1: per (head, chunk) the weight exp(m_c - M) and per head the
+        // denominator, one thread per pair (a head's 16 chunk slots are one
+        // DPP row).  Phase 2: 8 consecutive outputs per thread per 2048
+        // columns (coalesced partial loads); with tables, the thread writes
+        // the entries of its two nibbles (unit e0 / 32; the main loop's reads
+        // stay one lane per unit).  All partials of the first
         // MERGE_MAX_CHUNKS chunks are loaded up front, independently of the
         // live length.
         static_assert(MERGE_MAX_CHUNKS == 16, "one DPP row per head");
         __shared__ __align__(16) f16_t xs[2048 * NV];
-        __shared__ float mw[(2048 * NV / 64) * MERGE_MAX_CHUNKS];   // >= heads x 16 (D >= 64)
+        __shared__ __align__(16) float mw[(2048 * NV / 64) * MERGE_MAX_CHUNKS];   // >= heads x 16 (D >= 64)
         __shared__ float mden[2048 * NV / 64];
         const MergeIn &mg = a.mg;
         const uint32_t D = mg.head_dim;
@@ -670,35 +672,79 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
             const uint32_t e0 = (threadIdx.x + 256u * kk) * 8u;
             if (e0 < K) {
                 const uint32_t hd = e0 / D;
+                // the head's 16 chunk weights in 4 LDS reads, before any use
+                float wv[MERGE_MAX_CHUNKS];
+#pragma unroll
+                for (int q = 0; q < MERGE_MAX_CHUNKS / 4; ++q) {
+                    const float4 w4 = *(const float4 *)&mw[hd * MERGE_MAX_CHUNKS + 4 * q];
+                    wv[4 * q] = w4.x; wv[4 * q + 1] = w4.y; wv[4 * q + 2] = w4.z; wv[4 * q + 3] = w4.w;
+                }
+                const float den = mden[hd];
                 float num[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int c = 0; c < MERGE_MAX_CHUNKS; ++c) {
                     if ((uint32_t)c < mg.nchunks) {
-                        const float wgt = mw[hd * MERGE_MAX_CHUNKS + c];
+                        const float wgt = wv[c];
                         num[0] = fmaf(wgt, oa[kk][c].x, num[0]); num[1] = fmaf(wgt, oa[kk][c].y, num[1]);
                         num[2] = fmaf(wgt, oa[kk][c].z, num[2]); num[3] = fmaf(wgt, oa[kk][c].w, num[3]);
                         num[4] = fmaf(wgt, ob[kk][c].x, num[4]); num[5] = fmaf(wgt, ob[kk][c].y, num[5]);
                         num[6] = fmaf(wgt, ob[kk][c].z, num[6]); num[7] = fmaf(wgt, ob[kk][c].w, num[7]);
                     }
                 }
-                const float den = mden[hd];
+                // one division, then products (the f16 result differs from
+                // num / den only where the two straddle an f16 rounding edge)
+                const float rden = 1.f / den;
+                if constexpr (LUT) {
+                    float x8[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) xs[e0 + e] = (f16_t)(num[e] / den);
+                    for (int e = 0; e < 8; ++e) x8[e] = (float)(f16_t)(num[e] * rden);
+                    const uint32_t u = e0 >> 5, n0 = (e0 & 31) >> 2;   // unit, first nibble
+                    float *const dst = lut + ((u >> 6) * 8 + n0) * 16 * 64 + (u & 63);
+#pragma unroll
+                    for (int sb = 0; sb < 2; ++sb) {
+                        const float *x4 = x8 + 4 * sb;
+                        const float p1 = x4[0] - x4[1], p3 = x4[0] + x4[1];
+                        const float q1 = x4[2] - x4[3], q3 = x4[2] + x4[3];
+                        const float pp[4] = {-p3, p1, -p1, p3};
+                        const float qq[4] = {-q3, q1, -q1, q3};
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) dst[(sb * 16 + e) * 64] = pp[e & 3] + qq[e >> 2];
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) xs[e0 + e] = (f16_t)(num[e] * rden);
+                }
+            }
+        }
+        if constexpr (LUT) {
+            // units past the row end (K < 2048 NV) read all-zero tables:
+            // thread (lane, wave) clears nibbles 2 wave, 2 wave + 1 of its lane's
+            const int wid = threadIdx.x >> 6;
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                if (!uvalid[j]) {
+#pragma unroll
+                    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) lut[((j * 8 + 2 * wid + sb) * 16 + e) * 64 + lane] = 0.f;
+                }
             }
         }
         __syncthreads();
+        if constexpr (!LUT) {
 #pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            const uint32_t u = uvalid[j] ? (uint32_t)ll + (uint32_t)(LPR * j) : 0u;
-            const uint4 *p = (const uint4 *)(xs + u * 32);
+            for (int j = 0; j < NV; ++j) {
+                const uint32_t u = uvalid[j] ? (uint32_t)ll + (uint32_t)(LPR * j) : 0u;
+                const uint4 *p = (const uint4 *)(xs + u * 32);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint4 q = p[i];
-                const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
+                for (int i = 0; i < 4; ++i) {
+                    const uint4 q = p[i];
+                    const uint32_t w4[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    xr[j][8 * i + 2 * t] = (float)__builtin_bit_cast(f16_t, (uint16_t)(w4[t] & 0xFFFFu));
-                    xr[j][8 * i + 2 * t + 1] = (float)__builtin_bit_cast(f16_t, (uint16_t)(w4[t] >> 16));
+                    for (int t = 0; t < 4; ++t) {
+                        xr[j][8 * i + 2 * t] = (float)__builtin_bit_cast(f16_t, (uint16_t)(w4[t] & 0xFFFFu));
+                        xr[j][8 * i + 2 * t + 1] = (float)__builtin_bit_cast(f16_t, (uint16_t)(w4[t] >> 16));
+                    }
                 }
             }
         }
@@ -1068,7 +1114,7 @@ int launch_nv(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks, bool lut) 
     } else {
         // rows narrower than a wave (K < 2048) occur only with one unit per lane
         const bool full = a.lpr_log2 == 6;
-        if constexpr (BITS == 1 && NV <= LUT_MAX_NV && XIN != XIN_MERGE) {
+        if constexpr (BITS == 1 && NV <= LUT_MAX_NV) {
             if (lut) launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, true, true>(ctx, a, R, blocks);
             else if (full) launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false, true>(ctx, a, R, blocks);
             else if constexpr (NV == 1) launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false, false>(ctx, a, R, blocks);
@@ -1209,7 +1255,7 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
     }
     // measured: tables pay off from 4 row-units per wave (fused Q/K/V, 4
     // rows per wave: 3.55 us without, 3.16 us with)
-    if (lut && ceil_div(d.M, blocks * 4u) * NMAT < 4u) lut = false;
+    if (lut && ceil_div(d.M, blocks * 4u) * NMAT < 4u && !MERGE) lut = false;
 
     QmvArgs a{};
     for (int i = 0; i < nw; ++i) {

@@ -150,13 +150,16 @@ def test_gqa_fused_1pass_successive_positions(dev, hq, hkv, d):
 
 @pytest.mark.parametrize("pos", [30, 700, 1023])
 @pytest.mark.parametrize("freq_table", [False, True])
-def test_attention_partials_merged_o_projection(dev, pos, freq_table):
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (24, 12)])
+def test_attention_partials_merged_o_projection(dev, pos, freq_table, hq, hkv):
     """The decode step's two halves: attention to per-chunk partials, then the
     1-bit O projection (residual +=) merging them in its prologue.  Checked
     against the one-call fused attention + plain O projection on the GPU
     (same f16 attention output, different QMV order: 1e-4), and against the
-    oracle (normwise, after the f16 rounding of the attention output)."""
-    hq, hkv, d, max_ctx, theta = 16, 8, 128, 1024, 1e6
+    oracle (normwise, after the f16 rounding of the attention output).
+    24 heads: K = 3072, rows of one and a half wave-widths (the second unit
+    block is half past the row end)."""
+    d, max_ctx, theta = 128, 1024, 1e6
     H = 2048
     qn = (1 + 0.1 * S.normal(461, d)).astype(np.float32)
     kn = (1 + 0.1 * S.normal(462, d)).astype(np.float32)

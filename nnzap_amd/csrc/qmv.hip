@@ -124,6 +124,7 @@ template <class T>
 using gptr = T *;   // host pass: device bodies are parsed, not generated
 #endif
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2v __attribute__((ext_vector_type(2)));
 
 template <class T>
 __device__ __forceinline__ gptr<T> uniform_ptr(T *p) {
@@ -1008,6 +1009,14 @@ __global__ __launch_bounds__(64 * KS) void qmv1_splitk_kernel(QmvArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < 32; ++i) xsum += xr[i];
+    uint32_t xw[16];   // f16 x: column pairs (2p, 2p + 1) as loaded
+    if constexpr (XDT == NNZ_F16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xw[4 * i] = xraw[i].x; xw[4 * i + 1] = xraw[i].y;
+            xw[4 * i + 2] = xraw[i].z; xw[4 * i + 3] = xraw[i].w;
+        }
+    }
 
     for (int it = 0; base < M; base += stride, ++it) {
         Step nxt;
@@ -1017,14 +1026,37 @@ __global__ __launch_bounds__(64 * KS) void qmv1_splitk_kernel(QmvArgs a) {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
             const uint32_t w = cur.cw[r];
-            float sb = 0.f;
+            if constexpr (XDT == NNZ_F16) {
+                // f16 x: the 32 weights as 16 pairs of f16 +-s (the sign of
+                // each half from one bit, as the prefill GEMM expands them)
+                // into v_dot2 with the x pairs, f32 accumulation: s * x is
+                // exact, so this is the f32 sum of the same products
+                const uint32_t s16 = uv ? (uint32_t)cur.sc[r] : 0u;
+                const uint32_t ns2 = (s16 | (s16 << 16)) ^ 0x80008000u;   // (-s, -s)
+                float acc = 0.f;
 #pragma unroll
-            for (int i = 0; i < 32; ++i) {
-                const int mask = ((int)(w << (31 - i))) >> 31;  // 0 or -1
-                sb += __int_as_float(mask & __float_as_int(xr[i]));
+                for (int b = 0; b < 4; ++b) {
+                    const uint32_t z = (w >> (8 * b)) & 0xFFu;
+                    uint32_t z2;   // the byte twice, 15 bits apart (kept from being folded into a multiply)
+                    asm("v_lshl_or_b32 %0, %1, 15, %1" : "=v"(z2) : "v"(z));
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const uint32_t pr2 = ((z2 << (15 - 2 * q)) & 0x80008000u) ^ ns2;
+                        acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2v, pr2),
+                                                     __builtin_bit_cast(h2v, xw[4 * b + q]), acc, false);
+                    }
+                }
+                pr[r] = acc;
+            } else {
+                float sb = 0.f;
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    const int mask = ((int)(w << (31 - i))) >> 31;  // 0 or -1
+                    sb += __int_as_float(mask & __float_as_int(xr[i]));
+                }
+                const float sc = uv ? (float)__builtin_bit_cast(f16_t, cur.sc[r]) : 0.f;
+                pr[r] = sc * (2.f * sb - xsum);
             }
-            const float sc = uv ? (float)__builtin_bit_cast(f16_t, cur.sc[r]) : 0.f;
-            pr[r] = sc * (2.f * sb - xsum);
         }
         // the R row partials of this wave in one exchange-halving reduction
         const float p = multi_row_sum<R>(pr);

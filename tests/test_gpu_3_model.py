@@ -326,6 +326,37 @@ def test_tiny_q4_prefill_chunks_match_single_prefill(mdev, tiny_q4):
         b.close()
 
 
+def test_bonsai_1_7b_q4_layer_shapes(mdev):
+    """The 4-bit decoder at the Bonsai-1.7B_Q4 layer shapes (transformer.zig:
+    336-350: hidden 2048, MLP 6144, 16 query / 8 KV heads x 128, q4_mlx gs 64,
+    Q4 embedding tied into the LM head), 2 layers and a 3000-token vocabulary
+    so the oracle stays fast: batched prefill, single decode steps and greedy
+    generation against the oracle -- every 4-bit projection shape of the model
+    goes through the Q4 QMV, GEMM and embedding kernels."""
+    cfg = cf.DecoderConfig(**{**cf.BONSAI_1_7B.__dict__, "vocab_size": 3000, "num_layers": 2,
+                              "max_context_length": 256, "max_prefill_length": 64, "group_size": 64,
+                              "embed_kind": 2, "lm_head_kind": 2, "quant_format": 1})
+    w = cf.decoder_weights(cfg, norm_mode="unit")
+    print("bonsai-1.7B_Q4 layer shapes", flush=True)
+    m = DecoderModel(mdev, cfg)
+    try:
+        m.load(w)
+        ids = cf.prompt_ids(cfg, 24)
+        ref = OracleDecoder(w)
+        got = m.prefill(ids, 0)
+        want = ref.forward(list(ids), 0)[-1]
+        assert_close_normwise(got, want, rtol=Q4_RTOL, what="q4 1.7B prefill")
+        for i, t in enumerate([11, 2999]):
+            pos = len(ids) + i
+            assert_close_normwise(m.forward_decode(t, pos), ref.forward([t], pos)[0], rtol=Q4_RTOL,
+                                  what=f"q4 1.7B decode {pos}")
+        toks, _, _ = m.generate(ids, 12)
+        ref_toks, _ = OracleDecoder(w).generate(ids, 12)
+        assert np.array_equal(toks, ref_toks), (toks, ref_toks)
+    finally:
+        m.close()
+
+
 def test_q4_checkpoint_model_matches_oracle(mdev, tmp_path):
     """A q4_mlx checkpoint (raw bf16 scales and biases, tied embedding) loaded
     from mapped shards: prefill logits and 16 greedy tokens against the oracle

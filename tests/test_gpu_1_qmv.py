@@ -51,7 +51,8 @@ def test_config2_q1_qmv_f32(dev):
     assert_close(host(y), O.qmv(w, x), what="config2")
 
 
-@pytest.mark.parametrize("M,K", [(64, 5504), (48, 128), (33, 256), (130, 2048), (20, 4096)])
+@pytest.mark.parametrize("M,K", [(64, 5504), (48, 128), (33, 256), (130, 2048), (20, 4096),
+                                 (3, 2048), (1, 4096)])
 def test_q1_qmv_shapes(dev, M, K):
     w = cf.q1_matrix(M, K, 128, 300 + K, 301 + K)
     x = S.normal(302, K).astype(np.float32)
@@ -189,6 +190,33 @@ def test_fused_norm_qkv_and_norm_lm_head(dev, qrows, kvrows, K):
     assert_close(host(k), _f16(O.qmv(wk, xn)), what="qkv k")
     assert_close(host(v), _f16(O.qmv(wv, xn)), what="qkv v")
     assert_close(host(y), O.qmv(wq, xn), what="norm lm head")
+
+
+def test_norm_lm_head_vocabulary_rows_ragged(dev):
+    """A vocabulary-sized norm + QMV (the LM head's form: nibble tables, 8
+    rows per wave step) with a row count that is not a multiple of the rows
+    per step: the last step is clamped back onto rows [M - 8, M) and must
+    store only the rows no other step wrote."""
+    M, K = 65536 + 13, 2048
+    w = cf.q1_matrix(M, K, 128, 390, 391)
+    res = S.normal(392, K).astype(np.float32)
+    nw = (1.0 + 0.1 * S.normal(393, K)).astype(np.float32)
+    y = torch.full((M,), float("nan"), dtype=torch.float32, device="cuda")
+    ops.dispatch_fused_norm_qmv_f16in(dev, _dw(dev, w), tdev(res), y, tdev(nw))
+    dev.sync()
+    assert_close(host(y), O.qmv(w, O.norm_to_half(res, nw)), what="vocabulary rows")
+
+
+@pytest.mark.parametrize("M", [6145, 5, 1])
+def test_q4_qmv_ragged_rows(dev, M):
+    """4-bit QMV on an f32 input (two rows per wave step) with row counts
+    that leave a partial last step, or fewer rows than a step."""
+    w = cf.q4_matrix(M, 2048, 64, 344, 345, 346)
+    x = S.normal(347, 2048).astype(np.float32)
+    y = torch.full((M,), float("nan"), dtype=torch.float32, device="cuda")
+    ops.dispatch_q4mv(dev, _dw(dev, w), tdev(x), y)
+    dev.sync()
+    assert_close(host(y), O.qmv(w, x), what=f"q4 M={M}")
 
 
 # ------------------------------------------------------------ Q4 family ---

@@ -1246,10 +1246,10 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
                 name, d.K, nv);
     int R = 4;
     // Rows per wave-step: as many as keep about one block per CU (pairs and
-    // 4-bit matrices on a plain input: two; config 1 5.55 -> 5.34 us) --
+    // 4-bit matrices: two; config 1 5.55 -> 5.34 us, 4-bit decode +2 %) --
     // measured best for the decode shapes -- bounded by the weight words a
     // lane holds in flight (two steps are live).
-    const uint32_t min_blocks = NMAT == 2 || (BITS == 4 && XIN == XIN_X) ? 512u : 256u;
+    const uint32_t min_blocks = NMAT == 2 || BITS == 4 ? 512u : 256u;
     while (R > 1 && (ceil_div(d.M, 4u * R * rpw) < min_blocks || NMAT * R * (int)nv * vec > 32)) R >>= 1;
     // 1-bit full-wave rows may use the nibble tables.  Building them is a
     // fixed cost per block that pays off from about four matrix rows per

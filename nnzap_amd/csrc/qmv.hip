@@ -1183,6 +1183,10 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
         total += rows;
     }
     if (NMAT == 1) NNZ_REQUIRE(ctx, total == d.M, NNZ_EINVAL, "%s: segments do not add up to M", name);
+    // whole-row steps address a matrix through 32-bit byte offsets
+    NNZ_REQUIRE(ctx, (uint64_t)d.M * d.K * BITS / 8 < (1ull << 32), NNZ_EUNSUPPORTED,
+                "%s: matrix of %llu bytes (4 GiB at most)", name,
+                (unsigned long long)((uint64_t)d.M * d.K * BITS / 8));
     NNZ_REQUIRE(ctx, EPI != EPI_RESADD || nw == 1, NNZ_EINVAL, "%s: residual add takes one matrix", name);
     if (MERGE) {
         NNZ_REQUIRE(ctx, merge && merge->part_o && merge->part_ml, NNZ_EINVAL, "%s: null partials", name);

@@ -644,24 +644,32 @@ def cpu_baseline(pos=512, warmup=5, runs=30, dq_warmup=1, dq_runs=3):
     td.fill_cache(pos)
     x = torch.randn(cfg.hidden_size, generator=torch.Generator().manual_seed(1)) * 0.02
     t_pre = _median_time(lambda: td.step(x, pos), warmup, runs)
+    # the 512-token prompt as one batch (the reference prefills token by
+    # token; one warm-up, the median of 3)
+    xs = torch.randn(512, cfg.hidden_size, generator=torch.Generator().manual_seed(2)) * 0.02
+    t_pf = _median_time(lambda: td.prefill(xs, 0), 1, 3)
     del td
     tq = TorchDecoder(w, pos + 8, predequantise=False)
     tq.fill_cache(pos)
     t_dq = _median_time(lambda: tq.step(x, pos), dq_warmup, dq_runs)
     del tq
     log(f"cpu decode (torch f32, {threads} threads): {1 / t_pre:.2f} tok/s pre-dequantised, "
-        f"{1 / t_dq:.3f} tok/s dequantising every step (one-time dequant {t_deq:.1f}s)")
+        f"{1 / t_dq:.3f} tok/s dequantising every step (one-time dequant {t_deq:.1f}s); "
+        f"prefill of 512 tokens {1000 * t_pf:.0f} ms")
     return {"value": round(1.0 / t_pre, 3), "unit": "tok/s", "cores": threads, "kind": "port",
             "impl": "PyTorch CPU float32 (oracle/torch_cpu.py)", "cpu_model": cpu_model(),
             "cpu_count": os.cpu_count(),
             "ms_per_token_predequantised": round(1000 * t_pre, 2),
             "ms_per_token_dequant_each_call": round(1000 * t_dq, 1),
             "tok_s_dequant_each_call": round(1.0 / t_dq, 4),
+            "prefill_512_ms": round(1000 * t_pf, 1),
+            "prefill_tok_s": round(512 / t_pf, 1),
             "sample": (f"one decode step of the full config-5 decoder (28 layers + 1-bit LM head, "
                        f"KV cache of {pos} tokens) in torch float32 on {threads} threads; "
                        f"value: weights pre-dequantised, {warmup} warm-up steps then the median "
                        f"of {runs}; dequantising every step: {dq_warmup} warm-up then the median "
-                       f"of {dq_runs}")}
+                       f"of {dq_runs}; prefill: the 512-token prompt as one batch "
+                       f"(pre-dequantised), 1 warm-up then the median of 3")}
 
 
 def cpu_configs(full=False):

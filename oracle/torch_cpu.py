@@ -15,7 +15,11 @@ written from the same formulas as the oracle:
   layer RMSNorm, Q/K/V, per-head q/k RMSNorm + consecutive-pair RoPE, KV
   append, GQA softmax attention, O += , RMSNorm, silu(gate)*up, down +=; final
   RMSNorm and the LM head.  Activations stay float32 (the reference's CPU
-  test precision, transformer_test.zig:364-716).
+  test precision, transformer_test.zig:364-716);
+* the prompt as one batch (``prefill``): the same layer arithmetic with
+  [P x K] products and causal attention -- the reference itself prefills
+  token by token (chunkedPrefill, transformer.zig:4032-4068), which on this
+  CPU would be P decode steps.
 
 Two variants are timed: weights dequantised once up front (float32 GEMVs on
 resident matrices), and dequantised from the packed codes on every call.
@@ -109,6 +113,55 @@ class TorchDecoder:
         g = torch.Generator().manual_seed(seed)
         self.kc[:, :, :upto] = torch.randn(self.kc[:, :, :upto].shape, generator=g).half().float()
         self.vc[:, :, :upto] = torch.randn(self.vc[:, :, :upto].shape, generator=g).half().float()
+
+    @torch.no_grad()
+    def prefill(self, xs: torch.Tensor, start: int = 0) -> torch.Tensor:
+        """The prompt as one batch: residual rows ``xs`` [P, H] at positions
+        start.. (every projection one [P x K] . W^T product, causal GQA
+        attention over the cache); fills the KV cache and returns the float32
+        logits of the last row [V] -- the same arithmetic as P ``step``
+        calls up to float32 summation order."""
+        cfg = self.cfg
+        D, Hq, Hkv = cfg.head_dim, cfg.num_query_heads, cfg.num_kv_heads
+        g, eps = Hq // Hkv, cfg.rms_eps
+        P = xs.shape[0]
+        pos = torch.arange(start, start + P, dtype=torch.float32)
+        ang = pos[:, None] * self.inv_freq[None, :]                      # [P, D/2]
+        c, s_ = torch.cos(ang)[:, None, :], torch.sin(ang)[:, None, :]
+
+        def rope_rows(x):                                                # [P, heads, D]
+            a, b = x[..., 0::2], x[..., 1::2]
+            out = torch.empty_like(x)
+            out[..., 0::2] = a * c - b * s_
+            out[..., 1::2] = a * s_ + b * c
+            return out
+
+        # query i sees keys 0 .. start + i
+        mask = torch.arange(start + P)[None, :] > (start + torch.arange(P))[:, None]
+        res = xs.clone()
+        for l in range(cfg.num_layers):
+            nm = self.norms[l]
+            xn = rmsnorm(res, nm["attn_norm"], eps)
+            q = xn @ self._weight(l, "q").T
+            k = xn @ self._weight(l, "k").T
+            v = xn @ self._weight(l, "v").T
+            q = rope_rows(rmsnorm(q.view(P, Hq, D), nm["q_norm"], eps))
+            k = rope_rows(rmsnorm(k.view(P, Hkv, D), nm["k_norm"], eps))
+            self.kc[l, :, start:start + P] = k.transpose(0, 1).half().float()
+            self.vc[l, :, start:start + P] = v.view(P, Hkv, D).transpose(0, 1).half().float()
+            K, V = self.kc[l, :, :start + P], self.vc[l, :, :start + P]   # [Hkv, T, D]
+            qh = q.view(P, Hkv, g, D).permute(1, 2, 0, 3)                 # [Hkv, g, P, D]
+            sc = torch.matmul(qh, K.transpose(1, 2)[:, None]) / np.sqrt(D)  # [Hkv, g, P, T]
+            sc = sc.masked_fill(mask, float("-inf"))
+            att = torch.matmul(torch.softmax(sc, dim=-1), V[:, None])       # [Hkv, g, P, D]
+            att = att.permute(2, 0, 1, 3).reshape(P, Hq * D)
+            res = res + att @ self._weight(l, "o").T
+            xn2 = rmsnorm(res, nm["ffn_norm"], eps)
+            h = torch.nn.functional.silu(xn2 @ self._weight(l, "gate").T) * (xn2 @ self._weight(l, "up").T)
+            res = res + h @ self._weight(l, "down").T
+        xf = rmsnorm(res[-1], self.final_norm, eps)
+        lm = self.lm if self.pre else self._deq(self.w.lm_head)
+        return lm @ xf
 
     @torch.no_grad()
     def step(self, x: torch.Tensor, pos: int) -> torch.Tensor:

@@ -277,6 +277,28 @@ def test_position_zero_attention_output_is_v():
     assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
 
 
+def test_torch_cpu_prefill_matches_oracle():
+    """The CPU baseline's batched prefill (oracle/torch_cpu.py) equals the
+    oracle's prompt pass (without the float16 activation roundings), in one
+    call and in two chunks, and leaves the cache a following decode step
+    continues from."""
+    import torch
+    from oracle.torch_cpu import TorchDecoder
+    cfg = cf.TINY
+    w = cf.decoder_weights(cfg, norm_mode="unit")
+    od = OracleDecoder(w, round16=False)
+    ids = list(cf.prompt_ids(cfg, 20))
+    want = od.forward(ids, 0)[-1]
+    xs = torch.from_numpy(od.embed_rows(ids).astype(np.float32))
+    td = TorchDecoder(w, cfg.max_context_length)
+    assert normwise(td.prefill(xs, 0).numpy(), want) <= 4 * F32_SUM
+    x = torch.from_numpy(od.embed_rows([7])[0].astype(np.float32))
+    assert normwise(td.step(x, 20).numpy(), od.forward([7], 20)[0]) <= 4 * F32_SUM
+    tc = TorchDecoder(w, cfg.max_context_length)
+    tc.prefill(xs[:12], 0)
+    assert normwise(tc.prefill(xs[12:], 12).numpy(), want) <= 4 * F32_SUM
+
+
 def test_torch_cpu_baseline_matches_oracle():
     """The timed CPU baseline (oracle/torch_cpu.py, float32 torch) computes the
     oracle's decode step (without the float16 activation roundings), both

@@ -42,7 +42,8 @@ def test_config4_gqa_decode(dev, L_):
 @pytest.mark.parametrize("L_,max_ctx,hq,hkv,d", [(1, 8, 4, 2, 64), (77, 128, 16, 8, 128),
                                                  (700, 1024, 8, 8, 128), (3000, 4096, 16, 2, 64),
                                                  (2000, 2048, 16, 4, 128), (104, 104, 16, 8, 128),
-                                                 (99, 104, 8, 8, 128)])
+                                                 (99, 104, 8, 8, 128), (20000, 20000, 2, 1, 128),
+                                                 (9000, 9216, 4, 2, 128)])
 def test_gqa_transposed_v_f16(dev, L_, max_ctx, hq, hkv, d):
     """Reference layout: f16 caches, V transposed [h][d][max_ctx], f16 q/out."""
     rng_q = (0.3 * S.normal(400, hq * d)).astype(np.float16).reshape(hq, d)

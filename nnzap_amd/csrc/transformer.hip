@@ -552,18 +552,16 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
 // and masked by selection (never multiplied), so stale partials cannot
 // leak in.  part_o rows are 16-byte aligned (checked by the launcher); the
 // launcher picks PRE to cover the chunk count (launch_combine).
-template <int D, int PRE, int DS>
+template <int D, int PRE>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
-    // DS blocks per query head, block ds taking dims [ds D / DS, (ds + 1) D / DS)
-    // (every one of them folds the chunks' (m, l) pairs itself)
-    constexpr int NV = D / 4 / DS, PARTS = 256 / NV;
+    constexpr int NV = D / 4, PARTS = 256 / NV;
     __shared__ float red[4];
     __shared__ float4 acc[256];
-    const uint32_t qh = blockIdx.x, z = blockIdx.y / DS, ds = blockIdx.y % DS, tid = threadIdx.x;
+    const uint32_t qh = blockIdx.x, z = blockIdx.y, tid = threadIdx.x;
     const uint32_t dv = tid % NV, p = tid / NV;
     const size_t base = ((size_t)z * a.hq + qh) * a.nchunks;
     const float2 *ml = (const float2 *)(a.part_ml + base * 2);
-    const float4 *po = (const float4 *)(a.part_o + base * D) + ds * NV + dv;
+    const float4 *po = (const float4 *)(a.part_o + base * D) + dv;
     const uint32_t last = a.nchunks - 1;
     const float2 mine = ml[min(tid, last)];
     float2 mlk[PRE];
@@ -572,7 +570,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     for (int k = 0; k < PRE; ++k) {
         const uint32_t c = min(p + (uint32_t)(PARTS * k), last);
         mlk[k] = ml[c];
-        ok[k] = po[(size_t)c * (D / 4)];
+        ok[k] = po[(size_t)c * NV];
     }
     const uint32_t seq = (a.d_seq ? *a.d_seq : a.seq_len) + z;
     const uint32_t nch = min(a.nchunks, ceil_div(seq, a.chunk));
@@ -600,7 +598,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 #pragma unroll 4
     for (uint32_t c = p + PARTS * PRE; c < nch; c += PARTS) {
         const float w = expf(ml[c].x - M);
-        const float4 o = po[(size_t)c * (D / 4)];
+        const float4 o = po[(size_t)c * NV];
         s.x = fmaf(w, o.x, s.x);
         s.y = fmaf(w, o.y, s.y);
         s.z = fmaf(w, o.z, s.z);
@@ -617,7 +615,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
             s.z += o.z;
             s.w += o.w;
         }
-        const size_t ob = (size_t)z * a.o_stride + (size_t)qh * D + 4 * (ds * NV + tid);
+        const size_t ob = (size_t)z * a.o_stride + (size_t)qh * D + 4 * tid;
         store_dt(a.out, ob + 0, s.x / den, a.odt);
         store_dt(a.out, ob + 1, s.y / den, a.odt);
         store_dt(a.out, ob + 2, s.z / den, a.odt);
@@ -1624,16 +1622,16 @@ size_t nnz_attn_scratch_bytes_impl(uint32_t hq, uint32_t head_dim, uint32_t seq_
 
 // The combine step for Hq x nq queries: the preload depth covers the chunks
 // each lane group folds (ceil(nchunks / (256 / (D/4)))), up to 16.
-template <int D, int DS>
-static void launch_combine_ds(nnz_ctx *ctx, const AttnArgs &a, uint32_t nq) {
-    constexpr uint32_t PARTS = 256 / (D / 4 / DS);
+template <int D>
+static void launch_combine_blocks(nnz_ctx *ctx, const AttnArgs &a, uint32_t nq) {
+    constexpr uint32_t PARTS = 256 / (D / 4);
     const uint32_t per = ceil_div(a.nchunks, PARTS);
-    const dim3 grid(a.hq, nq * DS);
-    if (per <= 1) attn_combine_kernel<D, 1, DS><<<grid, 256, 0, ctx->stream>>>(a);
-    else if (per <= 2) attn_combine_kernel<D, 2, DS><<<grid, 256, 0, ctx->stream>>>(a);
-    else if (per <= 4) attn_combine_kernel<D, 4, DS><<<grid, 256, 0, ctx->stream>>>(a);
-    else if (per <= 8) attn_combine_kernel<D, 8, DS><<<grid, 256, 0, ctx->stream>>>(a);
-    else attn_combine_kernel<D, 16, DS><<<grid, 256, 0, ctx->stream>>>(a);
+    const dim3 grid(a.hq, nq);
+    if (per <= 1) attn_combine_kernel<D, 1><<<grid, 256, 0, ctx->stream>>>(a);
+    else if (per <= 2) attn_combine_kernel<D, 2><<<grid, 256, 0, ctx->stream>>>(a);
+    else if (per <= 4) attn_combine_kernel<D, 4><<<grid, 256, 0, ctx->stream>>>(a);
+    else if (per <= 8) attn_combine_kernel<D, 8><<<grid, 256, 0, ctx->stream>>>(a);
+    else attn_combine_kernel<D, 16><<<grid, 256, 0, ctx->stream>>>(a);
 }
 
 // Few chunks: one wave per (query head, query, 64 dims), lane = dim,
@@ -1686,7 +1684,7 @@ static void launch_combine(nnz_ctx *ctx, const AttnArgs &a, uint32_t nq) {
     if (a.nchunks <= 8)
         attn_combine_wave_kernel<D><<<dim3(a.hq, nq * (D / 64)), 64, 0, ctx->stream>>>(a);
     else
-        launch_combine_ds<D, 1>(ctx, a, nq);
+        launch_combine_blocks<D>(ctx, a, nq);
 }
 
 template <int D, int G, int KVDT, bool VT>

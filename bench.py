@@ -497,6 +497,57 @@ def _kernel_cases():
             return us, V * 4, None
         return run
 
+    def stacked(kind):
+        # One launch over `count` independently drawn matrices of a config
+        # shape (>= 64 of them and >= 640 MB in all, so the launch streams
+        # from HBM): the kernel's streaming rate without the per-launch
+        # floor.  HIP events on the library stream around single launches,
+        # best of 5 after a warm-up.
+        def run(dev, n):
+            shp = {"config1": (6144, 2048, 64, 4), "config2": (2048, 6144, 128, 1),
+                   "config3": (6144, 2048, 128, 1)}[kind]
+            M_, K_, gs, bits = shp
+            nmat = 2 if kind == "config3" else 1
+            each = (M_ * K_ * bits // 8 + M_ * K_ // gs * 2 * (2 if bits == 4 else 1)) * nmat
+            count = max(MIN_COPIES, -(-ROTATE_BYTES // each))
+            rng = (0.005, 0.02) if bits == 4 else (0.01, 0.05)
+            sws = [ops.StackedQWeights(dev, M_, K_, gs, bits, count, 900 + i, rng)
+                   for i in range(nmat)]
+            x = torch.randn(count, K_, device="cuda")
+            y = torch.empty(count, M_, device="cuda")
+            if kind == "config1":
+                fn = lambda: ops.dispatch_q4mv_stacked(dev, sws[0], x, y)  # noqa: E731
+            elif kind == "config2":
+                fn = lambda: ops.dispatch_qmv_stacked(dev, sws[0], x, y)  # noqa: E731
+            else:
+                fn = lambda: ops.dispatch_qmv_fused_pair_silu_stacked(dev, sws[0], sws[1], x, y)  # noqa: E731
+            fn()
+            dev.sync()
+            best = None
+            for _ in range(5):
+                dev.mark(0)
+                fn()
+                dev.mark(1)
+                ms = dev.elapsed_ms(0, 1)
+                best = ms if best is None else min(best, ms)
+            nbytes = count * (each + K_ * 4 + M_ * 4)
+            del sws
+            return best * 1000.0, nbytes, None, None, {"matrices": count,
+                                                       "us_per_matrix": round(best * 1000.0 / count, 3)}
+        return run
+
+    def cores(case, value):
+        # the same case with NNZ_OPT_Q1_MATRIX_CORES forced (1: the
+        # block-scaled MFMA 1-bit kernel wherever it applies, 2: never)
+        def run(dev, n):
+            dev.call("nnz_ctx_set_option", L.OPT_Q1_MATRIX_CORES, value)
+            try:
+                r = case(dev, n)   # an A/B variant: not a launch of the decode step
+                return (r[0], r[1], None) + tuple(r[3:])
+            finally:
+                dev.call("nnz_ctx_set_option", L.OPT_Q1_MATRIX_CORES, 0)
+        return run
+
     def copy_calib(dev, n):
         # a plain device copy of known size: the scale for FETCH/WRITE_SIZE
         a = torch.ones(64 << 20, dtype=f32, device="cuda")
@@ -521,6 +572,12 @@ def _kernel_cases():
         "floor_residual_add": floor_small,
         "config4_attention_L512": config4(512), "config4_attention_L4096": config4(4096),
         "config4_attention_L32768": config4(32768), "copy_256MiB": copy_calib,
+        "stacked_config1_q4mv": stacked("config1"), "stacked_config2_qmv": stacked("config2"),
+        "stacked_config3_gate_up_silu": stacked("config3"),
+        "stacked_config3_gate_up_silu_valu": cores(stacked("config3"), 2),
+        "dec_lm_head_norm_valu": cores(dec_lm_head, 2),
+        "config3_gate_up_silu_mfma": cores(config3, 1),
+        "dec_gate_up_norm_silu_mfma": cores(dec_gate_up, 1),
         "prefill_gemm_q": prefill_gemm(QD, H, L.GEMM_STORE_F16),
         "prefill_gemm_kv": prefill_gemm(KVD, H, L.GEMM_STORE_F16),
         "prefill_gemm_o_resadd": prefill_gemm(H, QD, L.GEMM_RESADD),
@@ -540,14 +597,14 @@ def bench_kernels(dev, quick=False, only=None):
 
     n_iter = 64 if quick else 256
     cases = _kernel_cases()
-    names = [n for n in cases if n != "copy_256MiB"] if not only else only.split(",")
+    names = list(cases) if not only else only.split(",")
     res = {}
     for name in names:
         r = cases[name](dev, n_iter)
         us, nbytes, per_token = r[:3]
         torch.cuda.synchronize()
         gbs = nbytes / (us * 1e-6) / 1e9
-        if len(r) > 3:   # MFMA-bound: FLOP/s against the dense f16 peak
+        if len(r) > 3 and r[3] is not None:   # MFMA-bound: FLOP/s against the dense f16 peak
             tf = r[3] / (us * 1e-6) / 1e12
             res[name] = {"us": round(us, 3), "flops": int(r[3]), "TFLOPs": round(tf, 1),
                          "frac": round(tf / PEAK_F16_TFLOPS, 4)}
@@ -557,6 +614,8 @@ def bench_kernels(dev, quick=False, only=None):
                      "frac": round(gbs / PEAK_HBM_GBS, 4)}
         if per_token is not None:
             res[name]["per_token"] = per_token
+        if len(r) > 4:
+            res[name].update(r[4])
         log(f"{name:28s} {us:8.2f} us  {gbs:8.1f} GB/s  ({nbytes} B)")
     return res
 
@@ -834,6 +893,8 @@ def main():
             "lm_head_kernel": kern.get("dec_lm_head_tied"),
             "workload": "config 5 with the tied bf16 embedding table as LM head (622 MB/token)"},
         "qmv": {k: v for k, v in kern.items() if k.startswith("config")},
+        "qmv_stacked": {k: v for k, v in kern.items() if k.startswith("stacked_")},
+        "copy_ceiling": kern.get("copy_256MiB"),
         "prefill_gemm": {k: v for k, v in kern.items() if k.startswith("prefill_gemm")},
         "decode_kernels": dec_k,
     }

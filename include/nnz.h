@@ -134,6 +134,15 @@ int nnz_graph_end(nnz_ctx *ctx, nnz_graph **out);
 int nnz_graph_replay(nnz_ctx *ctx, nnz_graph *g);
 int nnz_graph_destroy(nnz_graph *g);
 
+/* Context options (new; the reference has no counterpart).
+ * NNZ_OPT_Q1_MATRIX_CORES selects the kernel of 1-bit QMVs with K = 2048 and
+ * group size 128: 0 = the library's choice by shape (default), 1 = the
+ * block-scaled MFMA kernel wherever it applies, 2 = never it (the VALU
+ * kernels).  Results agree to float32 rounding either way; a captured graph
+ * keeps the kernels chosen at capture. */
+#define NNZ_OPT_Q1_MATRIX_CORES 1
+int nnz_ctx_set_option(nnz_ctx *ctx, int option, int value);
+
 /* Device-side timing on the ctx stream (HIP events). */
 int nnz_timer_mark(nnz_ctx *ctx, int slot);           /* slot 0..63 */
 int nnz_timer_elapsed_ms(nnz_ctx *ctx, int slot_a, int slot_b, float *ms);
@@ -246,6 +255,32 @@ int nnz_dispatch_q4_fused_norm_pair_silu_f16io(nnz_ctx *ctx, const nnz_qweight *
                                                const nnz_qweight *wb, const float *residual,
                                                void *output, const float *norm_scale,
                                                nnz_qmv_dims dims);
+
+/* ---- stacked QMV: many matrices of one shape in one launch ---------------
+ * New (the reference has no counterpart; the arithmetic is that of
+ * dispatchQMV transformer.zig:1565, dispatchQ4MV :1895 and
+ * dispatchQMVFusedPairSiLUf16io :1304 with f32 input and output).  Matrix i
+ * (0 <= i < count) has its codes, scales (and biases) at i * codes_stride /
+ * i * scales_stride bytes past those of `w` (a pair: `wa` and `wb` advance
+ * together), its input at i * input_stride and its output at
+ * i * output_stride bytes past `input` / `output`.  One launch streams them
+ * all: the stacked-launch form of an HBM-bandwidth measurement and a
+ * batched decode of independent matrices.  Strides keep 16-byte alignment
+ * (codes, inputs) and 4-byte alignment (scales, outputs).
+ * blocks_per_matrix 0 lets the library choose. */
+typedef struct {
+    uint32_t count;
+    uint32_t blocks_per_matrix;
+    uint64_t codes_stride, scales_stride, input_stride, output_stride;
+} nnz_qmv_stack;
+int nnz_dispatch_qmv_stacked(nnz_ctx *ctx, const nnz_qweight *w, const float *input,
+                             float *output, nnz_qmv_dims dims, const nnz_qmv_stack *stack);
+int nnz_dispatch_q4mv_stacked(nnz_ctx *ctx, const nnz_qweight *w, const float *input,
+                              float *output, nnz_qmv_dims dims, const nnz_qmv_stack *stack);
+int nnz_dispatch_qmv_fused_pair_silu_stacked(nnz_ctx *ctx, const nnz_qweight *wa,
+                                             const nnz_qweight *wb, const float *input,
+                                             float *output, nnz_qmv_dims dims,
+                                             const nnz_qmv_stack *stack);
 
 /* ---- dequantisation (bit-exact artefact) -------------------------------- */
 /* New (no reference kernel; the math of transformer.metal:469-480 / :537-545):

@@ -19,6 +19,7 @@ GEMM_STORE_F16, GEMM_STORE_F32, GEMM_RESADD, GEMM_SILU_PAIR = 0, 1, 2, 3
 GQA_NOALLOC_MAX_BYTES = 8 << 20   # NNZ_GQA_NOALLOC_MAX_BYTES
 EMBED_Q1, EMBED_BF16, EMBED_Q4 = 0, 1, 2
 LMHEAD_Q1, LMHEAD_TIED_BF16, LMHEAD_Q4 = 0, 1, 2
+OPT_Q1_MATRIX_CORES = 1
 QUANT_FORMAT_Q1, QUANT_FORMAT_Q4 = 0, 1
 
 u32, f32, vp, i32, sz = C.c_uint32, C.c_float, C.c_void_p, C.c_int32, C.c_size_t
@@ -77,6 +78,13 @@ class QWeightDesc(C.Structure):
                 ("group_size", u32), ("bits", u32), ("scale_dtype", u32)]
 
 
+class QmvStack(C.Structure):
+    """nnz_qmv_stack: `count` matrices at fixed byte strides (stacked launch)."""
+    _fields_ = [("count", u32), ("blocks_per_matrix", u32), ("codes_stride", C.c_uint64),
+                ("scales_stride", C.c_uint64), ("input_stride", C.c_uint64),
+                ("output_stride", C.c_uint64)]
+
+
 class SamplingParams(C.Structure):
     """nnz_sampling_params (SamplingParams, transformer.zig:3652-3657)."""
     _fields_ = [("temperature", f32), ("top_k", u32), ("top_p", f32), ("reserved", u32),
@@ -110,6 +118,7 @@ PROTOS = {
     "nnz_graph_end": (C.c_int, [vp, P(vp)]),
     "nnz_graph_replay": (C.c_int, [vp, vp]),
     "nnz_graph_destroy": (C.c_int, [vp]),
+    "nnz_ctx_set_option": (C.c_int, [vp, C.c_int, C.c_int]),
     "nnz_timer_mark": (C.c_int, [vp, C.c_int]),
     "nnz_timer_elapsed_ms": (C.c_int, [vp, C.c_int, C.c_int, P(f32)]),
     # Q1
@@ -138,6 +147,11 @@ PROTOS = {
     "nnz_dispatch_q4_fused_norm_qmv_f16io": (C.c_int, [vp, QW, vp, vp, vp, QMVDims]),
     "nnz_dispatch_q4_fused_norm_pair_qmv_f16io": (C.c_int, [vp, QW, QW, vp, vp, vp, vp, QMVDims]),
     "nnz_dispatch_q4_fused_norm_pair_silu_f16io": (C.c_int, [vp, QW, QW, vp, vp, vp, QMVDims]),
+    # stacked
+    "nnz_dispatch_qmv_stacked": (C.c_int, [vp, QW, vp, vp, QMVDims, P(QmvStack)]),
+    "nnz_dispatch_q4mv_stacked": (C.c_int, [vp, QW, vp, vp, QMVDims, P(QmvStack)]),
+    "nnz_dispatch_qmv_fused_pair_silu_stacked": (C.c_int, [vp, QW, QW, vp, vp, QMVDims,
+                                                           P(QmvStack)]),
     # dequant / gemm
     "nnz_dispatch_dequant": (C.c_int, [vp, QW, vp, QMVDims]),
     "nnz_dispatch_dequant_gemm": (C.c_int, [vp, QW, QW, vp, u32, vp, C.c_int, QMVDims]),

@@ -15,6 +15,7 @@ struct nnz_ctx {
     hipStream_t stream = nullptr;
     bool own_stream = false;
     bool capturing = false;
+    int q1_matrix_cores = 0;   // NNZ_OPT_Q1_MATRIX_CORES
     std::string err;
     hipEvent_t ev[64] = {};
     bool ev_ok[64] = {};

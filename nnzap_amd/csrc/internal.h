@@ -130,3 +130,25 @@ int nnz_attn_prep_waves_launch(nnz_ctx *ctx, const void *q, const void *kr, cons
 // the f16 A operand, each written to its own f16 output [P][rows] (gemm.hip).
 int nnz_gemm_segments_launch(nnz_ctx *ctx, const nnz_qweight *const *w, void *const *out, int nw,
                              const void *a, uint32_t P, uint32_t K, uint32_t group_size);
+
+// 1-bit QMV on the block-scaled matrix cores (qmv_mfma.hip): K = 2048, group
+// size 128.  nmat 2 = a pair sharing the input with the SiLU epilogue.
+// xdt / odt: NNZ_F32 / NNZ_F16 / NNZ_BF16; xin 0 = x as given, 1 = RMSNorm
+// of the f32 residual `x` with `norm_w` (f16-rounded); epi 0 = store,
+// 1 = residual +=, 2 = silu(a) * b.  Stacked launch: stack_count matrices at
+// the byte strides cs (codes), ss (scales), xs (inputs), os (outputs).
+struct NnzQ1Mfma {
+    const void *codes[2] = {nullptr, nullptr};
+    const void *scales[2] = {nullptr, nullptr};
+    const void *x = nullptr;
+    const float *norm_w = nullptr;
+    void *out = nullptr;
+    uint32_t M = 0, K = 0, group_size = 0, nmat = 1;
+    int xdt = NNZ_F32, xin = 0, epi = 0, odt = NNZ_F32;
+    float eps = 1e-6f;
+    uint32_t stack_count = 1, blocks_per_matrix = 0;
+    uint64_t cs = 0, ss = 0, xs = 0, os = 0;
+};
+bool nnz_q1_mfma_supported(uint32_t K, uint32_t group_size);
+bool nnz_q1_mfma_has_variant(const NnzQ1Mfma &c);
+int nnz_q1_mfma_launch(nnz_ctx *ctx, const NnzQ1Mfma &c);

@@ -64,6 +64,13 @@ struct QmvMat {
     uint32_t seg_end;      // NMAT == 1: one past the segment's last row
 };
 
+// Stacked launch (gridDim.y > 1): block row y works on matrix y, whose
+// codes, scales (and biases), input and output lie these many bytes past
+// matrix 0's.  All zero for an ordinary launch.
+struct StackArgs {
+    uint64_t codes, scales, x, out;
+};
+
 struct QmvArgs {
     // NMAT == 2: matrices m0 and m1 share rows [0, M).  NMAT == 1: rows are
     // the concatenation of `nseg` segments, segment s = rows
@@ -79,8 +86,16 @@ struct QmvArgs {
     uint32_t lpr_log2;     // lanes per row = 1 << lpr_log2
     uint32_t sdt;          // scale/bias dtype (NNZ_F16 / NNZ_BF16)
     float eps;
+    StackArgs stk;
 };
 
+// Pointer `p` of matrix blockIdx.y of a stacked launch (`stride` bytes
+// between matrices; 0 for an ordinary launch).  The argument block itself
+// is never modified: a modified copy of it would live in scratch memory.
+template <class T>
+__device__ __forceinline__ T *stk(T *p, uint64_t stride) {
+    return (T *)((uintptr_t)p + (uint64_t)blockIdx.y * stride);
+}
 // Weight registers of one row-step.
 template <int NMAT, int R, int NV, int VEC>
 struct StepRegs {
@@ -149,10 +164,10 @@ struct SegPtrs {
 
 __device__ __forceinline__ SegPtrs seg_mat(const QmvArgs &a, int seg) {
     SegPtrs r;
-    r.codes = pick3(seg, a.m0.codes, a.m1.codes, a.m2.codes);
-    r.scales = pick3(seg, a.m0.scales, a.m1.scales, a.m2.scales);
-    r.biases = pick3(seg, a.m0.biases, a.m1.biases, a.m2.biases);
-    r.out = pick3(seg, a.m0.out, a.m1.out, a.m2.out);
+    r.codes = stk(pick3(seg, a.m0.codes, a.m1.codes, a.m2.codes), a.stk.codes);
+    r.scales = stk(pick3(seg, a.m0.scales, a.m1.scales, a.m2.scales), a.stk.scales);
+    r.biases = stk(pick3(seg, a.m0.biases, a.m1.biases, a.m2.biases), a.stk.scales);
+    r.out = stk(pick3(seg, a.m0.out, a.m1.out, a.m2.out), a.stk.out);
     return r;
 }
 
@@ -184,11 +199,11 @@ __device__ __forceinline__ void load_step(const QmvArgs &a, StepRegs<NMAT, R, NV
         cp[0] = sm.codes; sp[0] = sm.scales; bp[0] = sm.biases;
         outp = sm.out;
     } else {
-        cp[0] = uniform_ptr(a.m0.codes); sp[0] = uniform_ptr(a.m0.scales);
-        bp[0] = uniform_ptr(a.m0.biases);
-        cp[NMAT - 1] = uniform_ptr(mat_of<NMAT - 1>(a).codes);
-        sp[NMAT - 1] = uniform_ptr(mat_of<NMAT - 1>(a).scales);
-        bp[NMAT - 1] = uniform_ptr(mat_of<NMAT - 1>(a).biases);
+        cp[0] = stk(uniform_ptr(a.m0.codes), a.stk.codes); sp[0] = stk(uniform_ptr(a.m0.scales), a.stk.scales);
+        bp[0] = stk(uniform_ptr(a.m0.biases), a.stk.scales);
+        cp[NMAT - 1] = stk(uniform_ptr(mat_of<NMAT - 1>(a).codes), a.stk.codes);
+        sp[NMAT - 1] = stk(uniform_ptr(mat_of<NMAT - 1>(a).scales), a.stk.scales);
+        bp[NMAT - 1] = stk(uniform_ptr(mat_of<NMAT - 1>(a).biases), a.stk.scales);
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -275,20 +290,22 @@ __device__ __forceinline__ void load_step_full(const QmvArgs &a, StepRegs<NMAT, 
         auto sel = [&](const void *p0, const void *p1, const void *p2) {
             return seg == 0 ? p0 : (seg == 1 ? p1 : p2);
         };
-        cr[0] = weight_rsrc(sel(a.m0.codes, a.m1.codes, a.m2.codes));
-        sr[0] = weight_rsrc(sel(a.m0.scales, a.m1.scales, a.m2.scales));
-        br[0] = weight_rsrc(sel(a.m0.biases, a.m1.biases, a.m2.biases));
+        cr[0] = weight_rsrc(stk(sel(a.m0.codes, a.m1.codes, a.m2.codes), a.stk.codes));
+        sr[0] = weight_rsrc(stk(sel(a.m0.scales, a.m1.scales, a.m2.scales), a.stk.scales));
+        br[0] = weight_rsrc(stk(sel(a.m0.biases, a.m1.biases, a.m2.biases), a.stk.scales));
     } else {
-        cr[0] = weight_rsrc(a.m0.codes); sr[0] = weight_rsrc(a.m0.scales); br[0] = weight_rsrc(a.m0.biases);
-        cr[NMAT - 1] = weight_rsrc(mat_of<NMAT - 1>(a).codes);
-        sr[NMAT - 1] = weight_rsrc(mat_of<NMAT - 1>(a).scales);
-        br[NMAT - 1] = weight_rsrc(mat_of<NMAT - 1>(a).biases);
+        cr[0] = weight_rsrc(stk(a.m0.codes, a.stk.codes));
+        sr[0] = weight_rsrc(stk(a.m0.scales, a.stk.scales));
+        br[0] = weight_rsrc(stk(a.m0.biases, a.stk.scales));
+        cr[NMAT - 1] = weight_rsrc(stk(mat_of<NMAT - 1>(a).codes, a.stk.codes));
+        sr[NMAT - 1] = weight_rsrc(stk(mat_of<NMAT - 1>(a).scales, a.stk.scales));
+        br[NMAT - 1] = weight_rsrc(stk(mat_of<NMAT - 1>(a).biases, a.stk.scales));
     }
     const uint32_t lr = rb - seg_start;
     const uint32_t co = lr * words_per_row * 4u, so = lr * G * 2u;
     if constexpr (RES) {
         static_assert(NMAT == 1, "residual add has one matrix");
-        s.res[0] = *(gptr<const float>)((gptr<const char>)uniform_ptr(a.m0.out) + (size_t)rb * 4u + fo.res);
+        s.res[0] = *(gptr<const float>)((gptr<const char>)stk(uniform_ptr(a.m0.out), a.stk.out) + (size_t)rb * 4u + fo.res);
     }
 #pragma unroll
     for (int m = 0; m < NMAT; ++m)
@@ -323,7 +340,7 @@ __device__ __forceinline__ void qmv_epilogue(const QmvArgs &a, void *out0, uint3
             for (int m = 0; m < NMAT; ++m) {
                 float v = tot[m];
                 if constexpr (FAITH) v = bf16_trunc(v);
-                store_from_f32<ODT>(m == 0 ? a.m0.out : a.m1.out, row, v);
+                store_from_f32<ODT>(stk(m == 0 ? a.m0.out : a.m1.out, a.stk.out), row, v);
             }
         }
     } else if constexpr (EPI == EPI_RESADD) {
@@ -343,6 +360,7 @@ __device__ __forceinline__ void qmv_epilogue(const QmvArgs &a, void *out0, uint3
 template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH, int NV, int R, bool LUT,
           bool FULL>
 __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
+    const void *const ax = stk(a.x, a.stk.x);
     static_assert(!LUT || BITS == 1, "nibble tables are for 1-bit weights");
     static_assert(!LUT || FULL, "nibble tables need whole-wave rows");
     constexpr bool NORM = XIN == XIN_NORM;
@@ -429,7 +447,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
         float v[NV][2][4];
         if constexpr (NORM) {
             __shared__ float red[4];
-            const float4 *res4 = (const float4 *)a.x;
+            const float4 *res4 = (const float4 *)ax;
             const float4 *nw4 = (const float4 *)a.norm_w;
             float4 rv[NV][2], wv[NV][2];
 #pragma unroll
@@ -478,8 +496,8 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
 #pragma unroll
                 for (int sb = 0; sb < 2; ++sb) {
                     const uint32_t i4 = uvalid[j] ? (uint32_t)(lane + 64 * j) * 8u + 2u * wid + sb : 0u;
-                    if constexpr (XDT == NNZ_F32) xf[j][sb] = ((const float4 *)a.x)[i4];
-                    else xh[j][sb] = ((const uint2 *)a.x)[i4];
+                    if constexpr (XDT == NNZ_F32) xf[j][sb] = ((const float4 *)ax)[i4];
+                    else xh[j][sb] = ((const uint2 *)ax)[i4];
                 }
             first_weights();
 #pragma unroll
@@ -525,7 +543,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
         constexpr int P4 = 2 * NV;
         __shared__ __align__(16) f16_t xs[2048 * NV];
         __shared__ float red[4];
-        const float4 *res4 = (const float4 *)a.x;
+        const float4 *res4 = (const float4 *)ax;
         const float4 *nw4 = (const float4 *)a.norm_w;
         const uint32_t n4 = K / 4;
         float4 rv[P4], wv[P4];
@@ -757,8 +775,8 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const uint32_t u = uvalid[j] ? (uint32_t)ll + (uint32_t)(LPR * j) : 0u;
-            const uint4 *p = XDT == NNZ_F32 ? (const uint4 *)((const float *)a.x + (size_t)u * 32)
-                                            : (const uint4 *)((const uint16_t *)a.x + (size_t)u * 32);
+            const uint4 *p = XDT == NNZ_F32 ? (const uint4 *)((const float *)ax + (size_t)u * 32)
+                                            : (const uint4 *)((const uint16_t *)ax + (size_t)u * 32);
 #pragma unroll
             for (int i = 0; i < XV; ++i) xraw[j][i] = p[i];
         }
@@ -886,7 +904,8 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
         uint32_t seg_start = 0;
         int seg = 0;
         if constexpr (NMAT == 1) seg = step_segment(a, rb, seg_start);
-        void *out0 = NMAT == 1 ? (seg == 0 ? a.m0.out : (seg == 1 ? a.m1.out : a.m2.out)) : a.m0.out;
+        void *out0 = stk(NMAT == 1 ? (seg == 0 ? a.m0.out : (seg == 1 ? a.m1.out : a.m2.out)) : a.m0.out,
+                         a.stk.out);
         if constexpr (FULL) {
             // The NMAT x R row totals in one exchange-halving reduction
             // (slot r * NMAT + m); the lanes heading each slot's lane group
@@ -943,13 +962,14 @@ template <int XDT, int EPI, int ODT, int KS, int R>
 __global__ __launch_bounds__(64 * KS) void qmv1_splitk_kernel(QmvArgs a) {
     static_assert(EPI == EPI_STORE || EPI == EPI_RESADD, "store or residual add");
     const int lane = threadIdx.x & 63, kp = threadIdx.x >> 6;
+    const void *const ax = stk(a.x, a.stk.x);
     const uint32_t K = a.K, units = K >> 5, G = K / a.gs, M = a.M;
     const uint32_t u = (uint32_t)(kp * 64 + lane);
     const bool uv = u < units;
     const uint32_t uc = uv ? u : 0u;
-    const gptr<const uint32_t> codes = uniform_ptr(a.m0.codes);
-    const gptr<const uint16_t> scales = uniform_ptr(a.m0.scales);
-    float *const out = (float *)a.m0.out;
+    const gptr<const uint32_t> codes = stk(uniform_ptr(a.m0.codes), a.stk.codes);
+    const gptr<const uint16_t> scales = stk(uniform_ptr(a.m0.scales), a.stk.scales);
+    float *const out = stk((float *)a.m0.out, a.stk.out);
     __shared__ float part[2][KS][R];
 
     struct Step { uint32_t cw[R]; uint16_t sc[R]; float prev; };
@@ -976,8 +996,8 @@ __global__ __launch_bounds__(64 * KS) void qmv1_splitk_kernel(QmvArgs a) {
     constexpr int XV = XDT == NNZ_F32 ? 8 : 4;
     uint4 xraw[XV];
     {
-        const uint4 *p = XDT == NNZ_F32 ? (const uint4 *)((const float *)a.x + (size_t)uc * 32)
-                                        : (const uint4 *)((const uint16_t *)a.x + (size_t)uc * 32);
+        const uint4 *p = XDT == NNZ_F32 ? (const uint4 *)((const float *)ax + (size_t)uc * 32)
+                                        : (const uint4 *)((const uint16_t *)ax + (size_t)uc * 32);
 #pragma unroll
         for (int i = 0; i < XV; ++i) xraw[i] = p[i];
     }
@@ -1069,11 +1089,31 @@ __global__ __launch_bounds__(64 * KS) void qmv1_splitk_kernel(QmvArgs a) {
             const uint32_t row = base + (uint32_t)lane;
             if (row < M) {
                 if constexpr (EPI == EPI_RESADD) out[row] = cur.prev + t;
-                else store_from_f32<ODT>(a.m0.out, row, t);
+                else store_from_f32<ODT>(out, row, t);
             }
         }
         cur = nxt;
     }
+}
+
+// Whether a 1-bit QMV of this shape goes to the block-scaled MFMA kernel:
+// the context's NNZ_OPT_Q1_MATRIX_CORES, by default for stacked launches
+// only, where its per-block set-up (a 64 KB fp4 table, the input's digit
+// rows) is amortised over many rows (measured, stacked config-3 pairs: 168
+// against 203 us; the 1-bit LM head, ~4.6 tiles per wave: 16.4 against
+// 14.5 us, so it stays on the VALU kernel).
+bool q1_matrix_cores_wanted(nnz_ctx *ctx, const nnz_qmv_dims &d, bool stacked) {
+    if (!nnz_q1_mfma_supported(d.K, d.group_size) || ctx->q1_matrix_cores == 2) return false;
+    return ctx->q1_matrix_cores == 1 || stacked;
+}
+
+// Blocks per matrix of a stacked launch: the caller's choice, else enough
+// for about 2048 blocks in all (every block amortises its prologue -- the
+// input slice or the nibble tables -- over many rows), never more than a
+// single launch of the shape would use.
+uint32_t stack_blocks(const nnz_qmv_stack *stk, uint32_t single) {
+    uint32_t b = stk->blocks_per_matrix ? stk->blocks_per_matrix : ceil_div(2048u, stk->count);
+    return b < 1 ? 1 : (b > single ? single : b);
 }
 
 int check_weight(nnz_ctx *ctx, const nnz_qweight *w, int bits, uint32_t M, const nnz_qmv_dims &d,
@@ -1119,8 +1159,8 @@ constexpr int LUT_MAX_NV = 3;
 constexpr int step_words(int BITS, int NMAT, int NV, int R) { return NMAT * R * NV * (BITS == 1 ? 1 : 4); }
 
 template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH, int NV, bool LUT, bool FULL>
-void launch_r(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks) {
-    dim3 grid(blocks), block(256);
+void launch_r(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks, uint32_t gy) {
+    dim3 grid(blocks, gy), block(256);
 #define QK(RR) qmv_kernel<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, RR, LUT, FULL><<<grid, block, 0, ctx->stream>>>(a)
     if (R == 8) {
         // long matrices only (the 1-bit LM head): more rows in flight per wave
@@ -1139,7 +1179,7 @@ void launch_r(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks) {
 }
 
 template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH, int NV>
-int launch_nv(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks, bool lut) {
+int launch_nv(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks, bool lut, uint32_t gy) {
     if constexpr (XIN == XIN_MERGE && NV > 2) {
         // the merge prologue keeps every chunk's partials in registers
         return nnz_fail(ctx, NNZ_EUNSUPPORTED, "merge_o_resadd: K > 4096");
@@ -1147,13 +1187,13 @@ int launch_nv(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks, bool lut) 
         // rows narrower than a wave (K < 2048) occur only with one unit per lane
         const bool full = a.lpr_log2 == 6;
         if constexpr (BITS == 1 && NV <= LUT_MAX_NV) {
-            if (lut) launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, true, true>(ctx, a, R, blocks);
-            else if (full) launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false, true>(ctx, a, R, blocks);
-            else if constexpr (NV == 1) launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false, false>(ctx, a, R, blocks);
+            if (lut) launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, true, true>(ctx, a, R, blocks, gy);
+            else if (full) launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false, true>(ctx, a, R, blocks, gy);
+            else if constexpr (NV == 1) launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false, false>(ctx, a, R, blocks, gy);
         } else if (full) {
-            launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false, true>(ctx, a, R, blocks);
+            launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false, true>(ctx, a, R, blocks, gy);
         } else if constexpr (NV == 1) {
-            launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false, false>(ctx, a, R, blocks);
+            launch_r<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, false, false>(ctx, a, R, blocks, gy);
         }
         NNZ_LAUNCHED(ctx);
         return NNZ_OK;
@@ -1165,12 +1205,25 @@ int launch_nv(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks, bool lut) 
 template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH>
 int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg_rows, int nw,
                   const void *x, const float *norm_w, void *const *out, nnz_qmv_dims d,
-                  const char *name, const MergeIn *merge = nullptr, float eps = 1e-6f) {
+                  const char *name, const MergeIn *merge = nullptr, float eps = 1e-6f,
+                  const nnz_qmv_stack *stk = nullptr) {
     constexpr bool NORM = XIN == XIN_NORM;
     constexpr bool MERGE = XIN == XIN_MERGE;
     NNZ_CHECK_CTX(ctx);
     int rc = check_dims(ctx, d, name);
     if (rc) return rc;
+    // Stacked launch: `count` matrices of this shape at fixed byte strides,
+    // one block row each (x and the outputs advance by their own strides).
+    const uint32_t gy = stk ? stk->count : 1u;
+    if (stk) {
+        NNZ_REQUIRE(ctx, !MERGE && !NORM && nw == 1 + (NMAT == 2), NNZ_EUNSUPPORTED,
+                    "%s: stacking takes one matrix or a pair with a plain input", name);
+        NNZ_REQUIRE(ctx, stk->count >= 1 && stk->count <= 65535, NNZ_EINVAL,
+                    "%s: stack count %u (1..65535)", name, stk->count);
+        NNZ_REQUIRE(ctx, stk->codes_stride % 16 == 0 && stk->scales_stride % 4 == 0 &&
+                             stk->input_stride % 16 == 0 && stk->output_stride % 4 == 0,
+                    NNZ_EINVAL, "%s: stack strides must keep the 16/4/16/4-byte alignments", name);
+    }
     uint32_t total = 0;
     for (int i = 0; i < nw; ++i) {
         const uint32_t rows = NMAT == 1 ? seg_rows[i] : d.M;
@@ -1204,6 +1257,38 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
                     "%s: norm_scale must be 16-byte aligned", name);
     }
 
+    // 1-bit rows of K = 2048, group size 128: the block-scaled MFMA kernel
+    // (qmv_mfma.hip) where the context's policy picks it.
+    if constexpr (BITS == 1 && !FAITH && !MERGE) {
+        if (q1_matrix_cores_wanted(ctx, d, stk != nullptr) && (NMAT == 2 || nw == 1)) {
+            NnzQ1Mfma c;
+            for (int i = 0; i < NMAT; ++i) {
+                c.codes[i] = w[i]->codes;
+                c.scales[i] = w[i]->scales;
+            }
+            c.x = x;
+            c.norm_w = norm_w;
+            c.out = out[0];
+            c.M = d.M;
+            c.K = d.K;
+            c.group_size = d.group_size;
+            c.nmat = NMAT;
+            c.xdt = XDT;
+            c.xin = NORM ? 1 : 0;
+            c.epi = EPI == EPI_STORE ? 0 : (EPI == EPI_RESADD ? 1 : 2);
+            c.odt = ODT;
+            c.eps = eps;
+            if (stk) {
+                c.stack_count = stk->count;
+                c.blocks_per_matrix = stk->blocks_per_matrix;
+                c.cs = stk->codes_stride;
+                c.ss = stk->scales_stride;
+                c.xs = stk->input_stride;
+                c.os = stk->output_stride;
+            }
+            if (nnz_q1_mfma_has_variant(c)) return nnz_q1_mfma_launch(ctx, c);
+        }
+    }
     const uint32_t units = d.K / 32;
     uint32_t lpr = 1;
     while (lpr < units && lpr < 64) lpr <<= 1;
@@ -1232,14 +1317,19 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
             a.sdt = w[0]->scale_dtype;
             uint32_t blocks = ceil_div(d.M, (uint32_t)SR);
             if (blocks > 4096) blocks = 4096;
+            if (stk) {
+                a.stk = {stk->codes_stride, stk->scales_stride, stk->input_stride, stk->output_stride};
+                blocks = stack_blocks(stk, blocks);
+            }
+            const dim3 grid(blocks, gy);
             switch (nv) {
-            case 2: qmv1_splitk_kernel<XDT, EPI, ODT, 2, SR><<<blocks, 128, 0, ctx->stream>>>(a); break;
-            case 3: qmv1_splitk_kernel<XDT, EPI, ODT, 3, SR><<<blocks, 192, 0, ctx->stream>>>(a); break;
-            case 4: qmv1_splitk_kernel<XDT, EPI, ODT, 4, SR><<<blocks, 256, 0, ctx->stream>>>(a); break;
-            case 5: qmv1_splitk_kernel<XDT, EPI, ODT, 5, SR><<<blocks, 320, 0, ctx->stream>>>(a); break;
-            case 6: qmv1_splitk_kernel<XDT, EPI, ODT, 6, SR><<<blocks, 384, 0, ctx->stream>>>(a); break;
-            case 7: qmv1_splitk_kernel<XDT, EPI, ODT, 7, SR><<<blocks, 448, 0, ctx->stream>>>(a); break;
-            default: qmv1_splitk_kernel<XDT, EPI, ODT, 8, SR><<<blocks, 512, 0, ctx->stream>>>(a); break;
+            case 2: qmv1_splitk_kernel<XDT, EPI, ODT, 2, SR><<<grid, 128, 0, ctx->stream>>>(a); break;
+            case 3: qmv1_splitk_kernel<XDT, EPI, ODT, 3, SR><<<grid, 192, 0, ctx->stream>>>(a); break;
+            case 4: qmv1_splitk_kernel<XDT, EPI, ODT, 4, SR><<<grid, 256, 0, ctx->stream>>>(a); break;
+            case 5: qmv1_splitk_kernel<XDT, EPI, ODT, 5, SR><<<grid, 320, 0, ctx->stream>>>(a); break;
+            case 6: qmv1_splitk_kernel<XDT, EPI, ODT, 6, SR><<<grid, 384, 0, ctx->stream>>>(a); break;
+            case 7: qmv1_splitk_kernel<XDT, EPI, ODT, 7, SR><<<grid, 448, 0, ctx->stream>>>(a); break;
+            default: qmv1_splitk_kernel<XDT, EPI, ODT, 8, SR><<<grid, 512, 0, ctx->stream>>>(a); break;
             }
             NNZ_LAUNCHED(ctx);
             return NNZ_OK;
@@ -1290,6 +1380,7 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
         while (R > 1 && d.M < (uint32_t)R) R >>= 1;
         blocks = ceil_div(d.M, 4u * R * rpw);
     }
+    if (stk) blocks = stack_blocks(stk, blocks);
     // measured: tables pay off from 4 row-units per wave (fused Q/K/V, 4
     // rows per wave: 3.55 us without, 3.16 us with)
     if (lut && ceil_div(d.M, blocks * 4u) * NMAT < 4u && !MERGE) lut = false;
@@ -1317,11 +1408,12 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
     a.lpr_log2 = (uint32_t)lpr_log2;
     a.sdt = w[0]->scale_dtype;
     a.eps = eps;
+    if (stk) a.stk = {stk->codes_stride, stk->scales_stride, stk->input_stride, stk->output_stride};
     switch (nv) {
-    case 1: return launch_nv<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, 1>(ctx, a, R, blocks, lut);
-    case 2: return launch_nv<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, 2>(ctx, a, R, blocks, lut);
-    case 3: return launch_nv<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, 3>(ctx, a, R, blocks, lut);
-    default: return launch_nv<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, 4>(ctx, a, R, blocks, lut);
+    case 1: return launch_nv<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, 1>(ctx, a, R, blocks, lut, gy);
+    case 2: return launch_nv<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, 2>(ctx, a, R, blocks, lut, gy);
+    case 3: return launch_nv<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, 3>(ctx, a, R, blocks, lut, gy);
+    default: return launch_nv<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, 4>(ctx, a, R, blocks, lut, gy);
     }
 }
 
@@ -1518,6 +1610,41 @@ int nnz_dispatch_fused_norm_qmv_f16in(nnz_ctx *ctx, const nnz_qweight *w, const 
     NNZ_CHECK_CTX(ctx);
     NNZ_REQUIRE(ctx, w && w->bits == 1, NNZ_EINVAL, "fused_norm_qmv_f16in: 1-bit weights");
     return nnz_qmv_norm_f32out_launch(ctx, w, residual, norm_scale, output, dims, 1e-6f);
+}
+
+// ---------------------------- stacked (one launch, many matrices) --------
+int nnz_dispatch_qmv_stacked(nnz_ctx *ctx, const nnz_qweight *w, const float *input,
+                             float *output, nnz_qmv_dims dims, const nnz_qmv_stack *stack) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, stack != nullptr, NNZ_EINVAL, "qmv_stacked: null stack");
+    const nnz_qweight *ws[1] = {w};
+    void *out[1] = {output};
+    const uint32_t rows[1] = {dims.M};
+    return launch_qmv_ex<1, NNZ_F32, 1, XIN_X, EPI_STORE, NNZ_F32, false>(
+        ctx, ws, rows, 1, input, nullptr, out, dims, "qmv_stacked", nullptr, 1e-6f, stack);
+}
+int nnz_dispatch_q4mv_stacked(nnz_ctx *ctx, const nnz_qweight *w, const float *input,
+                              float *output, nnz_qmv_dims dims, const nnz_qmv_stack *stack) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, stack != nullptr, NNZ_EINVAL, "q4mv_stacked: null stack");
+    const nnz_qweight *ws[1] = {w};
+    void *out[1] = {output};
+    const uint32_t rows[1] = {dims.M};
+    return launch_qmv_ex<4, NNZ_F32, 1, XIN_X, EPI_STORE, NNZ_F32, false>(
+        ctx, ws, rows, 1, input, nullptr, out, dims, "q4mv_stacked", nullptr, 1e-6f, stack);
+}
+int nnz_dispatch_qmv_fused_pair_silu_stacked(nnz_ctx *ctx, const nnz_qweight *wa,
+                                             const nnz_qweight *wb, const float *input,
+                                             float *output, nnz_qmv_dims dims,
+                                             const nnz_qmv_stack *stack) {
+    NNZ_CHECK_CTX(ctx);
+    NNZ_REQUIRE(ctx, stack != nullptr, NNZ_EINVAL, "pair_silu_stacked: null stack");
+    NNZ_REQUIRE(ctx, wb != nullptr, NNZ_EINVAL, "pair_silu_stacked: null second weight");
+    const nnz_qweight *ws[2] = {wa, wb};
+    void *out[2] = {output, nullptr};
+    const uint32_t rows[1] = {dims.M};
+    return launch_qmv_ex<1, NNZ_F32, 2, XIN_X, EPI_SILU, NNZ_F32, false>(
+        ctx, ws, rows, 2, input, nullptr, out, dims, "pair_silu_stacked", nullptr, 1e-6f, stack);
 }
 
 // ---------------------------- Q4 ------------------------------------------

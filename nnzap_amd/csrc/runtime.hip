@@ -65,6 +65,16 @@ int nnz_ctx_destroy(nnz_ctx *ctx) {
 
 void *nnz_ctx_stream(nnz_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
 
+int nnz_ctx_set_option(nnz_ctx *ctx, int option, int value) {
+    NNZ_CHECK_CTX(ctx);
+    if (option == NNZ_OPT_Q1_MATRIX_CORES) {
+        NNZ_REQUIRE(ctx, value >= 0 && value <= 2, NNZ_EINVAL, "q1 matrix cores: %d (0, 1 or 2)", value);
+        ctx->q1_matrix_cores = value;
+        return NNZ_OK;
+    }
+    return nnz_fail(ctx, NNZ_EINVAL, "unknown option %d", option);
+}
+
 const char *nnz_last_error(nnz_ctx *ctx) { return ctx ? ctx->err.c_str() : "null context"; }
 
 int nnz_alloc(nnz_ctx *ctx, size_t bytes, void **out) {

@@ -337,9 +337,6 @@ struct AttnArgs {
 };
 
 constexpr int ATT_MAX_CHUNK = 512;
-#ifndef STREAM_DMA
-#define STREAM_DMA true
-#endif
 #ifndef NNZ_DEC_TARGET_BLOCKS
 #define NNZ_DEC_TARGET_BLOCKS 1024u
 #endif
@@ -1244,14 +1241,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecAttnArgs a) {
 //   * the next group's loads are issued before the current one is used;
 //   * the 4 waves' (m, l, o) are merged once at the end: the output (one
 //     chunk) or the chunk's partials for attn_combine_kernel.
-template <int G, int KVDT, bool VT, bool DMA = false>
+template <int G, int KVDT, bool VT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))   // <= 128 VGPRs: 4 blocks per CU
 void attn_stream_kernel(DecAttnArgs a) {
     constexpr int D = 128, DP = 16, KT = 4, TPI = 16, NR = VT ? 1 : 4;
     static_assert(G == 1 || G == 2, "one or two query heads per block");
-    static_assert(!DMA || !VT, "the LDS ring path reads row-major V");
-    __shared__ uint4 ring0[DMA ? 4 : 1][2][4][64], ring1[DMA ? 4 : 1][2][4][64];
-    __shared__ uint4 ring2[DMA ? 4 : 1][2][4][64], ring3[DMA ? 4 : 1][2][4][64];
     __shared__ float qs[G][D];
     __shared__ float pw[4][G][TPI];
     __shared__ float wml[4][G][2];
@@ -1307,7 +1301,7 @@ void attn_stream_kernel(DecAttnArgs a) {
         }
     };
     uint4 kA[KT], vA[4], kB[KT], vB[4];
-    if constexpr (!DMA) load(kA, vA, 0);
+    load(kA, vA, 0);
 
     // q (optionally RoPE-rotated at rope_pos) -> LDS -> this lane's 8 dims
     {
@@ -1443,57 +1437,11 @@ void attn_stream_kernel(DecAttnArgs a) {
         __builtin_amdgcn_wave_barrier();   // the next group rewrites pw[w]
     };
 
-    if constexpr (DMA) {
-        // Groups go from global memory straight into a 4-slot LDS ring per
-        // wave (global_load_lds: lane l's 16 bytes land at slot + 16 l, the
-        // layout the register path uses), three groups in flight while one
-        // is used; each slot is its own array so the compiler can tell the
-        // loads into one slot from the reads of another.
-        auto issue = [&](uint4 (&sl)[4][2][4][64], uint32_t i) __attribute__((always_inline)) {
-            const uint32_t t0 = c0 + grp(i) * TPI, len = min((uint32_t)TPI, cend - t0);
-#pragma unroll
-            for (int v = 0; v < KT; ++v) {
-                const uint32_t t = min((uint32_t)(4 * v + row), len - 1);
-                __builtin_amdgcn_global_load_lds(
-                    (const __attribute__((address_space(1))) void *)((const uint4 *)(kb + (size_t)(t0 + t) * D) + dp),
-                    (__attribute__((address_space(3))) void *)&sl[w][0][v][0], 16, 0, 0);
-                __builtin_amdgcn_global_load_lds(
-                    (const __attribute__((address_space(1))) void *)((const uint4 *)(vb + (size_t)(t0 + t) * D) + dp),
-                    (__attribute__((address_space(3))) void *)&sl[w][1][v][0], 16, 0, 0);
-            }
-        };
-        auto use = [&](uint4 (&sl)[4][2][4][64], uint32_t i) __attribute__((always_inline)) {
-            // the three newer groups' 24 loads may still be in flight
-            __builtin_amdgcn_s_waitcnt((24 & 15) | ((24 >> 4) << 14) | (7 << 4) | (15 << 8));
-            uint4 kr[KT], vr[4];
-#pragma unroll
-            for (int v = 0; v < KT; ++v) {
-                kr[v] = sl[w][0][v][lane];
-                vr[v] = sl[w][1][v][lane];
-            }
-            if (i < nit) compute(kr, vr, i);   // wave-uniform
-        };
-        issue(ring0, 0);
-        issue(ring1, 1);
-        issue(ring2, 2);
-        for (uint32_t i = 0; i < nit; i += 4) {
-            issue(ring3, i + 3);
-            use(ring0, i);
-            issue(ring0, i + 4);
-            use(ring1, i + 1);
-            issue(ring1, i + 5);
-            use(ring2, i + 2);
-            issue(ring2, i + 6);
-            use(ring3, i + 3);
-        }
-        __builtin_amdgcn_s_waitcnt((0 & 15) | (0 << 14) | (7 << 4) | (15 << 8));   // no load left writing LDS
-    } else {
-        for (uint32_t i = 0; i < nit; i += 2) {
-            load(kB, vB, i + 1);
-            compute(kA, vA, i);
-            load(kA, vA, i + 2);
-            if (i + 1 < nit) compute(kB, vB, i + 1);
-        }
+    for (uint32_t i = 0; i < nit; i += 2) {
+        load(kB, vB, i + 1);
+        compute(kA, vA, i);
+        load(kA, vA, i + 2);
+        if (i + 1 < nit) compute(kB, vB, i + 1);
     }
 
     // the 4 waves' states -> one (m, l, o) per query head
@@ -1919,10 +1867,10 @@ int nnz_attn_launch(nnz_ctx *ctx, const void *q, int qdt, const void *kc, const 
     do {                                                                                                \
         if (kvdt == NNZ_F16) {                                                                          \
             if (vt) attn_stream_kernel<GG, NNZ_F16, true><<<blocks, 256, 0, ctx->stream>>>(a);          \
-            else attn_stream_kernel<GG, NNZ_F16, false, STREAM_DMA><<<blocks, 256, 0, ctx->stream>>>(a); \
+            else attn_stream_kernel<GG, NNZ_F16, false><<<blocks, 256, 0, ctx->stream>>>(a); \
         } else {                                                                                        \
             if (vt) attn_stream_kernel<GG, NNZ_BF16, true><<<blocks, 256, 0, ctx->stream>>>(a);         \
-            else attn_stream_kernel<GG, NNZ_BF16, false, STREAM_DMA><<<blocks, 256, 0, ctx->stream>>>(a); \
+            else attn_stream_kernel<GG, NNZ_BF16, false><<<blocks, 256, 0, ctx->stream>>>(a); \
         }                                                                                               \
     } while (0)
         if (gb == 1) STR(1);

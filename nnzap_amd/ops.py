@@ -153,6 +153,102 @@ def _v(t):
     return C.c_void_p(_ptr(t))
 
 
+class StackedQWeights:
+    """`count` independently drawn quantised matrices of one shape [M x K],
+    generated on the device (seeded torch generator): codes uniform random
+    bits (Q1) or nibbles (Q4), 16-bit scales ~U(scale_range) and, for Q4,
+    biases ~U(bias_range).  Matrix i lives at a fixed stride in three device
+    arrays -- the layout nnz_dispatch_*_stacked reads.  Rows of every array
+    are padded to 16 bytes per matrix so the strides keep the codes aligned."""
+
+    def __init__(self, dev: Device, M: int, K: int, group_size: int, bits: int, count: int,
+                 seed: int, scale_range=(0.01, 0.05), bias_range=(-0.1, 0.1),
+                 scale_dtype: int = DT_F16):
+        torch = _torch()
+        td = dev.torch_device
+        g = torch.Generator(device=td)
+        g.manual_seed(seed)
+        self.M, self.K, self.group_size, self.bits, self.count = M, K, group_size, bits, count
+        self.scale_dtype = scale_dtype
+        words = M * K * bits // 32
+        ng = M * K // group_size
+        wpad = (words + 3) // 4 * 4
+        gpad = (ng + 7) // 8 * 8
+        self.codes = torch.randint(-2 ** 31, 2 ** 31 - 1, (count, wpad), dtype=torch.int32,
+                                   generator=g, device=td)
+        sdt = torch.float16 if scale_dtype == DT_F16 else torch.bfloat16
+
+        def uni(lo, hi):
+            return (lo + (hi - lo) * torch.rand(count, gpad, generator=g, device=td)) \
+                .to(sdt).view(torch.int16)
+        self.scales = uni(*scale_range)
+        self.biases = uni(*bias_range) if bits == 4 else None
+        self.desc = L.QWeightDesc(self.codes.data_ptr(), self.scales.data_ptr(),
+                                  _ptr(self.biases), M * K, group_size, bits, scale_dtype)
+        self.codes_stride = wpad * 4
+        self.scales_stride = gpad * 2
+
+    @property
+    def ref(self):
+        return C.byref(self.desc)
+
+    @property
+    def nbytes_each(self) -> int:
+        """Algorithmic bytes of one matrix (codes, scales and biases)."""
+        n = self.M * self.K * self.bits // 8 + self.M * self.K // self.group_size * 2
+        return n + (self.M * self.K // self.group_size * 2 if self.bits == 4 else 0)
+
+    def dims(self) -> QMVDims:
+        return QMVDims(self.M, self.K, self.group_size)
+
+    def stack(self, input_stride: int, output_stride: int, blocks_per_matrix: int = 0):
+        return L.QmvStack(self.count, blocks_per_matrix, self.codes_stride, self.scales_stride,
+                          input_stride, output_stride)
+
+    def host(self, i: int) -> QWeight:
+        """Host copy of matrix i (for checks against the oracle)."""
+        words = self.M * self.K * self.bits // 32
+        ng = self.M * self.K // self.group_size
+        codes = self.codes[i, :words].cpu().numpy().view(np.uint32).reshape(self.M, -1)
+        sc = self.scales[i, :ng].cpu().numpy().view(np.uint16).reshape(self.M, -1)
+        bi = (self.biases[i, :ng].cpu().numpy().view(np.uint16).reshape(self.M, -1)
+              if self.biases is not None else None)
+        return QWeight(self.bits, self.M, self.K, self.group_size, codes, sc, bi,
+                       self.scale_dtype)
+
+
+def _stack_io(x, y):
+    """Byte strides between the matrices' inputs x[count, K] and outputs y[count, M]."""
+    return x.stride(0) * x.element_size(), y.stride(0) * y.element_size()
+
+
+def dispatch_qmv_stacked(dev, sw: StackedQWeights, x, y, blocks_per_matrix: int = 0):
+    """Config-2 arithmetic (Q1, f32 in/out) over sw.count matrices in one
+    launch: y[i] = W_i . x[i]."""
+    xs, ys = _stack_io(x, y)
+    st = sw.stack(xs, ys, blocks_per_matrix)
+    dev.call("nnz_dispatch_qmv_stacked", sw.ref, _v(x), _v(y), sw.dims(), C.byref(st))
+
+
+def dispatch_q4mv_stacked(dev, sw: StackedQWeights, x, y, blocks_per_matrix: int = 0):
+    """Config-1 arithmetic (Q4, f32 in/out) over sw.count matrices in one launch."""
+    xs, ys = _stack_io(x, y)
+    st = sw.stack(xs, ys, blocks_per_matrix)
+    dev.call("nnz_dispatch_q4mv_stacked", sw.ref, _v(x), _v(y), sw.dims(), C.byref(st))
+
+
+def dispatch_qmv_fused_pair_silu_stacked(dev, wa: StackedQWeights, wb: StackedQWeights, x, y,
+                                         blocks_per_matrix: int = 0):
+    """Config-3 arithmetic (silu(Wg x) * (Wu x), f32 in/out) over wa.count
+    gate/up pairs in one launch; the two stacks share their strides."""
+    assert (wa.codes_stride, wa.scales_stride, wa.count) == \
+        (wb.codes_stride, wb.scales_stride, wb.count), "pair stacks differ in layout"
+    xs, ys = _stack_io(x, y)
+    st = wa.stack(xs, ys, blocks_per_matrix)
+    dev.call("nnz_dispatch_qmv_fused_pair_silu_stacked", wa.ref, wb.ref, _v(x), _v(y),
+             wa.dims(), C.byref(st))
+
+
 # ----------------------------------------------------------------- QMV, Q1
 def dispatch_qmv(dev, w, x, y, dims=None):
     """transformer.zig:1565 dispatchQMV (f32 in, f32 out)."""

@@ -72,6 +72,11 @@ OFF(nnz_embed_dims, num_tokens, 8); OFF(nnz_embed_dims, group_size, 12);
 /* :475-479 QMVDims */
 SIZE(nnz_qmv_dims, 12);
 OFF(nnz_qmv_dims, M, 0); OFF(nnz_qmv_dims, K, 4); OFF(nnz_qmv_dims, group_size, 8);
+/* the stacked-launch descriptor (no reference counterpart): two u32 then four u64 strides */
+SIZE(nnz_qmv_stack, 40);
+OFF(nnz_qmv_stack, count, 0); OFF(nnz_qmv_stack, blocks_per_matrix, 4);
+OFF(nnz_qmv_stack, codes_stride, 8); OFF(nnz_qmv_stack, scales_stride, 16);
+OFF(nnz_qmv_stack, input_stride, 24); OFF(nnz_qmv_stack, output_stride, 32);
 
 /* The build's own structs, as the ctypes table and nnz.zig lay them out. */
 SIZE(nnz_qweight, 40);

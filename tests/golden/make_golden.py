@@ -7,7 +7,9 @@ synthetic inputs -- the seeds make the inputs reproducible on any host.
 
   python tests/golden/make_golden.py small     # kernel-level vectors (seconds)
   python tests/golden/make_golden.py config5        # 28-layer greedy tokens + logits (minutes, ~20 GB RAM)
-  python tests/golden/make_golden.py config5_unit   # the same with norm weights 1 + N(0, 0.02)
+  python tests/golden/make_golden.py config5_unit [--all-steps]
+                                                    # the same with norm weights 1 + N(0, 0.02);
+                                                    # --all-steps: logits of every decode step
 """
 from __future__ import annotations
 
@@ -73,18 +75,20 @@ def small():
     print("wrote small_vectors.json")
 
 
-LOGIT_STEPS = 16     # decode steps whose logits are recorded
+LOGIT_STEPS = 16     # decode steps whose logits are recorded at LOGIT_STRIDE
 LOGIT_STRIDE = 512   # every 512th logit is recorded besides the top 8
+LATE_STRIDE = 1024   # steps past LOGIT_STEPS (all of them with --all-steps)
 
 
-def logit_summary(logits):
+def logit_summary(logits, stride=LOGIT_STRIDE):
     """What the GPU test compares at full size: the top 8 (index, value), a
     strided sample of the whole vector, max |logit|, and a sha256 of the
     float32 values (identifies the vector; not compared on the GPU)."""
     lg = np.asarray(logits, dtype=np.float64)
     top = np.argsort(-lg, kind="stable")[:8]
     return {"top8_idx": top.tolist(), "top8_val": lg[top].tolist(),
-            "sample": lg[::LOGIT_STRIDE].tolist(), "max_abs": float(np.max(np.abs(lg))),
+            "sample": lg[::stride].tolist(), "stride": stride,
+            "max_abs": float(np.max(np.abs(lg))),
             "sha256": sha(lg.astype(np.float32))}
 
 
@@ -112,7 +116,12 @@ def add_noise(name: str):
     print(f"{name}: fp32 noise {g['fp32_noise']:.3e}")
 
 
-def config5(n_prompt=512, n_new=256, norm_mode="small", out_name="config5_tokens.json"):
+def config5(n_prompt=512, n_new=256, norm_mode="small", out_name="config5_tokens.json",
+            all_steps=False):
+    """Greedy tokens of the full-size decoder and the logit summaries of the
+    last prompt token and of the first LOGIT_STEPS decode steps (every step
+    with all_steps: the later ones sampled every LATE_STRIDE logits), so the
+    GPU test can teacher-force the golden tokens through the whole stream."""
     t0 = time.time()
     cfg = cf.BONSAI_1_7B
     w = cf.decoder_weights(cfg, norm_mode=norm_mode, host_embed=False)  # rows on demand
@@ -133,6 +142,8 @@ def config5(n_prompt=512, n_new=256, norm_mode="small", out_name="config5_tokens
         logits = od.forward([t], pos)[0]
         if i < LOGIT_STEPS:
             summaries.append(logit_summary(logits))
+        elif all_steps and i < n_new - 1:
+            summaries.append(logit_summary(logits, LATE_STRIDE))
         pos += 1
         if i % 16 == 0:
             print(f"step {i} token {t} margin {margins[-1]:.3e} ({time.time() - t0:.0f}s)", flush=True)
@@ -163,6 +174,7 @@ if __name__ == "__main__":
     elif what == "config5_unit":
         # norm weights 1 + N(0, 0.02): the fallback of the norm-weight
         # decision, whose token stream is not periodic
-        config5(norm_mode="unit", out_name="config5_unit_tokens.json")
+        config5(norm_mode="unit", out_name="config5_unit_tokens.json",
+                all_steps="--all-steps" in sys.argv)
     else:
         raise SystemExit(f"unknown fixture set {what}")

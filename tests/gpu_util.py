@@ -39,6 +39,23 @@ def assert_close(got, ref, rtol=1e-3, what=""):
     return e
 
 
+def assert_close_f16(got, ref_f64, rtol=1e-3, what=""):
+    """An f16-stored output against the float64 oracle: each element within
+    the assert_close bar of the f16-rounded oracle value, or one f16 ulp of
+    it (the kernel's float32 sum and the float64 one may straddle a rounding
+    edge; near zero one ulp can exceed the relative bar)."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref_f64, dtype=np.float64)
+    r16 = ref.astype(np.float16).astype(np.float64)
+    denom = np.abs(r16) + 1e-2 * np.sqrt(np.mean(r16 ** 2) + 1e-300)
+    e = np.abs(got - r16)
+    mag = np.maximum(np.abs(ref), 2.0 ** -14)
+    ulp = 2.0 ** (np.floor(np.log2(mag)) - 10)
+    bad = (e > rtol * denom) & (e > ulp * (1 + 1e-9))
+    assert not bad.any(), (f"{what}: {bad.sum()} elements beyond the bar and one f16 ulp "
+                           f"(max rel {float(np.max(e / denom)):.3e})")
+
+
 def assert_close_normwise(got, ref, rtol=1e-3, what=""):
     """End-to-end bar for decoder logits: max|got - ref| <= rtol * max|ref|.
 

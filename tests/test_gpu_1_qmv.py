@@ -15,9 +15,20 @@ from nnzap_amd import ops
 from nnzap_amd import synth as S
 from oracle import oracle as O
 
-from gpu_util import assert_bf16_faithful, assert_close, host, tdev
+from gpu_util import assert_bf16_faithful, assert_close, assert_close_f16, host, tdev
 
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture
+def q1_cores(dev):
+    """Sets NNZ_OPT_Q1_MATRIX_CORES for one test, back to the default after."""
+    from nnzap_amd import _lib as L
+
+    def set_(v):
+        dev.call("nnz_ctx_set_option", L.OPT_Q1_MATRIX_CORES, v)
+    yield set_
+    set_(0)
 
 
 def _dw(dev, w):
@@ -386,3 +397,186 @@ def test_lm_head_bf16(dev, V, H):
     dev.sync()
     ref = S.bf16_bits_to_f32(table).astype(np.float64) @ x.astype(np.float64)
     assert_close(host(y), ref, what=f"lm_head_bf16 V={V} H={H}")
+
+
+# ------------------------------------------------- stacked (one launch) ---
+@pytest.mark.parametrize("kind", ["config1_q4", "config2_q1", "config3_pair_silu"])
+@pytest.mark.parametrize("bpm", [0, 1, 3])
+@pytest.mark.parametrize("cores", [1, 2])
+def test_stacked_matches_single(dev, kind, bpm, cores, q1_cores):
+    """nnz_dispatch_*_stacked: 5 independently drawn matrices of a config
+    shape in one launch (blocks per matrix: library choice, 1, 3); every
+    matrix's output equals the single-matrix launch bit for bit (a row is
+    reduced by one wave in a fixed order, whatever the grid) and the oracle
+    within the 1e-3 bar.  Both 1-bit kernels (matrix cores on / off: the
+    K = 2048 pair has both)."""
+    q1_cores(cores)
+    n = 5
+    if kind == "config1_q4":
+        M, K, gs, bits = 6144, 2048, 64, 4
+        sw = [ops.StackedQWeights(dev, M, K, gs, 4, n, 11, (0.005, 0.02), (-0.1, 0.1))]
+    elif kind == "config2_q1":
+        M, K, gs, bits = 2048, 6144, 128, 1
+        sw = [ops.StackedQWeights(dev, M, K, gs, 1, n, 12, (0.01, 0.05))]
+    else:
+        M, K, gs, bits = 6144, 2048, 128, 1
+        sw = [ops.StackedQWeights(dev, M, K, gs, 1, n, 13 + i, (0.01, 0.05)) for i in range(2)]
+    x = torch.randn(n, K, device="cuda", generator=torch.Generator("cuda").manual_seed(14))
+    y = torch.full((n, M), float("nan"), device="cuda")
+    if kind == "config1_q4":
+        ops.dispatch_q4mv_stacked(dev, sw[0], x, y, bpm)
+    elif kind == "config2_q1":
+        ops.dispatch_qmv_stacked(dev, sw[0], x, y, bpm)
+    else:
+        ops.dispatch_qmv_fused_pair_silu_stacked(dev, sw[0], sw[1], x, y, bpm)
+    dev.sync()
+    for i in (0, 2, n - 1):
+        ws = [s.host(i) for s in sw]
+        dws = [_dw(dev, w) for w in ws]
+        y1 = torch.empty(M, device="cuda")
+        if kind == "config1_q4":
+            ops.dispatch_q4mv(dev, dws[0], x[i].contiguous(), y1)
+        elif kind == "config2_q1":
+            ops.dispatch_qmv(dev, dws[0], x[i].contiguous(), y1)
+        else:
+            ops.dispatch_qmv_fused_pair_silu(dev, dws[0], dws[1], x[i].contiguous(), y1)
+        dev.sync()
+        assert torch.equal(y[i], y1), f"{kind} matrix {i}: stacked != single launch"
+        xi = x[i].cpu().numpy()
+        ref = O.qmv(ws[0], xi) if kind != "config3_pair_silu" else O.qmv_pair_silu(ws[0], ws[1], xi)
+        assert_close(host(y[i]), ref, what=f"{kind} matrix {i}")
+
+
+def test_stacked_refuses_bad_strides(dev):
+    """A stride that breaks the 16-byte code alignment, a zero count and a
+    missing stack descriptor are refused with an error code, never launched."""
+    import ctypes as C
+    from nnzap_amd import _lib as L
+    sw = ops.StackedQWeights(dev, 64, 2048, 128, 1, 2, 15)
+    x = torch.zeros(2, 2048, device="cuda")
+    y = torch.zeros(2, 64, device="cuda")
+    bad = L.QmvStack(2, 0, sw.codes_stride + 4, sw.scales_stride, 2048 * 4, 64 * 4)
+    rc = L.lib().nnz_dispatch_qmv_stacked(dev.ctx, sw.ref, C.c_void_p(x.data_ptr()),
+                                          C.c_void_p(y.data_ptr()), sw.dims(), C.byref(bad))
+    assert rc == L.EINVAL
+    zero = L.QmvStack(0, 0, sw.codes_stride, sw.scales_stride, 2048 * 4, 64 * 4)
+    rc = L.lib().nnz_dispatch_qmv_stacked(dev.ctx, sw.ref, C.c_void_p(x.data_ptr()),
+                                          C.c_void_p(y.data_ptr()), sw.dims(), C.byref(zero))
+    assert rc == L.EINVAL
+    rc = L.lib().nnz_dispatch_qmv_stacked(dev.ctx, sw.ref, C.c_void_p(x.data_ptr()),
+                                          C.c_void_p(y.data_ptr()), sw.dims(), None)
+    assert rc == L.EINVAL
+
+
+# ------------------------------------------- 1-bit on the matrix cores ---
+def _cores_pair(dev, q1_cores, run):
+    """run() under matrix cores forced on, then off: (mfma, valu) outputs."""
+    q1_cores(1)
+    a = run()
+    q1_cores(2)
+    b = run()
+    return a, b
+
+
+def _near_valu(a, b, what):
+    """The two 1-bit kernels sum in different orders: agree to float32
+    rounding, max |a - b| <= 1e-5 max |b| (the SiLU products are
+    heavy-tailed, so max |b|, not rms, is the scale)."""
+    a, b = host(a), host(b)
+    d = np.max(np.abs(a - b)) / (np.max(np.abs(b)) + 1e-30)
+    assert d <= 1e-5, f"{what}: matrix cores vs VALU kernel differ by {d:.2e} of max |y|"
+
+
+@pytest.mark.parametrize("M", [1, 16, 33, 2048, 20011])
+def test_q1_matrix_cores_qmv(dev, q1_cores, M):
+    """dispatchQMV (f32 in/out) and dispatchQMVf16in at K = 2048, gs 128 on
+    the block-scaled MFMA kernel (x split into five e4m3 terms, bits as fp4
+    +-1): the oracle within 1e-3, the VALU kernel within float32 rounding;
+    ragged row counts (1, 33, 20011 rows: partial 16-row tiles)."""
+    w = cf.q1_matrix(M, 2048, 128, 700 + M % 97, 701)
+    x = S.normal(702, 2048).astype(np.float32)
+    dw = _dw(dev, w)
+    xd = tdev(x)
+    x16 = tdev(x, torch.float16)
+
+    def run32():
+        y = torch.full((M,), float("nan"), device="cuda")
+        ops.dispatch_qmv(dev, dw, xd, y)
+        dev.sync()
+        return y
+
+    def run16():
+        y = torch.full((M,), float("nan"), device="cuda")
+        ops.dispatch_qmv_f16in(dev, dw, x16, y)
+        dev.sync()
+        return y
+    a, b = _cores_pair(dev, q1_cores, run32)
+    assert_close(host(a), O.qmv(w, x), what=f"f32 M={M}")
+    _near_valu(a, b, f"f32 M={M}")
+    a, b = _cores_pair(dev, q1_cores, run16)
+    assert_close(host(a), O.qmv(w, x16.cpu().numpy().astype(np.float64)), what=f"f16in M={M}")
+    _near_valu(a, b, f"f16in M={M}")
+
+
+@pytest.mark.parametrize("M", [6144, 151936])
+def test_q1_matrix_cores_norm_lm_head(dev, q1_cores, M):
+    """Final RMSNorm + LM head (f16-rounded normalised input, f32 logits) on
+    the matrix cores, at the decoder's vocabulary size and a layer's."""
+    w = cf.q1_matrix(M, 2048, 128, 710, 711)
+    res = S.normal(712, 2048).astype(np.float32)
+    nw = (1.0 + 0.1 * S.normal(713, 2048)).astype(np.float32)
+    dw, rd, nd = _dw(dev, w), tdev(res), tdev(nw)
+
+    def run():
+        y = torch.full((M,), float("nan"), device="cuda")
+        ops.dispatch_fused_norm_qmv_f16in(dev, dw, rd, y, nd)
+        dev.sync()
+        return y
+    a, b = _cores_pair(dev, q1_cores, run)
+    assert_close(host(a), O.qmv(w, O.norm_to_half(res, nw)), what=f"norm lm head M={M}")
+    _near_valu(a, b, f"norm lm head M={M}")
+
+
+@pytest.mark.parametrize("M", [6144, 100])
+def test_q1_matrix_cores_pair_and_resadd(dev, q1_cores, M):
+    """Config 3 (fused gate/up + SiLU, f32 I/O), the decoder's fused norm +
+    gate/up + SiLU (f16 out) and the f16io residual add on the matrix cores."""
+    wg, wu = cf.q1_matrix(M, 2048, 128, 720, 721), cf.q1_matrix(M, 2048, 128, 722, 723)
+    x = S.normal(724, 2048).astype(np.float32)
+    res = S.normal(725, 2048).astype(np.float32)
+    nw = (1.0 + 0.1 * S.normal(726, 2048)).astype(np.float32)
+    dg, du, xd, rd, nd = _dw(dev, wg), _dw(dev, wu), tdev(x), tdev(res), tdev(nw)
+
+    def pair():
+        y = torch.full((M,), float("nan"), device="cuda")
+        ops.dispatch_qmv_fused_pair_silu(dev, dg, du, xd, y)
+        dev.sync()
+        return y
+
+    def norm_pair():
+        y = torch.full((M,), float("nan"), dtype=torch.float16, device="cuda")
+        ops.dispatch_fused_norm_pair_silu_f16io(dev, dg, du, rd, y, nd)
+        dev.sync()
+        return y
+    a, b = _cores_pair(dev, q1_cores, pair)
+    assert_close(host(a), O.qmv_pair_silu(wg, wu, x), what="pair silu")
+    _near_valu(a, b, "pair silu")
+    a, b = _cores_pair(dev, q1_cores, norm_pair)
+    xn = O.norm_to_half(res, nw)
+    ref = O.qmv_pair_silu(wg, wu, xn)
+    assert_close_f16(host(a), ref, what="norm pair silu (matrix cores)")
+    assert_close_f16(host(b), ref, what="norm pair silu (VALU)")
+    wo = cf.q1_matrix(M, 2048, 128, 727, 728)
+    do = _dw(dev, wo)
+    x16 = tdev((0.05 * x).astype(np.float16))
+    base = S.normal(729, M).astype(np.float32)
+
+    def resadd():
+        r = tdev(base)
+        ops.dispatch_qmv_f16io_resadd(dev, do, x16, r)
+        dev.sync()
+        return r
+    a, b = _cores_pair(dev, q1_cores, resadd)
+    ref = base.astype(np.float64) + O.qmv(wo, x16.cpu().numpy().astype(np.float64))
+    assert_close(host(a), ref, what="f16io resadd")
+    _near_valu(a, b, "f16io resadd")

@@ -152,7 +152,7 @@ def _check_logit_summary(got, ref, what, rel=1e-3):
     """Full-size logits against the golden summary (top 8 and a strided
     sample of the whole vector): max |err| <= rel * max |logit| on every
     recorded entry, and the same argmax wherever the oracle's top-2 margin
-    exceeds that bar."""
+    exceeds twice that bar.  Returns whether the argmax was asserted."""
     got = np.asarray(got, dtype=np.float64)
     idx = np.concatenate([np.array(ref["top8_idx"]),
                           np.arange(0, len(got), ref.get("stride", 512))])
@@ -163,16 +163,20 @@ def _check_logit_summary(got, ref, what, rel=1e-3):
     assert abs(np.max(np.abs(got)) - ref["max_abs"]) <= bar, f"{what}: max |logit|"
     if ref["top8_val"][0] - ref["top8_val"][1] > 2 * bar:
         assert int(np.argmax(got)) == ref["top8_idx"][0], f"{what}: argmax"
+        return True
+    return False
 
 
 @pytest.mark.parametrize("name", ["config5_tokens.json", "config5_unit_tokens.json"])
 def test_config5_golden(mdev, name):
     """BASELINE config 5 at full size: 512 prompt ids, 256 greedy steps;
-    tokens must equal the oracle's golden list, and the logits of the last
-    prompt token and of the first 16 decode steps (teacher-forced with the
-    golden tokens) must match the golden summaries.  Two fixtures: the
-    literal norm weights ~N(0, 0.02), and 1 + N(0, 0.02), whose token stream
-    is not periodic."""
+    tokens must equal the oracle's golden list up to the first near-tie, and
+    the logits of the last prompt token and of every recorded decode step
+    (teacher-forced with the golden tokens) must match the golden summaries,
+    with the argmax equal to the golden token wherever the oracle's top-2
+    margin exceeds twice the bar.  Two fixtures: the literal norm weights
+    ~N(0, 0.02) (16 recorded steps), and 1 + N(0, 0.02), whose token stream
+    is not periodic (all 255 steps that choose a next token)."""
     path = os.path.join(GOLDEN, name)
     if not os.path.exists(path):
         pytest.skip("golden fixture not generated yet")
@@ -193,6 +197,8 @@ def test_config5_golden(mdev, name):
         near = (2 * max(1e-3, 4 * gold.get("fp32_noise", 0.0)) * gold["logits"][0]["max_abs"]
                 if gold.get("logits") else 0.0)
         first_bad = int(np.argmax(toks != ref)) if np.any(toks != ref) else -1
+        print(f"{name}: free-running stream matches the golden tokens for "
+              f"{first_bad if first_bad >= 0 else len(ref)} of {len(ref)} steps", flush=True)
         if first_bad >= 0:
             mg = gold["margins"][first_bad]
             assert mg < near, (f"first mismatch at step {first_bad}: got {toks[first_bad]}, "
@@ -213,9 +219,12 @@ def test_config5_golden(mdev, name):
             for s_ in sums:
                 s_["stride"] = gold.get("logit_stride", 512)
             _check_logit_summary(m.prefill(prompt, 0), sums[0], "last prompt token", rel)
+            argmax_checked = 0
             for i, s_ in enumerate(sums[1:]):
                 got = m.forward_decode(int(ref[i]), gold["n_prompt"] + i)
-                _check_logit_summary(got, s_, f"decode step {i}", rel)
+                argmax_checked += _check_logit_summary(got, s_, f"decode step {i}", rel)
+            print(f"{name}: {len(sums) - 1} teacher-forced steps within the bar, argmax "
+                  f"asserted at {argmax_checked} of them", flush=True)
     finally:
         m.close()
 

@@ -497,30 +497,33 @@ def _kernel_cases():
             return us, V * 4, None
         return run
 
-    def stacked(kind):
+    def stacked(kind, pad=0, bpm=0):
         # One launch over `count` independently drawn matrices of a config
-        # shape (>= 64 of them and >= 640 MB in all, so the launch streams
+        # shape (>= 256 of them and >= 450 MB in all, so the launch streams
         # from HBM): the kernel's streaming rate without the per-launch
         # floor.  HIP events on the library stream around single launches,
         # best of 5 after a warm-up.
         def run(dev, n):
             shp = {"config1": (6144, 2048, 64, 4), "config2": (2048, 6144, 128, 1),
-                   "config3": (6144, 2048, 128, 1)}[kind]
+                   "config3": (6144, 2048, 128, 1), "q1_6144x2048": (6144, 2048, 128, 1)}[kind]
             M_, K_, gs, bits = shp
             nmat = 2 if kind == "config3" else 1
             each = (M_ * K_ * bits // 8 + M_ * K_ // gs * 2 * (2 if bits == 4 else 1)) * nmat
-            count = max(MIN_COPIES, -(-ROTATE_BYTES // each))
+            # a multiple of 256 matrices (>= 64, >= 640 MB where that is fewer):
+            # the matrix-core kernel runs one block per CU and matrix
+            count = max(256, -(-max(MIN_COPIES * each, ROTATE_BYTES) // each))
+            count = -(-count // 256) * 256
             rng = (0.005, 0.02) if bits == 4 else (0.01, 0.05)
-            sws = [ops.StackedQWeights(dev, M_, K_, gs, bits, count, 900 + i, rng)
+            sws = [ops.StackedQWeights(dev, M_, K_, gs, bits, count, 900 + i, rng, pad_bytes=pad)
                    for i in range(nmat)]
             x = torch.randn(count, K_, device="cuda")
             y = torch.empty(count, M_, device="cuda")
             if kind == "config1":
-                fn = lambda: ops.dispatch_q4mv_stacked(dev, sws[0], x, y)  # noqa: E731
-            elif kind == "config2":
-                fn = lambda: ops.dispatch_qmv_stacked(dev, sws[0], x, y)  # noqa: E731
+                fn = lambda: ops.dispatch_q4mv_stacked(dev, sws[0], x, y, bpm)  # noqa: E731
+            elif kind in ("config2", "q1_6144x2048"):
+                fn = lambda: ops.dispatch_qmv_stacked(dev, sws[0], x, y, bpm)  # noqa: E731
             else:
-                fn = lambda: ops.dispatch_qmv_fused_pair_silu_stacked(dev, sws[0], sws[1], x, y)  # noqa: E731
+                fn = lambda: ops.dispatch_qmv_fused_pair_silu_stacked(dev, sws[0], sws[1], x, y, bpm)  # noqa: E731
             fn()
             dev.sync()
             best = None
@@ -547,6 +550,26 @@ def _kernel_cases():
             finally:
                 dev.call("nnz_ctx_set_option", L.OPT_Q1_MATRIX_CORES, 0)
         return run
+
+    def q1_big(dev, n):
+        # one 1-bit matrix of 256 x 6144 rows, K = 2048 (~500 MB): a single
+        # ordinary launch, every CU sweeping neighbouring tiles of one region
+        M_ = 6144 * 256
+        sw = ops.StackedQWeights(dev, M_, 2048, 128, 1, 1, 950)
+        x = torch.randn(2048, device="cuda")
+        y = torch.empty(M_, device="cuda")
+        fn = lambda: ops.dispatch_qmv(dev, sw, x, y)  # noqa: E731
+        fn()
+        dev.sync()
+        best = None
+        for _ in range(5):
+            dev.mark(0)
+            fn()
+            dev.mark(1)
+            ms = dev.elapsed_ms(0, 1)
+            best = ms if best is None else min(best, ms)
+        del sw
+        return best * 1000.0, M_ * (256 + 32) + 2048 * 4 + M_ * 4, None
 
     def copy_calib(dev, n):
         # a plain device copy of known size: the scale for FETCH/WRITE_SIZE
@@ -575,7 +598,15 @@ def _kernel_cases():
         "stacked_config1_q4mv": stacked("config1"), "stacked_config2_qmv": stacked("config2"),
         "stacked_config3_gate_up_silu": stacked("config3"),
         "stacked_config3_gate_up_silu_valu": cores(stacked("config3"), 2),
+        "stacked_q1_6144x2048": stacked("q1_6144x2048"),
+        "q1_big_mfma": cores(q1_big, 1),
+        "q1_big_valu": cores(q1_big, 2),
+        "stacked_q1_6144x2048_bpm4": stacked("q1_6144x2048", 0, 4),
+        "stacked_config3_bpm4": stacked("config3", 0, 4),
+        "stacked_config1_bpm32": stacked("config1", 0, 32),
+        "stacked_q1_6144x2048_valu": cores(stacked("q1_6144x2048"), 2),
         "dec_lm_head_norm_valu": cores(dec_lm_head, 2),
+        "dec_lm_head_norm_mfma": cores(dec_lm_head, 1),
         "config3_gate_up_silu_mfma": cores(config3, 1),
         "dec_gate_up_norm_silu_mfma": cores(dec_gate_up, 1),
         "prefill_gemm_q": prefill_gemm(QD, H, L.GEMM_STORE_F16),

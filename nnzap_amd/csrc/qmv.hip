@@ -92,9 +92,10 @@ struct QmvArgs {
 // Pointer `p` of matrix blockIdx.y of a stacked launch (`stride` bytes
 // between matrices; 0 for an ordinary launch).  The argument block itself
 // is never modified: a modified copy of it would live in scratch memory.
-template <class T>
+template <bool STK, class T>
 __device__ __forceinline__ T *stk(T *p, uint64_t stride) {
-    return (T *)((uintptr_t)p + (uint64_t)blockIdx.y * stride);
+    if constexpr (STK) return (T *)((uintptr_t)p + (uint64_t)blockIdx.y * stride);
+    else return p;   // ordinary launches carry no stacked-offset arithmetic
 }
 // Weight registers of one row-step.
 template <int NMAT, int R, int NV, int VEC>
@@ -162,12 +163,13 @@ struct SegPtrs {
     gptr<void> out;
 };
 
+template <bool STK>
 __device__ __forceinline__ SegPtrs seg_mat(const QmvArgs &a, int seg) {
     SegPtrs r;
-    r.codes = stk(pick3(seg, a.m0.codes, a.m1.codes, a.m2.codes), a.stk.codes);
-    r.scales = stk(pick3(seg, a.m0.scales, a.m1.scales, a.m2.scales), a.stk.scales);
-    r.biases = stk(pick3(seg, a.m0.biases, a.m1.biases, a.m2.biases), a.stk.scales);
-    r.out = stk(pick3(seg, a.m0.out, a.m1.out, a.m2.out), a.stk.out);
+    r.codes = stk<STK>(pick3(seg, a.m0.codes, a.m1.codes, a.m2.codes), a.stk.codes);
+    r.scales = stk<STK>(pick3(seg, a.m0.scales, a.m1.scales, a.m2.scales), a.stk.scales);
+    r.biases = stk<STK>(pick3(seg, a.m0.biases, a.m1.biases, a.m2.biases), a.stk.scales);
+    r.out = stk<STK>(pick3(seg, a.m0.out, a.m1.out, a.m2.out), a.stk.out);
     return r;
 }
 
@@ -181,7 +183,7 @@ struct LaneUnits {
     bool ok[NV];         // the unit exists
 };
 
-template <int BITS, int NMAT, int R, int NV, bool RES>
+template <int BITS, int NMAT, int R, int NV, bool RES, bool STK>
 __device__ __forceinline__ void load_step(const QmvArgs &a, StepRegs<NMAT, R, NV, (BITS == 1 ? 1 : 4)> &s,
                                           uint32_t base, int RPW, int rr, const LaneUnits<NV> &lu,
                                           uint32_t units, uint32_t G) {
@@ -195,15 +197,15 @@ __device__ __forceinline__ void load_step(const QmvArgs &a, StepRegs<NMAT, R, NV
     uint32_t seg_start = 0;
     gptr<void> outp = nullptr;
     if constexpr (NMAT == 1) {
-        const SegPtrs sm = seg_mat(a, step_segment(a, base, seg_start));
+        const SegPtrs sm = seg_mat<STK>(a, step_segment(a, base, seg_start));
         cp[0] = sm.codes; sp[0] = sm.scales; bp[0] = sm.biases;
         outp = sm.out;
     } else {
-        cp[0] = stk(uniform_ptr(a.m0.codes), a.stk.codes); sp[0] = stk(uniform_ptr(a.m0.scales), a.stk.scales);
-        bp[0] = stk(uniform_ptr(a.m0.biases), a.stk.scales);
-        cp[NMAT - 1] = stk(uniform_ptr(mat_of<NMAT - 1>(a).codes), a.stk.codes);
-        sp[NMAT - 1] = stk(uniform_ptr(mat_of<NMAT - 1>(a).scales), a.stk.scales);
-        bp[NMAT - 1] = stk(uniform_ptr(mat_of<NMAT - 1>(a).biases), a.stk.scales);
+        cp[0] = stk<STK>(uniform_ptr(a.m0.codes), a.stk.codes); sp[0] = stk<STK>(uniform_ptr(a.m0.scales), a.stk.scales);
+        bp[0] = stk<STK>(uniform_ptr(a.m0.biases), a.stk.scales);
+        cp[NMAT - 1] = stk<STK>(uniform_ptr(mat_of<NMAT - 1>(a).codes), a.stk.codes);
+        sp[NMAT - 1] = stk<STK>(uniform_ptr(mat_of<NMAT - 1>(a).scales), a.stk.scales);
+        bp[NMAT - 1] = stk<STK>(uniform_ptr(mat_of<NMAT - 1>(a).biases), a.stk.scales);
     }
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -273,7 +275,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t weight_rsrc(const void *p) {
 // Loads of one step of R consecutive whole-wave rows starting at `rb`
 // (wave-uniform, rb + R <= M: the caller clamps the last step back onto
 // valid rows instead of clamping each row).
-template <int BITS, int NMAT, int R, int NV, bool RES>
+template <int BITS, int NMAT, int R, int NV, bool RES, bool STK>
 __device__ __forceinline__ void load_step_full(const QmvArgs &a, StepRegs<NMAT, R, NV, (BITS == 1 ? 1 : 4)> &s,
                                                uint32_t rb, const FullOffsets<R, NV> &fo,
                                                uint32_t words_per_row, uint32_t G) {
@@ -290,22 +292,22 @@ __device__ __forceinline__ void load_step_full(const QmvArgs &a, StepRegs<NMAT, 
         auto sel = [&](const void *p0, const void *p1, const void *p2) {
             return seg == 0 ? p0 : (seg == 1 ? p1 : p2);
         };
-        cr[0] = weight_rsrc(stk(sel(a.m0.codes, a.m1.codes, a.m2.codes), a.stk.codes));
-        sr[0] = weight_rsrc(stk(sel(a.m0.scales, a.m1.scales, a.m2.scales), a.stk.scales));
-        br[0] = weight_rsrc(stk(sel(a.m0.biases, a.m1.biases, a.m2.biases), a.stk.scales));
+        cr[0] = weight_rsrc(stk<STK>(sel(a.m0.codes, a.m1.codes, a.m2.codes), a.stk.codes));
+        sr[0] = weight_rsrc(stk<STK>(sel(a.m0.scales, a.m1.scales, a.m2.scales), a.stk.scales));
+        br[0] = weight_rsrc(stk<STK>(sel(a.m0.biases, a.m1.biases, a.m2.biases), a.stk.scales));
     } else {
-        cr[0] = weight_rsrc(stk(a.m0.codes, a.stk.codes));
-        sr[0] = weight_rsrc(stk(a.m0.scales, a.stk.scales));
-        br[0] = weight_rsrc(stk(a.m0.biases, a.stk.scales));
-        cr[NMAT - 1] = weight_rsrc(stk(mat_of<NMAT - 1>(a).codes, a.stk.codes));
-        sr[NMAT - 1] = weight_rsrc(stk(mat_of<NMAT - 1>(a).scales, a.stk.scales));
-        br[NMAT - 1] = weight_rsrc(stk(mat_of<NMAT - 1>(a).biases, a.stk.scales));
+        cr[0] = weight_rsrc(stk<STK>(a.m0.codes, a.stk.codes));
+        sr[0] = weight_rsrc(stk<STK>(a.m0.scales, a.stk.scales));
+        br[0] = weight_rsrc(stk<STK>(a.m0.biases, a.stk.scales));
+        cr[NMAT - 1] = weight_rsrc(stk<STK>(mat_of<NMAT - 1>(a).codes, a.stk.codes));
+        sr[NMAT - 1] = weight_rsrc(stk<STK>(mat_of<NMAT - 1>(a).scales, a.stk.scales));
+        br[NMAT - 1] = weight_rsrc(stk<STK>(mat_of<NMAT - 1>(a).biases, a.stk.scales));
     }
     const uint32_t lr = rb - seg_start;
     const uint32_t co = lr * words_per_row * 4u, so = lr * G * 2u;
     if constexpr (RES) {
         static_assert(NMAT == 1, "residual add has one matrix");
-        s.res[0] = *(gptr<const float>)((gptr<const char>)stk(uniform_ptr(a.m0.out), a.stk.out) + (size_t)rb * 4u + fo.res);
+        s.res[0] = *(gptr<const float>)((gptr<const char>)stk<STK>(uniform_ptr(a.m0.out), a.stk.out) + (size_t)rb * 4u + fo.res);
     }
 #pragma unroll
     for (int m = 0; m < NMAT; ++m)
@@ -327,7 +329,7 @@ __device__ __forceinline__ void load_step_full(const QmvArgs &a, StepRegs<NMAT, 
 
 // Store / residual-add / SiLU epilogue of one row.  `row` indexes the pair
 // outputs and the residual, `lrow` the row within the step's segment.
-template <int EPI, int ODT, bool FAITH, int NMAT>
+template <int EPI, int ODT, bool FAITH, int NMAT, bool STK>
 __device__ __forceinline__ void qmv_epilogue(const QmvArgs &a, void *out0, uint32_t row,
                                              uint32_t lrow, const float (&tot)[NMAT], float prev) {
     if constexpr (EPI == EPI_STORE) {
@@ -340,7 +342,7 @@ __device__ __forceinline__ void qmv_epilogue(const QmvArgs &a, void *out0, uint3
             for (int m = 0; m < NMAT; ++m) {
                 float v = tot[m];
                 if constexpr (FAITH) v = bf16_trunc(v);
-                store_from_f32<ODT>(stk(m == 0 ? a.m0.out : a.m1.out, a.stk.out), row, v);
+                store_from_f32<ODT>(stk<STK>(m == 0 ? a.m0.out : a.m1.out, a.stk.out), row, v);
             }
         }
     } else if constexpr (EPI == EPI_RESADD) {
@@ -358,9 +360,9 @@ __device__ __forceinline__ void qmv_epilogue(const QmvArgs &a, void *out0, uint3
 // FULL: whole-wave rows (LPR == 64, every K >= 2048) fixed at compile time,
 // so that row indices, offsets and the row reductions are wave-uniform.
 template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH, int NV, int R, bool LUT,
-          bool FULL>
+          bool FULL, bool STK>
 __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
-    const void *const ax = stk(a.x, a.stk.x);
+    const void *const ax = stk<STK>(a.x, a.stk.x);
     static_assert(!LUT || BITS == 1, "nibble tables are for 1-bit weights");
     static_assert(!LUT || FULL, "nibble tables need whole-wave rows");
     constexpr bool NORM = XIN == XIN_NORM;
@@ -417,9 +419,9 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
     auto step_base = [&](uint32_t b) { return b < a.M - (uint32_t)R ? b : a.M - (uint32_t)R; };
     auto load_rows = [&](StepRegs<NMAT, R, NV, VEC> &dst, uint32_t b) {
         if constexpr (FULL)
-            load_step_full<BITS, NMAT, R, NV, EPI == EPI_RESADD>(a, dst, step_base(b), fo, units * VEC, G);
+            load_step_full<BITS, NMAT, R, NV, EPI == EPI_RESADD, STK>(a, dst, step_base(b), fo, units * VEC, G);
         else
-            load_step<BITS, NMAT, R, NV, EPI == EPI_RESADD>(a, dst, b < a.M ? b : 0u, RPW, rr, lu, units, G);
+            load_step<BITS, NMAT, R, NV, EPI == EPI_RESADD, STK>(a, dst, b < a.M ? b : 0u, RPW, rr, lu, units, G);
     };
     auto first_weights = [&]() {
         // the prologue's own loads go out first (nothing of the weight
@@ -904,7 +906,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
         uint32_t seg_start = 0;
         int seg = 0;
         if constexpr (NMAT == 1) seg = step_segment(a, rb, seg_start);
-        void *out0 = stk(NMAT == 1 ? (seg == 0 ? a.m0.out : (seg == 1 ? a.m1.out : a.m2.out)) : a.m0.out,
+        void *out0 = stk<STK>(NMAT == 1 ? (seg == 0 ? a.m0.out : (seg == 1 ? a.m1.out : a.m2.out)) : a.m0.out,
                          a.stk.out);
         if constexpr (FULL) {
             // The NMAT x R row totals in one exchange-halving reduction
@@ -928,7 +930,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
             const uint32_t row = rb + (uint32_t)r;   // < M
             const bool head = (lane & ((64 / V) - 1)) == 0 && (NMAT == 1 || lane < 32);
             if (head && row >= base)
-                qmv_epilogue<EPI, ODT, FAITH, NMAT>(a, out0, row, row - seg_start, tot, c.res[0]);
+                qmv_epilogue<EPI, ODT, FAITH, NMAT, STK>(a, out0, row, row - seg_start, tot, c.res[0]);
         } else {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
@@ -937,7 +939,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                 for (int m = 0; m < NMAT; ++m) tot[m] = group_sum(acc[m][r], LPR);
                 const uint32_t row = base + (uint32_t)(r * RPW + rr);
                 if (ll == 0 && row < a.M)
-                    qmv_epilogue<EPI, ODT, FAITH, NMAT>(a, out0, row, row - seg_start, tot, c.res[r]);
+                    qmv_epilogue<EPI, ODT, FAITH, NMAT, STK>(a, out0, row, row - seg_start, tot, c.res[r]);
             }
         }
     };
@@ -958,18 +960,18 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
 // the full-row kernel's and a SIMD interleaves several short waves instead
 // of running one long one.  The KS row partials meet in LDS (double
 // buffered: one barrier per step).
-template <int XDT, int EPI, int ODT, int KS, int R>
+template <int XDT, int EPI, int ODT, int KS, int R, bool STK>
 __global__ __launch_bounds__(64 * KS) void qmv1_splitk_kernel(QmvArgs a) {
     static_assert(EPI == EPI_STORE || EPI == EPI_RESADD, "store or residual add");
     const int lane = threadIdx.x & 63, kp = threadIdx.x >> 6;
-    const void *const ax = stk(a.x, a.stk.x);
+    const void *const ax = stk<STK>(a.x, a.stk.x);
     const uint32_t K = a.K, units = K >> 5, G = K / a.gs, M = a.M;
     const uint32_t u = (uint32_t)(kp * 64 + lane);
     const bool uv = u < units;
     const uint32_t uc = uv ? u : 0u;
-    const gptr<const uint32_t> codes = stk(uniform_ptr(a.m0.codes), a.stk.codes);
-    const gptr<const uint16_t> scales = stk(uniform_ptr(a.m0.scales), a.stk.scales);
-    float *const out = stk((float *)a.m0.out, a.stk.out);
+    const gptr<const uint32_t> codes = stk<STK>(uniform_ptr(a.m0.codes), a.stk.codes);
+    const gptr<const uint16_t> scales = stk<STK>(uniform_ptr(a.m0.scales), a.stk.scales);
+    float *const out = stk<STK>((float *)a.m0.out, a.stk.out);
     __shared__ float part[2][KS][R];
 
     struct Step { uint32_t cw[R]; uint16_t sc[R]; float prev; };
@@ -1108,11 +1110,11 @@ bool q1_matrix_cores_wanted(nnz_ctx *ctx, const nnz_qmv_dims &d, bool stacked) {
 }
 
 // Blocks per matrix of a stacked launch: the caller's choice, else enough
-// for about 2048 blocks in all (every block amortises its prologue -- the
-// input slice or the nibble tables -- over many rows), never more than a
-// single launch of the shape would use.
+// for about 8192 blocks in all (measured, 256 config-1 matrices: 32 blocks
+// each 0.70 of 8 TB/s, 8 each 0.62), never more than a single launch of the
+// shape would use.
 uint32_t stack_blocks(const nnz_qmv_stack *stk, uint32_t single) {
-    uint32_t b = stk->blocks_per_matrix ? stk->blocks_per_matrix : ceil_div(2048u, stk->count);
+    uint32_t b = stk->blocks_per_matrix ? stk->blocks_per_matrix : ceil_div(8192u, stk->count);
     return b < 1 ? 1 : (b > single ? single : b);
 }
 
@@ -1152,6 +1154,14 @@ int check_dims(nnz_ctx *ctx, const nnz_qmv_dims &d, const char *name) {
     return NNZ_OK;
 }
 
+// The variants the stacked entry points launch (f32 in and out): Q1 and Q4
+// single matrices, the Q1 pair with SiLU.
+template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH>
+constexpr bool stackable() {
+    return XIN == XIN_X && !FAITH && XDT == NNZ_F32 && ODT == NNZ_F32 &&
+           ((NMAT == 1 && EPI == EPI_STORE) || (BITS == 1 && NMAT == 2 && EPI == EPI_SILU));
+}
+
 // Nibble tables take NV * 32 KB of LDS per block.
 constexpr int LUT_MAX_NV = 3;
 
@@ -1161,7 +1171,20 @@ constexpr int step_words(int BITS, int NMAT, int NV, int R) { return NMAT * R * 
 template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH, int NV, bool LUT, bool FULL>
 void launch_r(nnz_ctx *ctx, const QmvArgs &a, int R, uint32_t blocks, uint32_t gy) {
     dim3 grid(blocks, gy), block(256);
-#define QK(RR) qmv_kernel<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, RR, LUT, FULL><<<grid, block, 0, ctx->stream>>>(a)
+    // stacked launches (gy > 1) of the stackable variants take the kernel
+    // with per-matrix offsets; every other launch the one without
+    constexpr bool STACKABLE = stackable<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH>();
+#define QK(RR)                                                                                           \
+    do {                                                                                                 \
+        if constexpr (STACKABLE) {                                                                       \
+            if (gy > 1) {                                                                                \
+                qmv_kernel<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, RR, LUT, FULL, true>               \
+                    <<<grid, block, 0, ctx->stream>>>(a);                                                \
+                break;                                                                                   \
+            }                                                                                            \
+        }                                                                                                \
+        qmv_kernel<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH, NV, RR, LUT, FULL, false><<<grid, block, 0, ctx->stream>>>(a); \
+    } while (0)
     if (R == 8) {
         // long matrices only (the 1-bit LM head): more rows in flight per wave
         if constexpr (LUT && NMAT == 1 && step_words(BITS, NMAT, NV, 8) <= 32) QK(8);
@@ -1209,9 +1232,11 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
                   const nnz_qmv_stack *stk = nullptr) {
     constexpr bool NORM = XIN == XIN_NORM;
     constexpr bool MERGE = XIN == XIN_MERGE;
+    constexpr bool STACKABLE = stackable<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH>();
     NNZ_CHECK_CTX(ctx);
     int rc = check_dims(ctx, d, name);
     if (rc) return rc;
+    NNZ_REQUIRE(ctx, !stk || STACKABLE, NNZ_EUNSUPPORTED, "%s: no stacked form", name);
     // Stacked launch: `count` matrices of this shape at fixed byte strides,
     // one block row each (x and the outputs advance by their own strides).
     const uint32_t gy = stk ? stk->count : 1u;
@@ -1322,15 +1347,27 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
                 blocks = stack_blocks(stk, blocks);
             }
             const dim3 grid(blocks, gy);
+            // the stacked form only for the stackable shape (config 2's)
+#define SPLITK(KS_, TH_)                                                                          \
+    do {                                                                                          \
+        if constexpr (STACKABLE) {                                                                \
+            if (gy > 1) {                                                                         \
+                qmv1_splitk_kernel<XDT, EPI, ODT, KS_, SR, true><<<grid, TH_, 0, ctx->stream>>>(a); \
+                break;                                                                            \
+            }                                                                                     \
+        }                                                                                         \
+        qmv1_splitk_kernel<XDT, EPI, ODT, KS_, SR, false><<<grid, TH_, 0, ctx->stream>>>(a);      \
+    } while (0)
             switch (nv) {
-            case 2: qmv1_splitk_kernel<XDT, EPI, ODT, 2, SR><<<grid, 128, 0, ctx->stream>>>(a); break;
-            case 3: qmv1_splitk_kernel<XDT, EPI, ODT, 3, SR><<<grid, 192, 0, ctx->stream>>>(a); break;
-            case 4: qmv1_splitk_kernel<XDT, EPI, ODT, 4, SR><<<grid, 256, 0, ctx->stream>>>(a); break;
-            case 5: qmv1_splitk_kernel<XDT, EPI, ODT, 5, SR><<<grid, 320, 0, ctx->stream>>>(a); break;
-            case 6: qmv1_splitk_kernel<XDT, EPI, ODT, 6, SR><<<grid, 384, 0, ctx->stream>>>(a); break;
-            case 7: qmv1_splitk_kernel<XDT, EPI, ODT, 7, SR><<<grid, 448, 0, ctx->stream>>>(a); break;
-            default: qmv1_splitk_kernel<XDT, EPI, ODT, 8, SR><<<grid, 512, 0, ctx->stream>>>(a); break;
+            case 2: SPLITK(2, 128); break;
+            case 3: SPLITK(3, 192); break;
+            case 4: SPLITK(4, 256); break;
+            case 5: SPLITK(5, 320); break;
+            case 6: SPLITK(6, 384); break;
+            case 7: SPLITK(7, 448); break;
+            default: SPLITK(8, 512); break;
             }
+#undef SPLITK
             NNZ_LAUNCHED(ctx);
             return NNZ_OK;
         }

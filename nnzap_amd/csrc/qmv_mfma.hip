@@ -11,25 +11,32 @@
 //     nibbles of one B register.  The table holds one copy per lane (entry
 //     byte * 64 + lane), so a lookup's 64 reads hit 64 distinct banks, and its
 //     address is one v_perm of the code word with the lane offset.
-//   A (fp8 e4m3, 16 rows): x split into NSPLIT rows of signed integer digits
-//     (|d| <= 16, exact in e4m3) with one power-of-two scale per row and
+//   A (fp4 e2m1, 16 rows): x split into NDIG rows of signed integer digits
+//     (|d| <= 4, exact in e2m1) with one power-of-two scale per row and
 //     group (the MFMA's E8M0 block scales, equal for the group's four
-//     32-column blocks): x_c = sum_s d_s,c 2^e_s + rest, |rest| <= 2^-25 of
-//     the group's largest |x|; rows NSPLIT..15 are zero.
-//   C row s = the group's signed sum of split s, exact (an integer times
-//     2^e_s).  Their total times the group's f16 scale accumulates in f32.
+//     32-column blocks): x_c = sum_s d_s,c 2^e_s + rest; each row gains at
+//     least two bits, |rest| <= 2^-25 of the group's largest |x|; rows
+//     NDIG..15 are zero.
+//   C row s = the group's signed sum of digit row s, exact (an integer of
+//     at most 4 * 128 times 2^e_s: the matrix core adds such sums exactly,
+//     whereas rows of general fp8 values spanning several binades lose bits
+//     in its adder, measured 2^-14 of the largest product).  The rows'
+//     total times the group's f16 scale accumulates in f32.
 //
-// A wave owns whole 16-row tiles: its lane (n, q) (n = lane % 16, q =
-// lane / 16) loads the 16 bytes of group 4S + q of row n for every 512-column
-// piece S, a 4 x 4 transpose across the lane rows (two v_permlane32_swap and
-// two v_permlane16_swap) hands lane (n, g) word g of each of the four groups
-// -- the B layout -- and the x splits (A) stay in registers for the whole
-// kernel (16 groups x 8 VGPRs).  Tiles are software-pipelined one ahead.
-// The MFMA operand layouts used here (B: lane row g holds k = 32 g .. 32 g +
-// 31 of column lane % 16; A: lane row g holds k = 16 g .. 16 g + 15 in bytes
-// 0-15 and k = 64 + 16 g .. in bytes 16-31 of row lane % 16; A's scale lane
-// m + 16 b covers k = 32 b .. 32 b + 31; C[m][n] at lane n + 16 (m / 4),
-// element m % 4) were established by one-hot probes on MI355X.
+// A wave owns whole 16-row tiles (4 KB of codes, contiguous): each of its
+// four load instructions reads one contiguous KB (4 rows), the tile goes
+// through a per-wave LDS staging area with a 272-byte row pitch, and lane
+// (n, g) reads word g of each group of row n from it -- the B layout, with no
+// bank conflicts.  (Reading 16 rows x 64 B per instruction instead, which
+// needs no staging, streams at 5.1-5.7 TB/s on MI355X against 6.5-7.0 for
+// contiguous KB instructions, measured without any arithmetic.)  The digit
+// rows (A) stay in registers for the whole kernel (16 groups x 4 VGPRs).
+// One block per CU shares the table: 12 waves for a single matrix, 8 for a
+// pair; each wave keeps three tiles in flight.
+// The MFMA operand layouts used here (fp4 A and B: lane row g holds k =
+// 32 g .. 32 g + 31 of row / column lane % 16, nibble j = k 32 g + j; A's
+// scale lane m + 16 b covers k = 32 b .. 32 b + 31; C[m][n] at lane n +
+// 16 (m / 4), element m % 4) were established by one-hot probes on MI355X.
 #include <type_traits>
 #include <utility>
 
@@ -38,14 +45,20 @@
 namespace {
 
 typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int NSPLIT = 6;      // digit rows of x (A rows 0-3 in lane row 0, 4-5 in lane row 1)
+constexpr int NDIG = 12;       // digit rows of x (A rows; C rows 0-11 in lane rows 0-2)
 constexpr int KG = 16;         // 128-column groups per row (K = 2048)
 constexpr int KC = KG * 128;   // columns
 constexpr int NS = KG / 4;     // 512-column pieces per row
-constexpr int THREADS = 256;
+// Threads per block: one block per CU.  A single matrix: 12 waves of <= 168
+// VGPRs; a pair: 8 waves of <= 256 (its loop needs ~210: at 168 it spills,
+// even with two units in flight).
+template <int NMAT>
+constexpr int threads_of() { return NMAT == 2 ? 512 : 768; }
+constexpr int PREP = KC / 8;   // threads preparing x (8 columns each)
 
 enum { EPI_STORE = 0, EPI_RESADD = 1, EPI_SILU = 2 };
 enum { XIN_X = 0, XIN_NORM = 1 };
@@ -75,9 +88,9 @@ __host__ __device__ constexpr uint32_t spread4(uint32_t v) {
     return (v & 1u) | ((v & 2u) << 3) | ((v & 4u) << 6) | ((v & 8u) << 9);
 }
 
-// Weights of one 16-row tile of one matrix (lane (n, q)): the 16 bytes of
-// group 4S + q of row n for each piece S, the row's 16 f16 scales, and the
-// residual entry of the row (EPI_RESADD).
+// Weights of one 16-row tile of one matrix: lane l holds group l % 16 of row
+// 4S + l / 16 for each S (16 bytes), the 16 f16 scales of row l % 16, and the
+// residual entry of that row (EPI_RESADD).
 struct Tile {
     u32x4 code[NS];
     u32x4 scl[2];
@@ -94,31 +107,11 @@ __device__ __forceinline__ void static_for(F &&f) {
     static_for_seq(f, std::make_integer_sequence<int, N>{});
 }
 
-// 4 x 4 transpose across the four 16-lane rows: in, register i of lane row
-// q holds word i of group q; out, register i of lane row g holds word g of
-// group i (the B layout of group i).
-__device__ __forceinline__ void transpose4(uint32_t (&w)[4]) {
-    auto s32 = [](uint32_t &a, uint32_t &b) {
-        const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
-        a = r[0];
-        b = r[1];
-    };
-    auto s16 = [](uint32_t &a, uint32_t &b) {
-        const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
-        a = r[0];
-        b = r[1];
-    };
-    s32(w[0], w[2]);
-    s32(w[1], w[3]);
-    s16(w[0], w[1]);
-    s16(w[2], w[3]);
-}
-
-// One group's product: A (fp8, format 0) x B (fp4, format 4), A's scale in
+// One group's product: A (fp4, format 4) x B (fp4, format 4), A's scale in
 // byte `SEL` of `sa` (B's scale 1.0).
 template <int SEL>
 __device__ __forceinline__ v4f mfma_sel(const v8i &A, const v8i &B, int sa) {
-    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, v4f{0.f, 0.f, 0.f, 0.f}, 0, 4, SEL, sa,
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(A, B, v4f{0.f, 0.f, 0.f, 0.f}, 4, 4, SEL, sa,
                                                             0, 0x7F);
 }
 __device__ __forceinline__ v4f mfma_group(int sel, const v8i &A, const v8i &B, int sa) {
@@ -131,8 +124,10 @@ __device__ __forceinline__ v4f mfma_group(int sel, const v8i &A, const v8i &B, i
 }
 
 template <int XDT, int NMAT, int XIN, int EPI, int ODT>
-__global__ __launch_bounds__(THREADS) __attribute__((amdgpu_waves_per_eu(2)))
+__global__ __launch_bounds__(threads_of<NMAT>()) __attribute__((amdgpu_waves_per_eu(NMAT == 2 ? 2 : 3)))
 void qmv1_mfma_kernel(MqArgs a) {
+    constexpr int THREADS = threads_of<NMAT>();
+    constexpr int WAVES = THREADS / 64;
     static_assert(NMAT == 1 || EPI == EPI_SILU, "pairs take the SiLU epilogue");
     static_assert(NMAT == 2 || EPI != EPI_SILU, "SiLU takes a pair");
     const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -142,10 +137,16 @@ void qmv1_mfma_kernel(MqArgs a) {
 
     // Lane-private fp4 tables: entry b (byte value) at [b][lane].
     __shared__ __align__(16) uint32_t tab[256 * 64];
-    // x splits: split s, column c at xs8[s * KC + c]; scales [s][b][G] (E8M0).
-    __shared__ __align__(16) uint8_t xs8[NSPLIT * KC];
-    __shared__ __align__(16) uint8_t sc8[NSPLIT * 4 * KG];
-    __shared__ float red[THREADS / 64];
+    // digit rows: row s, columns 8 w .. 8 w + 7 in dword xs4[s * PREP + w]
+    // (nibble j = column 8 w + j); scales sc8[s * KG + G] (E8M0).
+    // (rows NDIG..15 are zero, so every lane loads its A row unconditionally)
+    __shared__ __align__(16) uint32_t xs4[16 * PREP];
+    __shared__ __align__(16) uint8_t sc8[16 * KG];
+    __shared__ float red[16];
+    // per-wave staging of one tile's codes: 16 rows at a 272-byte pitch
+    constexpr int STG_PITCH = KC / 8 + 16;
+    __shared__ __align__(16) char stage[WAVES * 16 * STG_PITCH];
+    char *const stg = stage + wid * 16 * STG_PITCH;
 
     const uint32_t *c0 = stk(a.codes0, a.cs), *c1 = stk(a.codes1, a.cs);
     const uint16_t *s0 = stk(a.scales0, a.ss), *s1 = stk(a.scales1, a.ss);
@@ -155,8 +156,8 @@ void qmv1_mfma_kernel(MqArgs a) {
     const __amdgpu_buffer_rsrc_t sr[2] = {rsrc(s0), rsrc(NMAT == 2 ? s1 : s0)};
 
     // This wave's units: (tile, matrix) pairs, tiles gw, gw + nw, ...
-    const uint32_t gw = __builtin_amdgcn_readfirstlane(blockIdx.x * (THREADS / 64) + wid);
-    const uint32_t nw = gridDim.x * (THREADS / 64);
+    const uint32_t gw = __builtin_amdgcn_readfirstlane(blockIdx.x * WAVES + wid);
+    const uint32_t nw = gridDim.x * WAVES;
     const uint32_t ntile = gw < T ? ceil_div(T - gw, nw) : 0u;
     const uint32_t nunit = ntile * NMAT;
 
@@ -167,16 +168,21 @@ void qmv1_mfma_kernel(MqArgs a) {
     constexpr uint32_t OB = ODT == NNZ_F32 ? 4u : 2u;
     const __amdgpu_buffer_rsrc_t orc =
         __builtin_amdgcn_make_buffer_rsrc(op, (short)0, (int)(M * (EPI == EPI_RESADD ? 4u : OB)), 0x00020000);
+    // Codes: instruction S reads rows 4S..4S+3 of the tile, one contiguous KB
+    // (lane l: row 4S + l / 16, bytes 16 (l % 16) .. of it -- the whole
+    // group l % 16); measured on MI355X, a read stream of contiguous KB
+    // instructions runs at 6.5-7.0 TB/s, one of 16 rows x 64 B at 5.1-5.7.
     auto load = [&](Tile &t, uint32_t k, int mat) {
         const uint32_t tile = gw + (k / NMAT) * nw;
         const uint32_t row0 = tile * 16u;
         const uint32_t row = min(row0 + (uint32_t)n, M - 1u);
-        const uint32_t co = row * (uint32_t)(KC / 8) + (uint32_t)q * 16u;
         const uint32_t so = row * (uint32_t)(KG * 2);
 #pragma unroll
-        for (int S = 0; S < NS; ++S)
+        for (int S = 0; S < NS; ++S) {
+            const uint32_t crow = min(row0 + 4u * S + ((uint32_t)lane >> 4), M - 1u);
             t.code[S] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                      cr[mat], co + (uint32_t)S * 64u, 0, 2));
+                                                      cr[mat], crow * (uint32_t)(KC / 8) + ((uint32_t)lane & 15u) * 16u, 0, 2));
+        }
 #pragma unroll
         for (int h = 0; h < 2; ++h)
             t.scl[h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
@@ -188,15 +194,17 @@ void qmv1_mfma_kernel(MqArgs a) {
     // ---- prologue loads (x, or the residual and norm weights) go out first,
     // the first unit's weights right after them: loads complete in order, so
     // the prologue waits for its own data only.
+    // threads >= PREP (waves 4..11) read x at column 0 (in bounds, unused)
+    const uint32_t xt = tid < PREP ? (uint32_t)tid : 0u;
     float4 xa[2], wn[2];
     uint4 xh;
     if constexpr (XIN == XIN_NORM) {
-        xa[0] = ((const float4 *)xp)[2 * tid]; xa[1] = ((const float4 *)xp)[2 * tid + 1];
-        wn[0] = ((const float4 *)a.norm_w)[2 * tid]; wn[1] = ((const float4 *)a.norm_w)[2 * tid + 1];
+        xa[0] = ((const float4 *)xp)[2 * xt]; xa[1] = ((const float4 *)xp)[2 * xt + 1];
+        wn[0] = ((const float4 *)a.norm_w)[2 * xt]; wn[1] = ((const float4 *)a.norm_w)[2 * xt + 1];
     } else if constexpr (XDT == NNZ_F32) {
-        xa[0] = ((const float4 *)xp)[2 * tid]; xa[1] = ((const float4 *)xp)[2 * tid + 1];
+        xa[0] = ((const float4 *)xp)[2 * xt]; xa[1] = ((const float4 *)xp)[2 * xt + 1];
     } else {
-        xh = ((const uint4 *)xp)[tid];
+        xh = ((const uint4 *)xp)[xt];
     }
     __builtin_amdgcn_sched_barrier(0);
     Tile ta, tb;
@@ -214,7 +222,7 @@ void qmv1_mfma_kernel(MqArgs a) {
         ss = wave_sum(ss);
         if (lane == 0) red[wid] = ss;
         __syncthreads();
-        ss = (red[0] + red[1]) + (red[2] + red[3]);
+        ss = (red[0] + red[1]) + (red[2] + red[3]);   // waves 0-3 hold the columns
         const float rms = rsqrtf(ss / (float)KC + a.eps);
         // the normalised input is stored as f16 (rms_norm_f16out)
 #pragma unroll
@@ -237,30 +245,24 @@ void qmv1_mfma_kernel(MqArgs a) {
         }
     }
 
-    // ---- fp4 tables: dwords [1024 it + 4 tid, +4) hold entry b = 16 it + tid / 16
-    {
-        const uint32_t lo = spread4((uint32_t)tid >> 4);
-#pragma unroll
-        for (int it = 0; it < 16; ++it) {
-            const uint32_t v = 0xAAAAAAAAu ^ ((lo | (spread4((uint32_t)it) << 16)) << 3);
-            *(u32x4 *)&tab[it * 1024 + tid * 4] = u32x4{v, v, v, v};
-        }
+    // ---- fp4 tables: the 16-byte piece i (dwords 4 i .. 4 i + 3) holds entry
+    // b = i / 16 for lanes 4 (i % 16) .. +3
+    for (uint32_t i = (uint32_t)tid; i < 256u * 16u; i += THREADS) {
+        const uint32_t b = i >> 4;
+        const uint32_t v = 0xAAAAAAAAu ^ ((spread4(b & 15u) | (spread4(b >> 4) << 16)) << 3);
+        *(u32x4 *)&tab[4 * i] = u32x4{v, v, v, v};
     }
 
-    // ---- x splits: NSPLIT signed digits per column, one scale per group ----
-    // Split s of group G: d = rint(r / 2^e) with 2^e set by the group's
-    // largest |r| (max |r| / 2^e in [8, 16), so |d| <= 16, every such integer
-    // exact in e4m3), then r -= d 2^e (exact).  Each MFMA row sums integers
-    // of at most 16 * 128 in magnitude, which the matrix core adds exactly
-    // (rows of general e4m3 values spanning several binades lose bits in its
-    // adder: measured 2^-14 of the largest product); six digits leave
-    // |r| <= 2^-25 of the group's largest |x| (float32 inputs within 3e-8 of
-    // the exact row sums, measured).  Thread t holds columns 8t..8t+7; the
-    // 16 threads of a group are one 16-lane row.
-    {
+    // ---- digit rows: NDIG signed digits per column, one scale per group ----
+    // Row s of group G: d = rint(r / 2^e) with 2^e set by the group's largest
+    // |r| (max |r| / 2^e in [2, 4), so |d| <= 4, every such integer exact in
+    // e2m1), then r -= d 2^e (exact): |r| drops at least fourfold per row.
+    // Thread t < PREP holds columns 8t..8t+7; a group's 16 threads are one
+    // 16-lane row (the maximum by DPP).
+    if (tid < PREP) {
         const uint32_t G = (uint32_t)tid >> 4;
 #pragma unroll
-        for (int s = 0; s < NSPLIT; ++s) {
+        for (int s = 0; s < NDIG; ++s) {
             float mx = 0.f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(r[i]));
@@ -269,7 +271,7 @@ void qmv1_mfma_kernel(MqArgs a) {
             mx = fmaxf(mx, dpp_move<DPP_ROW_HALF_MIRROR>(mx, 0.f));
             mx = fmaxf(mx, dpp_move<DPP_ROW_MIRROR>(mx, 0.f));
             int e = 0;
-            if (mx > 0.f) e = max(-126, min(126, __builtin_amdgcn_frexp_expf(mx) - 4));
+            if (mx > 0.f) e = max(-126, min(126, __builtin_amdgcn_frexp_expf(mx) - 2));
             const float inv = __int_as_float((127 - e) << 23), pw = __int_as_float((127 + e) << 23);
             float d[8];
 #pragma unroll
@@ -277,33 +279,30 @@ void qmv1_mfma_kernel(MqArgs a) {
                 d[i] = rintf(r[i] * inv);
                 r[i] = fmaf(-d[i], pw, r[i]);
             }
-            int qa = __builtin_amdgcn_cvt_pk_fp8_f32(d[0], d[1], 0, false);
-            qa = __builtin_amdgcn_cvt_pk_fp8_f32(d[2], d[3], qa, true);
-            int qb = __builtin_amdgcn_cvt_pk_fp8_f32(d[4], d[5], 0, false);
-            qb = __builtin_amdgcn_cvt_pk_fp8_f32(d[6], d[7], qb, true);
-            *(uint2 *)&xs8[s * KC + 8 * tid] = make_uint2((uint32_t)qa, (uint32_t)qb);
-            if ((tid & 15) < 4) sc8[(s * 4 + (tid & 3)) * KG + G] = (uint8_t)(127 + e);
+            // digits are exact in e2m1; the first operand lands in the low nibble
+            uint32_t q = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, d[0], d[1], 1.f, 0);
+            q = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(q, d[2], d[3], 1.f, 1);
+            q = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(q, d[4], d[5], 1.f, 2);
+            q = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(q, d[6], d[7], 1.f, 3);
+            xs4[s * PREP + tid] = q;
+            if ((tid & 15) == 0) sc8[s * KG + G] = (uint8_t)(127 + e);
+        }
+#pragma unroll
+        for (int s = NDIG; s < 16; ++s) {
+            xs4[s * PREP + tid] = 0u;
+            if ((tid & 15) == 0) sc8[s * KG + G] = 127;   // 1.0: finite, the row is zero
         }
     }
     __syncthreads();
 
-    // ---- A operands (x splits) and their scales, kept for the whole kernel
-    v8i A[KG];
+    // ---- A operands (digit rows) and their scales, kept for the whole kernel
+    v4i A[KG];
     uint32_t sa[KG / 4];
-    if (n < NSPLIT) {
 #pragma unroll
-        for (int G = 0; G < KG; ++G) {
-            const u32x4 lo = *(const u32x4 *)&xs8[n * KC + G * 128 + 16 * q];
-            const u32x4 hi = *(const u32x4 *)&xs8[n * KC + G * 128 + 64 + 16 * q];
-            A[G] = v8i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-        }
-        const u32x4 sv = *(const u32x4 *)&sc8[(n * 4 + q) * KG];
+    for (int G = 0; G < KG; ++G) A[G] = __builtin_bit_cast(v4i, *(const u32x4 *)&xs4[n * PREP + G * 16 + 4 * q]);
+    {
+        const u32x4 sv = *(const u32x4 *)&sc8[n * KG];
         sa[0] = sv.x; sa[1] = sv.y; sa[2] = sv.z; sa[3] = sv.w;
-    } else {
-#pragma unroll
-        for (int G = 0; G < KG; ++G) A[G] = v8i{0, 0, 0, 0, 0, 0, 0, 0};
-#pragma unroll
-        for (int i = 0; i < KG / 4; ++i) sa[i] = 0x7F7F7F7Fu;   // 1.0: finite, rows are zero
     }
 
     // ---- main loop -----------------------------------------------------------
@@ -318,31 +317,50 @@ void qmv1_mfma_kernel(MqArgs a) {
     auto compute = [&](const Tile &t, uint32_t k, auto mat_c) {
         constexpr int MAT = decltype(mat_c)::value;
         float acc = 0.f;
+        // the tile's codes into this wave's staging rows (272-byte pitch),
+        // then lane (n, g) reads word g of each group of row n: banks
+        // 4n + 4G + g, all distinct for a read (LDS keeps a wave's order)
+#pragma unroll
+        for (int S = 0; S < NS; ++S)
+            *(u32x4 *)(stg + (4 * S + (lane >> 4)) * STG_PITCH + 16 * (lane & 15)) = t.code[S];
 #pragma unroll
         for (int S = 0; S < NS; ++S) {
-            uint32_t w[4] = {t.code[S].x, t.code[S].y, t.code[S].z, t.code[S].w};
-            transpose4(w);
+            uint32_t w[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int G = 4 * S + i;
-                uint32_t b4[4];
+            for (int i = 0; i < 4; ++i) w[i] = *(const uint32_t *)(stg + n * STG_PITCH + 16 * (4 * S + i) + 4 * q);
+            // the piece's 16 table reads first (one LDS round trip for four
+            // groups), then its four independent MFMAs, then their sums
+            uint32_t b4[4][4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int bb = 0; bb < 4; ++bb) {
                     // address = byte bb of the word * 256 + lane * 4
                     const uint32_t off = __builtin_amdgcn_perm(w[i], lane4, 0x0C0C0000u | ((4u + bb) << 8));
-                    b4[bb] = *(const uint32_t *)(tb8 + off);
+                    b4[i][bb] = *(const uint32_t *)(tb8 + off);
                 }
-                const v8i B = v8i{(int)b4[0], (int)b4[1], (int)b4[2], (int)b4[3], 0, 0, 0, 0};
-                const v4f c = mfma_group(i, A[G], B, (int)sa[G >> 2]);
-                const float tsum = (c[0] + c[1]) + (c[2] + c[3]);
+            v4f c[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int G = 4 * S + i;
+                const v8i B = v8i{(int)b4[i][0], (int)b4[i][1], (int)b4[i][2], (int)b4[i][3], 0, 0, 0, 0};
+                const v8i A8 = v8i{A[G][0], A[G][1], A[G][2], A[G][3], 0, 0, 0, 0};
+                c[i] = mfma_group(i, A8, B, (int)sa[G >> 2]);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int G = 4 * S + i;
+                const float tsum = (c[i][0] + c[i][1]) + (c[i][2] + c[i][3]);
                 const uint32_t sw = t.scl[G >> 3][(G >> 1) & 3];
                 const float sc = (float)__builtin_bit_cast(f16_t, (uint16_t)((G & 1) ? (sw >> 16) : (sw & 0xFFFFu)));
                 acc = fmaf(sc, tsum, acc);
             }
         }
-        // splits 0-3 sit in lane row 0, split 4 in lane row 1
-        const float tot = acc + __int_as_float((int)__builtin_amdgcn_permlane16_swap(
-                                    __float_as_int(acc), __float_as_int(acc), false, false)[1]);
+        // digit rows 4r..4r+3 sit in lane row r: sum the four lane rows
+        const float t1 = acc + __int_as_float((int)__builtin_amdgcn_permlane32_swap(
+                                   __float_as_int(acc), __float_as_int(acc), false, false)[1]);
+        const float tot = t1 + __int_as_float((int)__builtin_amdgcn_permlane16_swap(
+                                   __float_as_int(t1), __float_as_int(t1), false, false)[1]);
         const uint32_t tile = gw + (k / NMAT) * nw;
         const uint32_t row = tile * 16u + (uint32_t)n;
         if constexpr (EPI == EPI_SILU && MAT == 0) {
@@ -362,24 +380,26 @@ void qmv1_mfma_kernel(MqArgs a) {
                 __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_rne(v), orc, off, 0, 0);
         }
     };
-    // Units in flight per wave: three for one matrix -- unit k + 2's loads
-    // are issued before anything of unit k's arithmetic (a scheduling fence:
-    // hoisted above them, the transposes would make the loads wait for unit
-    // k's data) -- and two for a pair (three spill: 2 x 24 more registers).
-    // The loop body covers one period of the ring (3 units; 2 for a pair,
-    // whose units alternate gate, up, so each position's matrix is a
-    // compile-time constant); the units left at the end run the same
+    // DEPTH units in flight per wave: unit k + DEPTH - 1's loads are issued
+    // before anything of unit k's arithmetic (a scheduling fence: hoisted
+    // above them, the transposes would make the loads wait for unit k's
+    // data).  The loop body covers one period of the ring; a pair's units
+    // alternate gate, up and its period is even, so each position's matrix
+    // is a compile-time constant.  The units left at the end run the same
     // positions with a (wave-uniform) guard.
-    constexpr int DEPTH = NMAT == 2 ? 2 : 3;
-    constexpr int PERIOD = DEPTH;
-    Tile tc;
+    constexpr int DEPTH = 3;
+    constexpr int PERIOD = NMAT == 2 ? 6 : 3;
+    Tile tc, td;
     if (nunit > 1) load(tb, 1, 1 % NMAT);
+    if constexpr (DEPTH > 3)
+        if (nunit > 2) load(tc, 2, 2 % NMAT);
     __builtin_amdgcn_sched_barrier(0);
     auto slot = [&](auto sc) -> Tile & {
         constexpr int S = decltype(sc)::value % DEPTH;
         if constexpr (S == 0) return ta;
         else if constexpr (S == 1) return tb;
-        else return tc;
+        else if constexpr (S == 2) return tc;
+        else return td;
     };
     uint32_t k = 0;
     auto body = [&](auto jc, bool guard) {
@@ -395,12 +415,14 @@ void qmv1_mfma_kernel(MqArgs a) {
     };
     for (; k + PERIOD <= nunit; k += PERIOD)
         static_for<PERIOD>([&](auto jc) { body(jc, false); });
+    // the rest (fewer than PERIOD units; a pair's count is even, so position
+    // J still takes matrix J % NMAT)
     static_for<PERIOD - 1>([&](auto jc) { body(jc, true); });
 }
 
 template <int XDT, int NMAT, int XIN, int EPI, int ODT>
 void launch(nnz_ctx *ctx, const MqArgs &a, uint32_t blocks, uint32_t gy) {
-    qmv1_mfma_kernel<XDT, NMAT, XIN, EPI, ODT><<<dim3(blocks, gy), THREADS, 0, ctx->stream>>>(a);
+    qmv1_mfma_kernel<XDT, NMAT, XIN, EPI, ODT><<<dim3(blocks, gy), threads_of<NMAT>(), 0, ctx->stream>>>(a);
 }
 
 }  // namespace
@@ -439,11 +461,11 @@ int nnz_q1_mfma_launch(nnz_ctx *ctx, const NnzQ1Mfma &c) {
     a.eps = c.eps;
     a.cs = c.cs; a.ss = c.ss; a.xs = c.xs; a.os = c.os;
     const uint32_t tiles = ceil_div(c.M, 16u);
-    // about two blocks per CU in all (75 KB of LDS and <= 256 VGPRs per lane
-    // each), never more than one wave per tile
+    // one 12-wave block per CU (the table's 64 KB of LDS and <= 168 VGPRs
+    // per lane), about 256 blocks in all, never more than one wave per tile
     const uint32_t gy = c.stack_count ? c.stack_count : 1u;
-    uint32_t blocks = c.blocks_per_matrix ? c.blocks_per_matrix : ceil_div(512u, gy);
-    blocks = min(blocks, ceil_div(tiles, (uint32_t)(THREADS / 64)));
+    uint32_t blocks = c.blocks_per_matrix ? c.blocks_per_matrix : ceil_div(256u, gy);
+    blocks = min(blocks, ceil_div(tiles, (uint32_t)(c.nmat == 2 ? threads_of<2>() : threads_of<1>()) / 64u));
     blocks = max(blocks, 1u);
 #define MQ(XDT, NMAT, XIN, EPI, ODT)                                                           \
     if (c.xdt == XDT && c.nmat == NMAT && c.xin == XIN && c.epi == EPI && c.odt == ODT) {     \

@@ -163,7 +163,7 @@ class StackedQWeights:
 
     def __init__(self, dev: Device, M: int, K: int, group_size: int, bits: int, count: int,
                  seed: int, scale_range=(0.01, 0.05), bias_range=(-0.1, 0.1),
-                 scale_dtype: int = DT_F16):
+                 scale_dtype: int = DT_F16, pad_bytes: int = 0):
         torch = _torch()
         td = dev.torch_device
         g = torch.Generator(device=td)
@@ -172,8 +172,12 @@ class StackedQWeights:
         self.scale_dtype = scale_dtype
         words = M * K * bits // 32
         ng = M * K // group_size
-        wpad = (words + 3) // 4 * 4
-        gpad = (ng + 7) // 8 * 8
+        # pad_bytes (a multiple of 16): extra bytes between consecutive
+        # matrices' codes and scales, so that their starts need not share
+        # the same low address bits
+        assert pad_bytes % 16 == 0
+        wpad = (words + 3) // 4 * 4 + pad_bytes // 4
+        gpad = (ng + 7) // 8 * 8 + pad_bytes // 2
         self.codes = torch.randint(-2 ** 31, 2 ** 31 - 1, (count, wpad), dtype=torch.int32,
                                    generator=g, device=td)
         sdt = torch.float16 if scale_dtype == DT_F16 else torch.bfloat16

@@ -217,7 +217,7 @@ def test_config5_golden(mdev, name):
         if sums:
             print(f"{name}: logits", flush=True)
             for s_ in sums:
-                s_["stride"] = gold.get("logit_stride", 512)
+                s_.setdefault("stride", gold.get("logit_stride", 512))
             _check_logit_summary(m.prefill(prompt, 0), sums[0], "last prompt token", rel)
             argmax_checked = 0
             for i, s_ in enumerate(sums[1:]):

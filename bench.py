@@ -147,8 +147,44 @@ def bench_decode(args, dev, lm_head=None, latency=True):
         n = min(len(g["tokens"]), args.steps)
         out["tokens_match_golden"] = bool(np.array_equal(toks[:n], np.array(g["tokens"][:n])))
         out["golden_compared"] = n
+    gold = os.path.join(ROOT, "tests", "golden", "config5_unit_tokens.json")
+    if os.path.exists(gold) and lm_head == "q1" and args.prompt == 512:
+        out.update(golden_unit_prefix(m, cfg, prompt, json.load(open(gold))))
     m.close()
     return out
+
+
+def golden_unit_prefix(m, cfg, prompt, g):
+    """Free-running greedy stream of the loaded decoder with its norm weights
+    switched to the fixture's (1 + N(0, 0.02)), against the oracle's 256
+    golden tokens: the length of the matching prefix, and the first step
+    where the oracle's top-2 margin is a near-tie (below twice the logit bar
+    of the parity test), from which on the streams may part.  Runs after the
+    timed region; the loaded model is left in the fixture's norm mode."""
+    from nnzap_amd import configs as cf
+    from nnzap_amd import model as MD
+    from nnzap_amd import synth as S
+
+    mode = g["norm_mode"]
+    m.upload(MD.T_FINAL_NORM, 0, cf.norm_weights(S.SEED_MODEL_BASE + 3, cfg.hidden_size, mode))
+    tids = {"attn_norm": MD.T_ATTN_NORM, "ffn_norm": MD.T_FFN_NORM,
+            "q_norm": MD.T_Q_NORM, "k_norm": MD.T_K_NORM}
+    for l in range(cfg.num_layers):
+        for name, arr in cf.layer_norm_weights(cfg, l, mode).items():
+            m.upload(tids[name], l, arr)
+    n = int(g["n_new"])
+    m.decode_begin(prompt, n)
+    m.decode_steps(n)
+    toks, _ = m.decode_read(n)
+    m.decode_end()
+    ref = np.array(g["tokens"][:n], dtype=np.int64)
+    toks = np.asarray(toks[:n], dtype=np.int64)
+    bad = np.nonzero(toks != ref)[0]
+    near = 2 * max(1e-3, 4 * g.get("fp32_noise", 0.0)) * g["logits"][0]["max_abs"]
+    ties = [i for i, mg in enumerate(g["margins"][:n]) if mg < near]
+    return {"tokens_match_golden_unit": int(bad[0]) if len(bad) else n,
+            "golden_unit_compared": n,
+            "golden_unit_first_near_tie": ties[0] if ties else None}
 
 
 def bench_decode_q4(args, dev):
@@ -915,6 +951,7 @@ def main():
                    "lm_head": args.lm_head, "prompt": args.prompt, "batch": 1,
                    "parallelism": "single GPU"},
         "roofline": roofline,
+        "tokens_match_golden_unit": dec.get("tokens_match_golden_unit"),
         "cpu_baseline": cpu,
         "cpu_configs": cpu_cfg,
         "decode": dec,

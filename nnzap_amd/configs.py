@@ -171,12 +171,21 @@ def decoder_weights(cfg: DecoderConfig, norm_mode: str = "small",
             M, K = proj_shape(cfg, name)
             layer[name] = q1_matrix(M, K, cfg.group_size, tensor_seed(l, 2 * i),
                                     tensor_seed(l, 2 * i + 1))
-        layer["attn_norm"] = norm_weights(tensor_seed(l, 20), H, norm_mode)
-        layer["ffn_norm"] = norm_weights(tensor_seed(l, 21), H, norm_mode)
-        layer["q_norm"] = norm_weights(tensor_seed(l, 22), cfg.head_dim, norm_mode)
-        layer["k_norm"] = norm_weights(tensor_seed(l, 23), cfg.head_dim, norm_mode)
+        layer.update(layer_norm_weights(cfg, l, norm_mode))
         dw.layers.append(layer)
     return dw
+
+
+def layer_norm_weights(cfg: DecoderConfig, l: int, norm_mode: str) -> dict:
+    """The four norm vectors of 1-bit decoder layer ``l`` (the final norm
+    is norm_weights(SEED_MODEL_BASE + 3, hidden, mode)).  Only these differ
+    between the norm modes, so a loaded model switches mode by uploading
+    them again."""
+    H = cfg.hidden_size
+    return {"attn_norm": norm_weights(tensor_seed(l, 20), H, norm_mode),
+            "ffn_norm": norm_weights(tensor_seed(l, 21), H, norm_mode),
+            "q_norm": norm_weights(tensor_seed(l, 22), cfg.head_dim, norm_mode),
+            "k_norm": norm_weights(tensor_seed(l, 23), cfg.head_dim, norm_mode)}
 
 
 def _decoder_weights_q4(cfg: DecoderConfig, norm_mode: str) -> DecoderWeights:

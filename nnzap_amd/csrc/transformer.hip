@@ -908,6 +908,209 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
     }
 }
 
+// The decode shape of attn_fused_kernel (head_dim 128, one query head per
+// block): same grid, chunking, outputs and cache append, organised by wave
+// so that one block barrier remains instead of six.
+//   * Every load is issued before the sequence length is read: the chunk's
+//     K rows and V groups are clamped to the cache (max_ctx), not to the live
+//     length, so they wait on nothing; rows past the length are masked by
+//     select (never multiplied), as are the blocks of chunks past it, which
+//     exit after issuing their loads.
+//   * Wave w owns tokens 16 w .. 16 w + 15 of the chunk.  Each wave normalises
+//     and rotates the query itself: lane l holds dims 2l, 2l + 1, a RoPE pair,
+//     so the rotation needs no partner exchange.  The scores take 4 lanes per
+//     token (32 dims each) and read the query from a wave-private LDS copy.
+//   * Softmax per wave (its own maximum and sum); P.V with lane l on dims 2l,
+//     2l + 1 over the wave's 16 tokens, the 16 weights read into scalar
+//     registers.
+//   * The new token (position seq - 1): the wave holding it normalises,
+//     rotates and f16-rounds the raw key in the pair layout, scores it with
+//     one whole-wave dot product, and takes its value from the raw
+//     projection (the writer block appends both to the caches).
+//   * The four waves' (m, l, o) meet in LDS after the one barrier; wave 0
+//     writes the output (one chunk) or the chunk's partials.
+constexpr int WTOK = FCHUNK / 4;   // tokens per wave
+
+__global__ __launch_bounds__(256) void attn_fused_wave_kernel(FusedAttnArgs a) {
+    constexpr int D = 128;
+    __shared__ __align__(16) float2 qsh[4][64];   // per wave: the rotated query (pair layout)
+    __shared__ float2 osh[4][64];                 // per wave: o of dims 2l, 2l + 1
+    __shared__ float2 mlsh[4];                    // per wave: (max, sum)
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const uint32_t bid = blockIdx.x, span = 8 * a.parts;
+    const uint32_t j = a.parts == 1 ? 0u : (bid % span) / 8;
+    const uint32_t u = a.parts == 1 ? bid : (bid / span) * 8 + bid % 8;
+    if (u >= a.units) return;
+    const uint32_t c = u % a.nchunks, h = u / a.nchunks, qh = h * a.gfull + j;
+    const uint32_t t0 = c * FCHUNK, wt0 = (uint32_t)w * WTOK;
+
+    // ---- loads: q, norm scales, the new K/V projections and the RoPE
+    // frequency first (the prologue waits for these only), then K and V
+    const uint32_t qpair = ((const uint32_t *)(a.q + (size_t)qh * D))[lane];
+    const float2 qn2 = ((const float2 *)a.qn)[lane];
+    const uint32_t kpair = ((const uint32_t *)(a.kr + (size_t)h * D))[lane];
+    const float2 kn2 = ((const float2 *)a.kn)[lane];
+    const uint32_t vpair = ((const uint32_t *)(a.vr + (size_t)h * D))[lane];
+    // a null table gets an empty range: the load returns 0 without touching
+    // memory (no branch around a load) and the frequency is computed below
+    const float freq_t = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.inv_freq), (short)0,
+                                          a.inv_freq ? D * 2 : 0, 0x00020000),
+        lane * 4, 0, 0));
+    const size_t kvh = (size_t)h * a.max_ctx * D;
+    const int tk = lane >> 2, sub = lane & 3;
+    uint4 kreg[4];
+    {
+        const uint32_t kt = min(t0 + wt0 + (uint32_t)tk, a.max_ctx - 1);
+        const uint4 *kp = (const uint4 *)(a.kc + kvh + (size_t)kt * D + sub * 32);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kreg[i] = kp[i];
+    }
+    // V [d][t]: dims 2l, 2l + 1, two 8-token groups each (a group starting
+    // at or past max_ctx, which max_ctx % 8 == 0 keeps whole, reads group 0)
+    uint4 vreg[2][2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+        const f16_t *row = a.vc + kvh + (size_t)(2 * lane + e) * a.max_ctx;
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            const uint32_t vs = t0 + wt0 + 8u * g;
+            vreg[e][g] = *(const uint4 *)(row + (vs < a.max_ctx ? vs : 0u));
+        }
+    }
+
+    const uint32_t seq = a.d_seq ? *a.d_seq : a.seq_len;
+    if (t0 >= seq) return;   // block-uniform: no barrier is pending
+    const uint32_t pos = seq - 1;
+    const uint32_t len = min((uint32_t)FCHUNK, seq - t0);
+    const bool wnew = pos >= t0 + wt0 && pos < t0 + wt0 + WTOK;   // wave-uniform
+
+    // ---- q: RMSNorm * q_norm, RoPE (consecutive pairs), kept f32
+    const float freq = a.inv_freq ? freq_t : rope_inv_freq(lane, D, a.theta);
+    float sn, cs;
+    sincosf((float)pos * freq, &sn, &cs);
+    float qe, qo;
+    {
+        float q0, q1;
+        unpack2<NNZ_F16>(qpair, q0, q1);
+        const float r = rsqrtf(wave_sum(fmaf(q1, q1, q0 * q0)) / (float)D + a.eps);
+        const float x0 = q0 * r * qn2.x, x1 = q1 * r * qn2.y;
+        qe = fmaf(x0, cs, -x1 * sn);
+        qo = fmaf(x0, sn, x1 * cs);
+    }
+    qsh[w][lane] = make_float2(qe, qo);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- scores: lanes 4 tk .. 4 tk + 3 share token tk (32 dims each)
+    float dot = 0.f;
+    {
+        const float4 *q4 = (const float4 *)qsh[w] + sub * 8;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 qa = q4[2 * i], qb = q4[2 * i + 1];
+            const float qq[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+            const uint32_t wv[4] = {kreg[i].x, kreg[i].y, kreg[i].z, kreg[i].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float k0, k1;
+                unpack2<NNZ_F16>(wv[e], k0, k1);
+                dot = fmaf(qq[2 * e + 1], k1, fmaf(qq[2 * e], k0, dot));
+            }
+        }
+        dot += dpp_move<DPP_XOR1>(dot, 0.f);
+        dot += dpp_move<DPP_XOR2>(dot, 0.f);
+    }
+    float vn0 = 0.f, vn1 = 0.f;
+    if (wnew) {
+        // the new key: RMSNorm * k_norm, RoPE, f16; scored here, appended
+        // by the writer block
+        float k0, k1;
+        unpack2<NNZ_F16>(kpair, k0, k1);
+        const float r = rsqrtf(wave_sum(fmaf(k1, k1, k0 * k0)) / (float)D + a.eps);
+        const float x0 = k0 * r * kn2.x, x1 = k1 * r * kn2.y;
+        const float ke = f16_round(fmaf(x0, cs, -x1 * sn));
+        const float ko = f16_round(fmaf(x0, sn, x1 * cs));
+        const float snew = wave_sum(fmaf(qo, ko, qe * ke));
+        if ((uint32_t)tk == pos - t0 - wt0) dot = snew;
+        unpack2<NNZ_F16>(vpair, vn0, vn1);
+        if (j == 0) {
+            const f16_t he = (f16_t)ke, ho = (f16_t)ko;
+            ((uint32_t *)(a.kc + kvh + (size_t)pos * D))[lane] =
+                (uint32_t)__builtin_bit_cast(uint16_t, he) | ((uint32_t)__builtin_bit_cast(uint16_t, ho) << 16);
+            a.vc[kvh + (size_t)(2 * lane) * a.max_ctx + pos] = __builtin_bit_cast(f16_t, (uint16_t)(vpair & 0xFFFFu));
+            a.vc[kvh + (size_t)(2 * lane + 1) * a.max_ctx + pos] = __builtin_bit_cast(f16_t, (uint16_t)(vpair >> 16));
+        }
+    }
+
+    // ---- softmax over the wave's tokens
+    const bool tvalid = wt0 + (uint32_t)tk < len;
+    const float s = tvalid ? dot * a.scale : -INFINITY;
+    const float m = wave_max(s);                  // finite in wave 0 (token 0 is live)
+    const float p = tvalid ? expf(s - m) : 0.f;
+    const float l = wave_sum(sub == 0 ? p : 0.f);
+
+    // ---- P.V: lane l on dims 2l, 2l + 1
+    float pt[WTOK];
+#pragma unroll
+    for (int t = 0; t < WTOK; ++t) pt[t] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), 4 * t));
+    const bool plain = wt0 + WTOK <= len && !wnew;   // wave-uniform
+    float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+        const uint32_t wa[4] = {vreg[0][g].x, vreg[0][g].y, vreg[0][g].z, vreg[0][g].w};
+        const uint32_t wb[4] = {vreg[1][g].x, vreg[1][g].y, vreg[1][g].z, vreg[1][g].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int t = 8 * g + 2 * e;
+            float a0, a1, b0, b1;
+            unpack2<NNZ_F16>(wa[e], a0, a1);
+            unpack2<NNZ_F16>(wb[e], b0, b1);
+            if (!plain) {
+                // past the end: value 0 (the weight is 0 too; never NaN * 0)
+                const uint32_t tc = wt0 + (uint32_t)t;
+                if (tc >= len) a0 = b0 = 0.f;
+                if (tc + 1 >= len) a1 = b1 = 0.f;
+                if (t0 + tc == pos) { a0 = vn0; b0 = vn1; }
+                if (t0 + tc + 1 == pos) { a1 = vn0; b1 = vn1; }
+            }
+            o0 = fmaf(pt[t + 1], a1, fmaf(pt[t], a0, o0));
+            o1 = fmaf(pt[t + 1], b1, fmaf(pt[t], b0, o1));
+        }
+    }
+    osh[w][lane] = make_float2(o0, o1);
+    if (lane == 0) mlsh[w] = make_float2(m, l);
+    __syncthreads();
+
+    // ---- the four waves' partials -> the chunk's (m, l, o)
+    if (w == 0) {
+        float2 ml[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ml[i] = mlsh[i];
+        const float M = fmaxf(fmaxf(ml[0].x, ml[1].x), fmaxf(ml[2].x, ml[3].x));
+        float lsum = 0.f, r0 = 0.f, r1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float wgt = ml[i].x == -INFINITY ? 0.f : expf(ml[i].x - M);
+            const float2 o = osh[i][lane];
+            lsum = fmaf(wgt, ml[i].y, lsum);
+            r0 = fmaf(wgt, o.x, r0);
+            r1 = fmaf(wgt, o.y, r1);
+        }
+        if (a.direct) {
+            const f16_t he = (f16_t)(r0 / lsum), ho = (f16_t)(r1 / lsum);
+            ((uint32_t *)(a.out + (size_t)qh * D))[lane] =
+                (uint32_t)__builtin_bit_cast(uint16_t, he) | ((uint32_t)__builtin_bit_cast(uint16_t, ho) << 16);
+        } else {
+            const size_t slot = (size_t)qh * a.nchunks + c;
+            ((float2 *)(a.part_o + slot * D))[lane] = make_float2(r0, r1);
+            if (lane == 0) ((float2 *)a.part_ml)[slot] = make_float2(M, lsum);
+        }
+    }
+}
+
 // Fold the per-chunk partials of attn_fused_kernel: grid Hq, block 128.
 // The first MERGE_PRE chunks' (m, l) pairs and outputs are loaded in one
 // round together with seq_len -- (m, l) by one lane per chunk and shared
@@ -1953,7 +2156,7 @@ int nnz_attn_fused1_launch(nnz_ctx *ctx, const void *q, const void *kr, const vo
     const dim3 grid(a.parts == 1 ? a.units : ceil_div(a.units, 8u) * 8u * a.parts);
 #define FUSED(DD, GG) attn_fused_kernel<DD, GG><<<grid, 256, 0, ctx->stream>>>(a)
     if (gb == 1) {
-        if (head_dim == 128) FUSED(128, 1);
+        if (head_dim == 128) attn_fused_wave_kernel<<<grid, 256, 0, ctx->stream>>>(a);
         else FUSED(64, 1);
     } else if (head_dim == 128) {
         if (G == 2) FUSED(128, 2);

@@ -199,7 +199,17 @@ def test_attention_partials_merged_o_projection(dev, pos, freq_table, hq, hkv):
     ops.dispatch_qmv_f16io_resadd(dev, dwo, att, res2)
     dev.sync()
     assert np.array_equal(host(kc1), host(kc2)) and np.array_equal(host(vc1), host(vc2))
-    assert_close(host(res1), host(res2), rtol=1e-4, what=f"merged vs unmerged pos={pos}")
+    # The two O projections sum the same f32 products in different orders,
+    # and the merge divides by the softmax sum as a reciprocal product, so an
+    # f16 input where num * (1 / den) and num / den straddle a rounding edge
+    # moves by one ulp.  Per row |res1 - res2| stays within 64 float32 ulps of
+    # the sum of |terms| plus one ulp of the residual: two summation orders
+    # emulated in float32 reach 0.04 of that, one flipped input ~0.06.
+    r1, r2 = host(res1), host(res2)
+    terms = np.abs(O.dequant(wo)) @ np.abs(host(att))
+    bound = 64 * 2.0 ** -24 * terms + 2.0 ** -23 * np.abs(r2)
+    worst = float(np.max(np.abs(r1 - r2) / bound))
+    assert worst <= 1.0, f"merged vs unmerged pos={pos}: {worst:.2f} x the rounding bound"
     ref_att = O.f16(O.gqa_fused_step(q.astype(np.float64), kr.astype(np.float64),
                                      vr.astype(np.float64), kc.astype(np.float64),
                                      vc.astype(np.float64), qn, kn, pos, theta, v_transposed=True))

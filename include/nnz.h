@@ -405,8 +405,10 @@ int nnz_dispatch_gqa_attention_fused_1pass(nnz_ctx *ctx, const void *q, void *k_
  * followed by :1686 dispatchQMVf16io_resadd on the attention output):
  *   nnz_dispatch_gqa_attention_partials: the same norm/RoPE/append and
  *     attention, leaving per-chunk partials instead of the output --
- *     part_o f32 [Hq][nchunks][D] (unnormalised P.V), part_ml f32
- *     [Hq][nchunks][2] (max score, exp-sum), nchunks =
+ *     part_o f32 [nchunks][Hq*D] (unnormalised P.V; within a chunk, column
+ *     k = head * D + d sits at ((k >> 2) & 7) * (Hq*D / 8) + (k >> 5) * 4 +
+ *     (k & 3), the layout the merge reads with one 16-byte load per lane),
+ *     part_ml f32 [nchunks][Hq][2] (max score, exp-sum), nchunks =
  *     nnz_gqa_partial_chunks(dims.seq_len) (64-token chunks);
  *     rope_inv_freq: f32 [D/2] frequencies theta^(-2p/D) or NULL (computed
  *     in the kernel);

@@ -44,8 +44,10 @@ enum { EPI_STORE = 0, EPI_RESADD = 1, EPI_SILU = 2 };
 enum { XIN_X = 0, XIN_NORM = 1, XIN_MERGE = 2 };
 
 // Attention partials read by XIN_MERGE (written by the fused decode
-// attention): part_o [Hq][nchunks][D], part_ml [Hq][nchunks][2]; the live
-// chunk count is ceil(seq / chunk), seq = d_seq ? *d_seq : seq_len.
+// attention in its unit-major layout): part_o per chunk c the K = Hq * D
+// values, column k at c K + ((k >> 2) & 7) K / 8 + (k >> 5) 4 + (k & 3)
+// (nibble-major over the 32-column units); part_ml [nchunks][Hq][2]; the
+// live chunk count is ceil(seq / chunk), seq = d_seq ? *d_seq : seq_len.
 constexpr int MERGE_MAX_CHUNKS = 16;
 struct MergeIn {
     const float *part_o, *part_ml;
@@ -604,21 +606,23 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
         // The block merges the attention partials into x once -- the merge
         // that would otherwise be a launch of its own -- and builds the
         // nibble tables from it (LUT), or stages it f16 in LDS for every wave.
-        // Phase 1: per (head, chunk) the weight exp(m_c - M) and per head the
-        // denominator, one thread per pair (a head's 16 chunk slots are one
-        // DPP row).  Phase 2: 8 consecutive outputs per thread per 2048
-        // columns (coalesced partial loads); with tables, the thread writes
-        // the entries of its two nibbles (unit e0 / 32; the main loop's reads
-        // stay one lane per unit).  All partials of the first
-        // MERGE_MAX_CHUNKS chunks are loaded up front, independently of the
-        // live length.
-        static_assert(MERGE_MAX_CHUNKS == 16, "one DPP row per head");
-        __shared__ __align__(16) f16_t xs[2048 * NV];
-        __shared__ __align__(16) float mw[(2048 * NV / 64) * MERGE_MAX_CHUNKS];   // >= heads x 16 (D >= 64)
-        __shared__ float mden[2048 * NV / 64];
+        // Thread (lane l, wave w) merges columns 8 w .. 8 w + 7 (nibbles 2 w,
+        // 2 w + 1) of units u = l + 64 j, so the table entries it writes sit
+        // in its own lane's bank column (no bank conflicts), exactly as the
+        // lane that reads them in the row loop.  The partials come in the
+        // attention's unit-major layout (chunk c, nibble n, unit u: 4 floats
+        // at c K + n K / 8 + 4 u), one 16-byte load per (chunk, nibble): a
+        // wave's load is 1 KB contiguous.  Each lane derives its head's
+        // softmax weights from the head's (m, l) pairs itself, so no block
+        // exchange precedes the merge; one barrier follows the tables.
+        // All partials of the allocated chunks (<= MERGE_MAX_CHUNKS) are
+        // loaded up front, independently of the live length.
+        constexpr int NJ = FULL ? NV : 1;   // units per lane (K < 2048: one, lanes >= units idle)
+        __shared__ __align__(16) f16_t xs[LUT ? 8 : 2048 * NV];
         const MergeIn &mg = a.mg;
         const uint32_t D = mg.head_dim;
-        const uint32_t heads = K / D;
+        const int wid = threadIdx.x >> 6;
+        const uint32_t kq = K / 8;          // floats per nibble row of a chunk
         // The device sequence length as a vector load issued ahead of the
         // partials' loads, without a branch: a null d_seq gets an empty range,
         // so the load returns 0 without touching memory and seq_len is used.
@@ -628,32 +632,34 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
             __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t *>(mg.d_seq), (short)0,
                                               mg.d_seq ? 4 : 0, 0x00020000),
             0, 0, 0);
-
-        // (m, l) of this thread's (head, chunk) pairs p = tid + 256 i, then
-        // the partial outputs, then the weights
-        constexpr int PI = 2 * NV;   // heads x 16 <= 512 NV pairs
-        float2 mlv[PI];
+        bool mv[NJ];
+        uint32_t mu[NJ];
 #pragma unroll
-        for (int i = 0; i < PI; ++i) {
-            const uint32_t p = threadIdx.x + 256u * i;
-            const uint32_t hd = p / MERGE_MAX_CHUNKS, c = p % MERGE_MAX_CHUNKS;
-            const bool ok = hd < heads && c < mg.nchunks;
-            mlv[i] = *(const float2 *)(mg.part_ml + (ok ? ((size_t)hd * mg.nchunks + c) * 2 : 0));
+        for (int j = 0; j < NJ; ++j) {
+            const uint32_t u = (uint32_t)lane + 64u * j;
+            mv[j] = u < units;
+            mu[j] = mv[j] ? u : 0u;
         }
-        float4 oa[NV][MERGE_MAX_CHUNKS], ob[NV][MERGE_MAX_CHUNKS];
+        // (m, l) of the unit's head for every allocated chunk, then the
+        // partial outputs, then the weights
+        float2 mlv[NJ][MERGE_MAX_CHUNKS];
+        float4 oa[NJ][MERGE_MAX_CHUNKS], ob[NJ][MERGE_MAX_CHUNKS];
+        const uint32_t heads = K / D;
 #pragma unroll
-        for (int kk = 0; kk < NV; ++kk) {
-            const uint32_t e0 = (threadIdx.x + 256u * kk) * 8u;
-            const uint32_t ec = e0 < K ? e0 : 0u;
-            const size_t base = (size_t)(ec / D) * mg.nchunks;
-            const uint32_t d0 = ec % D;
+        for (int j = 0; j < NJ; ++j) {
+            const float2 *ml = (const float2 *)mg.part_ml + (mu[j] * 32u) / D;
+#pragma unroll
+            for (int c = 0; c < MERGE_MAX_CHUNKS; ++c)
+                if ((uint32_t)c < mg.nchunks) mlv[j][c] = ml[(size_t)c * heads];
+        }
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const float *po = mg.part_o + (size_t)(2 * wid) * kq + mu[j] * 4u;
 #pragma unroll
             for (int c = 0; c < MERGE_MAX_CHUNKS; ++c) {
                 if ((uint32_t)c < mg.nchunks) {   // launch bound: uniform
-                    oa[kk][c] = *(const float4 *)(mg.part_o + (base + c) * D + d0);
-                    ob[kk][c] = *(const float4 *)(mg.part_o + (base + c) * D + d0 + 4);
-                } else {
-                    oa[kk][c] = ob[kk][c] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    oa[j][c] = *(const float4 *)(po + (size_t)c * K);
+                    ob[j][c] = *(const float4 *)(po + (size_t)c * K + kq);
                 }
             }
         }
@@ -665,90 +671,64 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
         const uint32_t seq = mg.d_seq ? __builtin_amdgcn_readfirstlane(seq_v) : mg.seq_len;
         const uint32_t nch = min(mg.nchunks, ceil_div(seq, mg.chunk));
 #pragma unroll
-        for (int i = 0; i < PI; ++i) {
-            const uint32_t p = threadIdx.x + 256u * i;
-            if (p >= ((heads * MERGE_MAX_CHUNKS + 255) / 256) * 256) break;   // uniform
-            const uint32_t hd = p / MERGE_MAX_CHUNKS, c = p % MERGE_MAX_CHUNKS;
-            const bool on = hd < heads && c < nch;
-            const float2 ml = on ? mlv[i] : make_float2(-INFINITY, 0.f);
-            float M = ml.x;   // max over the head's 16 lanes
-            M = fmaxf(M, dpp_move<DPP_XOR1>(M, -INFINITY));
-            M = fmaxf(M, dpp_move<DPP_XOR2>(M, -INFINITY));
-            M = fmaxf(M, dpp_move<DPP_ROW_HALF_MIRROR>(M, -INFINITY));
-            M = fmaxf(M, dpp_move<DPP_ROW_MIRROR>(M, -INFINITY));
-            const float wgt = on ? expf(ml.x - M) : 0.f;
-            float den = wgt * ml.y;
-            den += dpp_move<DPP_XOR1>(den, 0.f);
-            den += dpp_move<DPP_XOR2>(den, 0.f);
-            den += dpp_move<DPP_ROW_HALF_MIRROR>(den, 0.f);
-            den += dpp_move<DPP_ROW_MIRROR>(den, 0.f);
-            if (hd < heads) {
-                mw[p] = wgt;
-                if (c == 0) mden[hd] = den;
-            }
-        }
-        __syncthreads();
+        for (int j = 0; j < NJ; ++j) {
+            float M = -INFINITY;
 #pragma unroll
-        for (int kk = 0; kk < NV; ++kk) {
-            const uint32_t e0 = (threadIdx.x + 256u * kk) * 8u;
-            if (e0 < K) {
-                const uint32_t hd = e0 / D;
-                // the head's 16 chunk weights in 4 LDS reads, before any use
-                float wv[MERGE_MAX_CHUNKS];
+            for (int c = 0; c < MERGE_MAX_CHUNKS; ++c)
+                if ((uint32_t)c < nch) M = fmaxf(M, mlv[j][c].x);
+            // the chunk weights exp(m_c - M) <= 1, all computed before any
+            // is used (independent, no branch between them) as 2^((m_c - M)
+            // log2 e) on the hardware exponential: 3 instructions each
+            // instead of the ~19 of a full-range expf (relative difference
+            // <= |m_c - M| 2^-24 plus one ulp)
+            float wv[MERGE_MAX_CHUNKS];
 #pragma unroll
-                for (int q = 0; q < MERGE_MAX_CHUNKS / 4; ++q) {
-                    const float4 w4 = *(const float4 *)&mw[hd * MERGE_MAX_CHUNKS + 4 * q];
-                    wv[4 * q] = w4.x; wv[4 * q + 1] = w4.y; wv[4 * q + 2] = w4.z; wv[4 * q + 3] = w4.w;
-                }
-                const float den = mden[hd];
-                float num[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            for (int c = 0; c < MERGE_MAX_CHUNKS; ++c)
+                wv[c] = (uint32_t)c < nch ? __builtin_amdgcn_exp2f((mlv[j][c].x - M) * 1.44269504088896341f)
+                                          : 0.f;
+            float den = 0.f;
+            float num[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int c = 0; c < MERGE_MAX_CHUNKS; ++c) {
-                    if ((uint32_t)c < mg.nchunks) {
-                        const float wgt = wv[c];
-                        num[0] = fmaf(wgt, oa[kk][c].x, num[0]); num[1] = fmaf(wgt, oa[kk][c].y, num[1]);
-                        num[2] = fmaf(wgt, oa[kk][c].z, num[2]); num[3] = fmaf(wgt, oa[kk][c].w, num[3]);
-                        num[4] = fmaf(wgt, ob[kk][c].x, num[4]); num[5] = fmaf(wgt, ob[kk][c].y, num[5]);
-                        num[6] = fmaf(wgt, ob[kk][c].z, num[6]); num[7] = fmaf(wgt, ob[kk][c].w, num[7]);
-                    }
-                }
-                // one division, then products (the f16 result differs from
-                // num / den only where the two straddle an f16 rounding edge)
-                const float rden = 1.f / den;
-                if constexpr (LUT) {
-                    float x8[8];
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) x8[e] = (float)(f16_t)(num[e] * rden);
-                    const uint32_t u = e0 >> 5, n0 = (e0 & 31) >> 2;   // unit, first nibble
-                    float *const dst = lut + ((u >> 6) * 8 + n0) * 16 * 64 + (u & 63);
-#pragma unroll
-                    for (int sb = 0; sb < 2; ++sb) {
-                        const float *x4 = x8 + 4 * sb;
-                        const float p1 = x4[0] - x4[1], p3 = x4[0] + x4[1];
-                        const float q1 = x4[2] - x4[3], q3 = x4[2] + x4[3];
-                        const float pp[4] = {-p3, p1, -p1, p3};
-                        const float qq[4] = {-q3, q1, -q1, q3};
-#pragma unroll
-                        for (int e = 0; e < 16; ++e) dst[(sb * 16 + e) * 64] = pp[e & 3] + qq[e >> 2];
-                    }
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) xs[e0 + e] = (f16_t)(num[e] * rden);
+            for (int c = 0; c < MERGE_MAX_CHUNKS; ++c) {
+                if ((uint32_t)c < nch) {
+                    const float wgt = wv[c];
+                    den = fmaf(wgt, mlv[j][c].y, den);
+                    num[0] = fmaf(wgt, oa[j][c].x, num[0]); num[1] = fmaf(wgt, oa[j][c].y, num[1]);
+                    num[2] = fmaf(wgt, oa[j][c].z, num[2]); num[3] = fmaf(wgt, oa[j][c].w, num[3]);
+                    num[4] = fmaf(wgt, ob[j][c].x, num[4]); num[5] = fmaf(wgt, ob[j][c].y, num[5]);
+                    num[6] = fmaf(wgt, ob[j][c].z, num[6]); num[7] = fmaf(wgt, ob[j][c].w, num[7]);
                 }
             }
-        }
-        if constexpr (LUT) {
-            // units past the row end (K < 2048 NV) read all-zero tables:
-            // thread (lane, wave) clears nibbles 2 wave, 2 wave + 1 of its lane's
-            const int wid = threadIdx.x >> 6;
+            // one division, then products (the f16 result differs from
+            // num / den only where the two straddle an f16 rounding edge);
+            // a unit past the row end merges to zeros (its tables then read 0)
+            const float rden = mv[j] ? 1.f / den : 0.f;
+            float x8[8];
 #pragma unroll
-            for (int j = 0; j < NV; ++j) {
-                if (!uvalid[j]) {
+            for (int e = 0; e < 8; ++e) x8[e] = (float)(f16_t)(num[e] * rden);
+            if constexpr (LUT) {
+                float *const dst = lut + (j * 8 + 2 * wid) * 16 * 64 + lane;
 #pragma unroll
-                    for (int sb = 0; sb < 2; ++sb)
+                for (int sb = 0; sb < 2; ++sb) {
+                    const float *x4 = x8 + 4 * sb;
+                    const float p1 = x4[0] - x4[1], p3 = x4[0] + x4[1];
+                    const float q1 = x4[2] - x4[3], q3 = x4[2] + x4[3];
+                    const float pp[4] = {-p3, p1, -p1, p3};
+                    const float qq[4] = {-q3, q1, -q1, q3};
 #pragma unroll
-                        for (int e = 0; e < 16; ++e) lut[((j * 8 + 2 * wid + sb) * 16 + e) * 64 + lane] = 0.f;
+                    for (int e = 0; e < 16; ++e) dst[(sb * 16 + e) * 64] = pp[e & 3] + qq[e >> 2];
                 }
+            } else if (mv[j]) {
+                uint4 h;
+                h.x = (uint32_t)__builtin_bit_cast(uint16_t, (f16_t)x8[0]) |
+                      ((uint32_t)__builtin_bit_cast(uint16_t, (f16_t)x8[1]) << 16);
+                h.y = (uint32_t)__builtin_bit_cast(uint16_t, (f16_t)x8[2]) |
+                      ((uint32_t)__builtin_bit_cast(uint16_t, (f16_t)x8[3]) << 16);
+                h.z = (uint32_t)__builtin_bit_cast(uint16_t, (f16_t)x8[4]) |
+                      ((uint32_t)__builtin_bit_cast(uint16_t, (f16_t)x8[5]) << 16);
+                h.w = (uint32_t)__builtin_bit_cast(uint16_t, (f16_t)x8[6]) |
+                      ((uint32_t)__builtin_bit_cast(uint16_t, (f16_t)x8[7]) << 16);
+                *(uint4 *)(xs + mu[j] * 32u + 8u * (uint32_t)wid) = h;
             }
         }
         __syncthreads();
@@ -825,7 +805,9 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
     // ---- software-pipelined row loop ---------------------------------------
     // Two register sets used alternately (the loop body appears twice), so
     // the next step's weights land in the set not being read and nothing is
-    // copied at the back edge.
+    // copied at the back edge.  (A third set for the 8-row steps of the LM
+    // head, one more step of loads in flight per wave, measured slower:
+    // 13.2 -> 15.0 us.)
     const uint32_t stride = nwaves * rows_per_iter;
     // nibble-table addresses: byte 0 = lane * 4, byte 1 = the nibble (the
     // table of one (unit, nibble) pair is 16 entries x 64 lanes x 4 bytes)
@@ -1420,6 +1402,8 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
     if (stk) blocks = stack_blocks(stk, blocks);
     // measured: tables pay off from 4 row-units per wave (fused Q/K/V, 4
     // rows per wave: 3.55 us without, 3.16 us with)
+    // (the merge keeps its tables at any row count: built from the merged
+    // values, they measured 0.2-0.5 us faster than the f16 staging)
     if (lut && ceil_div(d.M, blocks * 4u) * NMAT < 4u && !MERGE) lut = false;
 
     QmvArgs a{};

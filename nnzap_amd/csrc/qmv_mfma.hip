@@ -137,10 +137,15 @@ void qmv1_mfma_kernel(MqArgs a) {
 
     // Lane-private fp4 tables: entry b (byte value) at [b][lane].
     __shared__ __align__(16) uint32_t tab[256 * 64];
-    // digit rows: row s, columns 8 w .. 8 w + 7 in dword xs4[s * PREP + w]
+    // digit rows: row s, columns 8 w .. 8 w + 7 in dword xs4[s * XP + w]
     // (nibble j = column 8 w + j); scales sc8[s * KG + G] (E8M0).
     // (rows NDIG..15 are zero, so every lane loads its A row unconditionally)
-    __shared__ __align__(16) uint32_t xs4[16 * PREP];
+    // The row pitch XP = PREP + 4 dwords puts row n's A reads 4 n banks
+    // apart: the 16 lane rows of a 16-byte read cover the 64 banks once (a
+    // pitch of PREP, a multiple of 64 banks, made that read 16-way
+    // conflicted).
+    constexpr int XP = PREP + 4;
+    __shared__ __align__(16) uint32_t xs4[16 * XP];
     __shared__ __align__(16) uint8_t sc8[16 * KG];
     __shared__ float red[16];
     // per-wave staging of one tile's codes: 16 rows at a 272-byte pitch
@@ -284,12 +289,12 @@ void qmv1_mfma_kernel(MqArgs a) {
             q = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(q, d[2], d[3], 1.f, 1);
             q = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(q, d[4], d[5], 1.f, 2);
             q = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(q, d[6], d[7], 1.f, 3);
-            xs4[s * PREP + tid] = q;
+            xs4[s * XP + tid] = q;
             if ((tid & 15) == 0) sc8[s * KG + G] = (uint8_t)(127 + e);
         }
 #pragma unroll
         for (int s = NDIG; s < 16; ++s) {
-            xs4[s * PREP + tid] = 0u;
+            xs4[s * XP + tid] = 0u;
             if ((tid & 15) == 0) sc8[s * KG + G] = 127;   // 1.0: finite, the row is zero
         }
     }
@@ -299,7 +304,7 @@ void qmv1_mfma_kernel(MqArgs a) {
     v4i A[KG];
     uint32_t sa[KG / 4];
 #pragma unroll
-    for (int G = 0; G < KG; ++G) A[G] = __builtin_bit_cast(v4i, *(const u32x4 *)&xs4[n * PREP + G * 16 + 4 * q]);
+    for (int G = 0; G < KG; ++G) A[G] = __builtin_bit_cast(v4i, *(const u32x4 *)&xs4[n * XP + G * 16 + 4 * q]);
     {
         const u32x4 sv = *(const u32x4 *)&sc8[n * KG];
         sa[0] = sv.x; sa[1] = sv.y; sa[2] = sv.z; sa[3] = sv.w;

@@ -646,16 +646,37 @@ struct FusedAttnArgs {
     const float *qn, *kn;           // per-head norm scales [D]
     f16_t *kc, *vc;                 // caches
     f16_t *out;                     // [Hq*D]
-    float *part_o, *part_ml;        // [Hq][nchunks][D], [Hq][nchunks][2]
+    float *part_o, *part_ml;        // see part_o_at, part_ml_at
     const uint32_t *d_seq;          // device seq_len (= position + 1) or null
     const float *inv_freq;          // [D/2] RoPE frequencies, or null (computed here)
     uint32_t seq_len, max_ctx, nchunks;
+    uint32_t unit_major;            // part_o layout: 0 head-major, 1 unit-major
+    uint32_t kdim;                  // Hq * D
     uint32_t gfull;                 // query heads per KV head
     uint32_t units;                 // nchunks * Hkv (chunk, KV head) pairs
     uint32_t parts;                 // blocks per unit (query-head groups of G)
     int direct;                     // one chunk and no consumer merge: write out
     float eps, theta, scale;
 };
+
+// Offset of partial output (query head qh, chunk c, dim d) in part_o.
+// Head-major (attn_merge_kernel): [Hq][nchunks][D].  Unit-major (the O
+// projection's merge prologue, qmv.hip): chunk by chunk, column k = qh D + d
+// of the K = Hq D columns at ((k >> 2) & 7) K / 8 + (k >> 5) 4 + (k & 3) --
+// nibble n of every 32-column unit together, so a lane per unit reads one
+// nibble's 4 values with one 16-byte load and a wave's load is contiguous.
+// The (max, sum) pair of (qh, c) sits at float2 index part_ml_at: head-major
+// [Hq][nchunks], or chunk-major [nchunks][Hq] beside the unit-major part_o
+// (a chunk's pairs of all heads are then one contiguous read).
+__device__ __forceinline__ size_t part_o_at(const FusedAttnArgs &a, uint32_t qh, uint32_t c, uint32_t d,
+                                            uint32_t D) {
+    if (!a.unit_major) return ((size_t)qh * a.nchunks + c) * D + d;
+    const uint32_t k = qh * D + d;
+    return (size_t)c * a.kdim + ((k >> 2) & 7u) * (a.kdim >> 3) + (k >> 5) * 4u + (k & 3u);
+}
+__device__ __forceinline__ size_t part_ml_at(const FusedAttnArgs &a, uint32_t qh, uint32_t c, uint32_t D) {
+    return a.unit_major ? (size_t)c * (a.kdim / D) + qh : (size_t)qh * a.nchunks + c;
+}
 
 template <int D, int G>
 __global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
@@ -898,8 +919,8 @@ __global__ __launch_bounds__(256) void attn_fused_kernel(FusedAttnArgs a) {
         if (a.direct) {
             a.out[(size_t)(qb + g) * D + d] = (f16_t)(s / lval[g]);
         } else {
-            const size_t slot = (size_t)(qb + g) * a.nchunks + c;
-            a.part_o[slot * D + d] = s;
+            const size_t slot = part_ml_at(a, qb + g, c, D);
+            a.part_o[part_o_at(a, qb + g, c, d, D)] = s;
             if (d == 0) {
                 a.part_ml[slot * 2] = mval[g];
                 a.part_ml[slot * 2 + 1] = lval[g];
@@ -1104,8 +1125,9 @@ __global__ __launch_bounds__(256) void attn_fused_wave_kernel(FusedAttnArgs a) {
             ((uint32_t *)(a.out + (size_t)qh * D))[lane] =
                 (uint32_t)__builtin_bit_cast(uint16_t, he) | ((uint32_t)__builtin_bit_cast(uint16_t, ho) << 16);
         } else {
-            const size_t slot = (size_t)qh * a.nchunks + c;
-            ((float2 *)(a.part_o + slot * D))[lane] = make_float2(r0, r1);
+            // dims 2l, 2l + 1: adjacent in either layout (8-byte aligned)
+            const size_t slot = part_ml_at(a, qh, c, D);
+            *(float2 *)(a.part_o + part_o_at(a, qh, c, 2u * lane, D)) = make_float2(r0, r1);
             if (lane == 0) ((float2 *)a.part_ml)[slot] = make_float2(M, lsum);
         }
     }
@@ -2144,6 +2166,9 @@ int nnz_attn_fused1_launch(nnz_ctx *ctx, const void *q, const void *kr, const vo
     a.max_ctx = max_ctx;
     a.nchunks = ceil_div(max_seq, (uint32_t)FCHUNK);
     a.direct = a.nchunks == 1 && !partials_only;
+    // partials for the O projection's merge: its unit-major layout
+    a.unit_major = partials_only ? 1u : 0u;
+    a.kdim = hq * head_dim;
     a.eps = eps;
     a.theta = theta;
     a.scale = 1.0f / sqrtf((float)head_dim);

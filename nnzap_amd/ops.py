@@ -480,8 +480,8 @@ def dispatch_gqa_attention_partials(dev, q, k_cache, v_cache, k_raw, v_raw, q_no
                                     part_o, part_ml, dims: L.GQAFusedDims, d_seq_len=None,
                                     rope_inv_freq=None):
     """The decode step's attention half: transformer.zig:3244-3370 up to the
-    per-chunk partials (part_o [Hq][n][D], part_ml [Hq][n][2], n =
-    gqa_partial_chunks(seq_len))."""
+    per-chunk partials (part_o [n][Hq*D] in the merge's unit-major column
+    order, part_ml [n][Hq][2], n = gqa_partial_chunks(seq_len))."""
     dev.call("nnz_dispatch_gqa_attention_partials", _v(q), _v(k_cache), _v(v_cache), _v(k_raw),
              _v(v_raw), _v(q_norm), _v(k_norm), _v(rope_inv_freq), _v(part_o), _v(part_ml),
              _v(d_seq_len), dims)

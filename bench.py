@@ -33,6 +33,7 @@ python bench.py [--gpus 1] [--steps K] [--warmup W] [--lm-head q1|tied] [--quick
 from __future__ import annotations
 
 import argparse
+import glob
 import json
 import os
 import sys
@@ -687,22 +688,40 @@ def bench_kernels(dev, quick=False, only=None):
     return res
 
 
+def sources_digest():
+    """sha256 (first 16 hex digits) of the HIP sources the library is built
+    from (nnzap_amd/csrc/*.hip, *.h and include/nnz.h, sorted by name): the
+    profiles under profiles/ record the digest of the sources they measured."""
+    import hashlib
+    h = hashlib.sha256()
+    files = sorted(glob.glob(os.path.join(ROOT, "nnzap_amd", "csrc", "*.hip")) +
+                   glob.glob(os.path.join(ROOT, "nnzap_amd", "csrc", "*.h")) +
+                   [os.path.join(ROOT, "include", "nnz.h")], key=os.path.basename)
+    for f in files:
+        h.update(os.path.basename(f).encode())
+        h.update(open(f, "rb").read())
+    return h.hexdigest()[:16]
+
+
 def load_trace_us():
-    """Mean per-dispatch device duration (us) of every kernel case from the
-    committed rocprofv3 kernel-trace summary (profiles/kernel_case_traces.md,
-    first table: the case's kernels summed)."""
+    """Mean per-dispatch device duration (us) and kernel name(s) of every
+    kernel case from the committed rocprofv3 kernel-trace summary
+    (profiles/kernel_case_traces.md, first table: the case's kernels summed),
+    and the sources digest that summary records ("Sources: <digest>")."""
     path = os.path.join(ROOT, "profiles", "kernel_case_traces.md")
-    out = {}
+    out, digest = {}, None
     if not os.path.exists(path):
-        return out
+        return out, digest
     for line in open(path):
+        if line.startswith("Sources:"):
+            digest = line.split()[1].strip("`")
         f = [x.strip() for x in line.strip().strip("|").split("|")]
         if len(f) >= 10 and f[0] and f[0] not in out:
             try:
-                out[f[0]] = float(f[3])
+                out[f[0]] = (float(f[3]), f[1].strip("`"))
             except ValueError:
                 pass
-    return out
+    return out, digest
 
 
 def load_traffic():
@@ -923,12 +942,17 @@ def main():
                     "timing": "live: launches back to back in one hipGraph, HIP events on the "
                               "library stream / launches",
                     "traffic_source": "profiles/pmc_traffic.md" if traffic else None}
-        tr = load_trace_us().get(dom)
+        traces, digest = load_trace_us()
+        tr = traces.get(dom)
         if tr:   # the committed rocprofv3 per-dispatch mean of the same case
-            roofline.update({"trace_us": tr,
-                             "achieved_trace": round(d["bytes"] / (tr * 1e-6) / 1e9, 1),
-                             "frac_trace": round(d["bytes"] / (tr * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
-                             "trace_source": "profiles/kernel_case_traces.md"})
+            us_tr, kname = tr
+            roofline.update({"trace_us": us_tr,
+                             "achieved_trace": round(d["bytes"] / (us_tr * 1e-6) / 1e9, 1),
+                             "frac_trace": round(d["bytes"] / (us_tr * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                             "trace_kernel": kname,
+                             "trace_source": "profiles/kernel_case_traces.md (committed "
+                                             "rocprofv3 summary, not re-measured by this run)",
+                             "trace_matches_sources": digest == sources_digest()})
     cpu = None if args.skip_cpu else cpu_baseline()
     cpu_cfg = None if args.skip_cpu else cpu_configs(full=args.cpu_full)
 

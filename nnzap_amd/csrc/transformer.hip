@@ -542,87 +542,6 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
     }
 }
 
-// Combine the per-chunk partials of one query head (grid = (Hq, Z), 256
-// threads) in one round of loads: every thread issues its (m, l) pair (one
-// chunk per thread) and, as one of 256/(D/4) groups of D/4 lanes, the o
-// rows of up to PRE chunks of its strided subset with 16-byte loads,
-// before any of them is used; longer sequences loop over the rest.  The
-// chunk maxima and weighted exp-sums are folded block-wide, the o sums in
-// LDS.  Indices past the live chunk count are clamped to a written chunk
-// and masked by selection (never multiplied), so stale partials cannot
-// leak in.  part_o rows are 16-byte aligned (checked by the launcher); the
-// launcher picks PRE to cover the chunk count (launch_combine).
-template <int D, int PRE>
-__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
-    constexpr int NV = D / 4, PARTS = 256 / NV;
-    __shared__ float red[4];
-    __shared__ float4 acc[256];
-    const uint32_t qh = blockIdx.x, z = blockIdx.y, tid = threadIdx.x;
-    const uint32_t dv = tid % NV, p = tid / NV;
-    const size_t base = ((size_t)z * a.hq + qh) * a.nchunks;
-    const float2 *ml = (const float2 *)(a.part_ml + base * 2);
-    const float4 *po = (const float4 *)(a.part_o + base * D) + dv;
-    const uint32_t last = a.nchunks - 1;
-    const float2 mine = ml[min(tid, last)];
-    float2 mlk[PRE];
-    float4 ok[PRE];
-#pragma unroll
-    for (int k = 0; k < PRE; ++k) {
-        const uint32_t c = min(p + (uint32_t)(PARTS * k), last);
-        mlk[k] = ml[c];
-        ok[k] = po[(size_t)c * NV];
-    }
-    const uint32_t seq = (a.d_seq ? *a.d_seq : a.seq_len) + z;
-    const uint32_t nch = min(a.nchunks, ceil_div(seq, a.chunk));
-
-    float m = tid < nch ? mine.x : -INFINITY;
-    for (uint32_t c = tid + 256; c < nch; c += 256) m = fmaxf(m, ml[c].x);
-    const float M = block_max_256(m, red);
-    float den = tid < nch ? expf(mine.x - M) * mine.y : 0.f;
-    for (uint32_t c = tid + 256; c < nch; c += 256) {
-        const float2 v = ml[c];
-        den = fmaf(expf(v.x - M), v.y, den);
-    }
-    den = block_sum_256(den, red);
-
-    float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int k = 0; k < PRE; ++k) {
-        const bool live = p + (uint32_t)(PARTS * k) < nch;
-        const float w = expf(mlk[k].x - M);
-        s.x = live ? fmaf(w, ok[k].x, s.x) : s.x;
-        s.y = live ? fmaf(w, ok[k].y, s.y) : s.y;
-        s.z = live ? fmaf(w, ok[k].z, s.z) : s.z;
-        s.w = live ? fmaf(w, ok[k].w, s.w) : s.w;
-    }
-#pragma unroll 4
-    for (uint32_t c = p + PARTS * PRE; c < nch; c += PARTS) {
-        const float w = expf(ml[c].x - M);
-        const float4 o = po[(size_t)c * NV];
-        s.x = fmaf(w, o.x, s.x);
-        s.y = fmaf(w, o.y, s.y);
-        s.z = fmaf(w, o.z, s.z);
-        s.w = fmaf(w, o.w, s.w);
-    }
-    acc[tid] = s;
-    __syncthreads();
-    if (tid < (uint32_t)NV) {
-#pragma unroll
-        for (int q = 1; q < PARTS; ++q) {
-            const float4 o = acc[q * NV + tid];
-            s.x += o.x;
-            s.y += o.y;
-            s.z += o.z;
-            s.w += o.w;
-        }
-        const size_t ob = (size_t)z * a.o_stride + (size_t)qh * D + 4 * tid;
-        store_dt(a.out, ob + 0, s.x / den, a.odt);
-        store_dt(a.out, ob + 1, s.y / den, a.odt);
-        store_dt(a.out, ob + 2, s.z / den, a.odt);
-        store_dt(a.out, ob + 3, s.w / den, a.odt);
-    }
-}
-
 // ------------------------------------------------- fused decode attention --
 // The attention half of a decode step for one layer:
 //   attn_fused_kernel, grid (chunks of FCHUNK tokens, Hkv), 256 threads:
@@ -1192,7 +1111,7 @@ __global__ __launch_bounds__(128) void attn_merge_kernel(const float *part_o, co
 //     register sets while the current one is used, and all loads of a
 //     sub-chunk are issued before the first of them is consumed;
 //   * scores with 256/FCHUNK lanes per token, P.V from registers;
-//   * one chunk: the output; several: partials for attn_combine_kernel.
+//   * one chunk: the output; several: partials for the combine (launch_combine).
 struct DecAttnArgs {
     const void *q;                  // [Hq][D] in qdt
     const uint16_t *kc, *vc;        // caches (f16 or bf16 bits)
@@ -1465,7 +1384,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(DecAttnArgs a) {
 //     V transposed: dims lane and lane + 64 over the group's 16 tokens);
 //   * the next group's loads are issued before the current one is used;
 //   * the 4 waves' (m, l, o) are merged once at the end: the output (one
-//     chunk) or the chunk's partials for attn_combine_kernel.
+//     chunk) or the chunk's partials for the combine (launch_combine).
 template <int G, int KVDT, bool VT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))   // <= 128 VGPRs: 4 blocks per CU
 void attn_stream_kernel(DecAttnArgs a) {
@@ -1845,20 +1764,6 @@ size_t nnz_attn_scratch_bytes_impl(uint32_t hq, uint32_t head_dim, uint32_t seq_
     return ((size_t)hq * nch * head_dim + (size_t)hq * nch * 2 + (size_t)hq * head_dim) * 4 + 256;
 }
 
-// The combine step for Hq x nq queries: the preload depth covers the chunks
-// each lane group folds (ceil(nchunks / (256 / (D/4)))), up to 16.
-template <int D>
-static void launch_combine_blocks(nnz_ctx *ctx, const AttnArgs &a, uint32_t nq) {
-    constexpr uint32_t PARTS = 256 / (D / 4);
-    const uint32_t per = ceil_div(a.nchunks, PARTS);
-    const dim3 grid(a.hq, nq);
-    if (per <= 1) attn_combine_kernel<D, 1><<<grid, 256, 0, ctx->stream>>>(a);
-    else if (per <= 2) attn_combine_kernel<D, 2><<<grid, 256, 0, ctx->stream>>>(a);
-    else if (per <= 4) attn_combine_kernel<D, 4><<<grid, 256, 0, ctx->stream>>>(a);
-    else if (per <= 8) attn_combine_kernel<D, 8><<<grid, 256, 0, ctx->stream>>>(a);
-    else attn_combine_kernel<D, 16><<<grid, 256, 0, ctx->stream>>>(a);
-}
-
 // Few chunks: one wave per (query head, query, 64 dims), lane = dim,
 // no barrier: every lane reads the chunks' (m, l) pairs (wave-uniform
 // addresses) and its dim of each partial, all issued before the first is
@@ -1902,14 +1807,65 @@ __global__ __launch_bounds__(64) void attn_combine_wave_kernel(AttnArgs a) {
     store_dt(a.out, (size_t)z * a.o_stride + (size_t)qh * D + d, num / den, a.odt);
 }
 
+// More chunks: one wave per (query head, query, 8 dims), lane = chunk (64
+// per pass), no barrier: a lane loads its chunk's (m, l) pair and the
+// slice's 8 partial values (two 16-byte loads), all issued before any is
+// used; the maximum is a wave reduction, and the exp-sum and the 8 weighted
+// sums are one exchange-halving reduction, whose 8 slots land in lanes 8 k
+// (slot multi_row_slot<8>) and are stored from there.  Over 64 chunks each
+// lane folds its chunks c, c + 64, ... after a first pass for the maximum.
+// Hq * D / 8 waves: 256 for 16 heads of 128.
+template <int D>
+__global__ __launch_bounds__(64) void attn_combine_slice_kernel(AttnArgs a) {
+    constexpr int SL = D / 8;   // slices per head
+    const uint32_t lane = threadIdx.x;
+    const uint32_t qh = blockIdx.x, z = blockIdx.y / SL, d0 = (blockIdx.y % SL) * 8;
+    const size_t base = ((size_t)z * a.hq + qh) * a.nchunks;
+    const float2 *ml = (const float2 *)(a.part_ml + base * 2);
+    const float4 *po = (const float4 *)(a.part_o + base * D + d0);
+    const uint32_t last = a.nchunks - 1;
+    const uint32_t c0 = min(lane, last);
+    const float2 m0 = ml[c0];
+    const float4 oa = po[(size_t)c0 * (D / 4)], ob = po[(size_t)c0 * (D / 4) + 1];
+    const uint32_t seq = (a.d_seq ? *a.d_seq : a.seq_len) + z;
+    const uint32_t nch = min(a.nchunks, ceil_div(seq, a.chunk));
+
+    float m = lane < nch ? m0.x : -INFINITY;
+    for (uint32_t c = lane + 64; c < nch; c += 64) m = fmaxf(m, ml[c].x);
+    const float M = wave_max(m);
+    // past the live count: weight 0 by selection (never NaN * 0)
+    const bool live = lane < nch;
+    const float w0 = expf(m0.x - M);
+    float v[9] = {live ? w0 * m0.y : 0.f,
+                  live ? w0 * oa.x : 0.f, live ? w0 * oa.y : 0.f,
+                  live ? w0 * oa.z : 0.f, live ? w0 * oa.w : 0.f,
+                  live ? w0 * ob.x : 0.f, live ? w0 * ob.y : 0.f,
+                  live ? w0 * ob.z : 0.f, live ? w0 * ob.w : 0.f};
+    for (uint32_t c = lane + 64; c < nch; c += 64) {
+        const float2 mc = ml[c];
+        const float4 xa = po[(size_t)c * (D / 4)], xb = po[(size_t)c * (D / 4) + 1];
+        const float w = expf(mc.x - M);
+        v[0] = fmaf(w, mc.y, v[0]);
+        v[1] = fmaf(w, xa.x, v[1]); v[2] = fmaf(w, xa.y, v[2]);
+        v[3] = fmaf(w, xa.z, v[3]); v[4] = fmaf(w, xa.w, v[4]);
+        v[5] = fmaf(w, xb.x, v[5]); v[6] = fmaf(w, xb.y, v[6]);
+        v[7] = fmaf(w, xb.z, v[7]); v[8] = fmaf(w, xb.w, v[8]);
+    }
+    const float den = wave_sum(v[0]);
+    const float num[8] = {v[1], v[2], v[3], v[4], v[5], v[6], v[7], v[8]};
+    const float t = multi_row_sum<8>(num);
+    if ((lane & 7) == 0)
+        store_dt(a.out, (size_t)z * a.o_stride + (size_t)qh * D + d0 + multi_row_slot<8>(), t / den, a.odt);
+}
+
 template <int D>
 static void launch_combine(nnz_ctx *ctx, const AttnArgs &a, uint32_t nq) {
     // measured at config 4: L = 512 (8 chunks) 7.49 -> 7.18 us with the
-    // one-wave form; 16 and 32 chunks are faster with the block form
+    // one-wave form; more chunks take a wave per 8-dim slice
     if (a.nchunks <= 8)
         attn_combine_wave_kernel<D><<<dim3(a.hq, nq * (D / 64)), 64, 0, ctx->stream>>>(a);
     else
-        launch_combine_blocks<D>(ctx, a, nq);
+        attn_combine_slice_kernel<D><<<dim3(a.hq, nq * (D / 8)), 64, 0, ctx->stream>>>(a);
 }
 
 template <int D, int G, int KVDT, bool VT>

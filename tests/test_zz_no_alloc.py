@@ -29,11 +29,11 @@ def _noalloc(dev, q, k, v, out, dims, rope_position, rope_theta):
     return rc
 
 
-def _case(dev, L_):
-    print(f"noalloc attention L={L_}", flush=True)
-    q, k, v = cf.config4(L_)
+def _case(dev, L_, hkv=8):
+    print(f"noalloc attention L={L_} hkv={hkv}", flush=True)
+    q, k, v = cf.config4(L_, hkv=hkv)
     qd, kd, vd = from_bits16(q, "bf16"), from_bits16(k, "bf16"), from_bits16(v, "bf16")
-    dims = L.GQADims(16, 8, 128, L_, L_, 2)
+    dims = L.GQADims(16, hkv, 128, L_, L_, 16 // hkv)
     ref_out = torch.empty(16, 128, dtype=torch.float32, device="cuda")
     scratch = torch.empty((ops.gqa_scratch_bytes(dims) + 3) // 4, dtype=torch.float32, device="cuda")
     ops.dispatch_gqa_attention(dev, qd, kd, vd, ref_out, scratch, dims, v_transposed=False,
@@ -50,8 +50,39 @@ def _case(dev, L_):
 
 
 def test_noalloc_attention_matches_workspace_variant(dev):
-    _case(dev, 32768)   # fills most of the fixed partials buffer
+    _case(dev, 32768)   # the config-4 shape at its longest (the streaming plan)
     _case(dev, 4096)    # then a smaller call over the previous contents
+
+
+def _largest_accepted(hq, hkv, d):
+    """The longest seq_len whose partials fit the fixed buffer (the need
+    grows by one chunk row every 64 tokens)."""
+    seq = 64
+    while ops.gqa_scratch_bytes(L.GQADims(hq, hkv, d, seq + 64, seq + 64, hq // hkv)) \
+            <= L.GQA_NOALLOC_MAX_BYTES:
+        seq += 64
+    return seq
+
+
+def test_noalloc_attention_fills_the_buffer(dev):
+    """16 query heads over 2 KV heads (groups of 8) take the 64-token chunk
+    plan: at the longest accepted length its partials end within one chunk
+    row of the buffer's end.  That call matches the workspace entry point and
+    the oracle; a smaller call follows over its contents; one more token is
+    refused."""
+    hq, hkv, d = 16, 2, 128
+    seq = _largest_accepted(hq, hkv, d)
+    need = ops.gqa_scratch_bytes(L.GQADims(hq, hkv, d, seq, seq, hq // hkv))
+    assert L.GQA_NOALLOC_MAX_BYTES - need < hq * (d + 2) * 4
+    _case(dev, seq, hkv=hkv)
+    _case(dev, 1000, hkv=hkv)
+    over = seq + 1
+    dims = L.GQADims(hq, hkv, d, over, over, hq // hkv)
+    assert ops.gqa_scratch_bytes(dims) > L.GQA_NOALLOC_MAX_BYTES
+    qz = torch.zeros(hq, d, dtype=torch.float32, device="cuda")
+    kz = torch.zeros(hkv, over, d, dtype=torch.bfloat16, device="cuda")
+    out = torch.zeros(hq, d, dtype=torch.float32, device="cuda")
+    assert _noalloc(dev, qz, kz, kz, out, dims, -1, 0.0) == L.EUNSUPPORTED
 
 
 def test_noalloc_attention_rejects_oversize(dev):

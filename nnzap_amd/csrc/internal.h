@@ -3,6 +3,26 @@
 
 #include "common.h"
 
+// Greedy token choice (transformer.zig:3694-3707: first maximum wins, NaN
+// never wins): the best value, its index and the runner-up value of a set
+// of logits.  Partials of disjoint index ranges merge in any order.
+struct NnzTop2 {
+    float best, second;
+    uint32_t idx;
+};
+// Capacity of a model's top-2 partials (one per block of the pass that
+// writes them; unwritten entries stay neutral).
+constexpr uint32_t NNZ_TOP2_MAX = 2048;
+
+__device__ __forceinline__ NnzTop2 nnz_top2_merge(NnzTop2 a, NnzTop2 b) {
+    const bool take_b = (b.best > a.best) || (b.best == a.best && b.idx < a.idx);
+    NnzTop2 r;
+    r.best = take_b ? b.best : a.best;
+    r.idx = take_b ? b.idx : a.idx;
+    r.second = fmaxf(fmaxf(a.second, b.second), take_b ? a.best : b.best);
+    return r;
+}
+
 // One attention launch with full control over chunking and batching.
 struct NnzAttnCall {
     const void *q = nullptr;
@@ -62,8 +82,11 @@ int nnz_qmv_merge_resadd_launch(nnz_ctx *ctx, const nnz_qweight *w, const float 
                                 const float *part_ml, const uint32_t *d_seq, uint32_t seq_len,
                                 uint32_t nchunks, uint32_t chunk, uint32_t head_dim,
                                 float *residual, nnz_qmv_dims d);
+// top2: when set, every block also writes the greedy top-2 partial of the
+// rows it stored to top2[block] (at most NNZ_TOP2_MAX blocks).
 int nnz_qmv_norm_f32out_launch(nnz_ctx *ctx, const nnz_qweight *w, const float *residual,
-                               const float *norm_w, float *out, nnz_qmv_dims d, float eps);
+                               const float *norm_w, float *out, nnz_qmv_dims d, float eps,
+                               NnzTop2 *top2 = nullptr);
 int nnz_gemm_launch(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, const void *a,
                     uint32_t P, void *out, int mode, const nnz_qmv_dims &d);
 

@@ -213,31 +213,22 @@ __global__ __launch_bounds__(256) void lm_head_bf16_kernel(const uint16_t *__res
     }
 }
 
-// Greedy sampling, two passes (argmax: first maximum wins, NaN never wins,
-// transformer.zig:3694-3707).  Pass 1: ARGMAX_BLOCKS blocks reduce strided
-// slices to (best, runner-up, index) partials.  Pass 2: one block merges
-// them, records the token and its top-2 margin, and advances the state.
+// Greedy sampling (argmax: first maximum wins, NaN never wins,
+// transformer.zig:3694-3707) from top-2 partials (best, index, runner-up).
+// The 1-bit and 4-bit LM heads write one partial per block themselves (the
+// qmv kernel's top-2 epilogue), so a decode step needs only the final pass;
+// other logits (the tied bf16 head, the prefill) take the first pass below,
+// ARGMAX_BLOCKS blocks over strided slices.  The final pass, one block,
+// merges n partials, records the token and its top-2 margin, and advances
+// the state.
 constexpr int ARGMAX_BLOCKS = 256;
-
-struct Top2 {
-    float best, second;
-    uint32_t idx;
-};
-
-__device__ __forceinline__ Top2 top2_merge(Top2 a, Top2 b) {
-    const bool take_b = (b.best > a.best) || (b.best == a.best && b.idx < a.idx);
-    Top2 r;
-    r.best = take_b ? b.best : a.best;
-    r.idx = take_b ? b.idx : a.idx;
-    r.second = fmaxf(fmaxf(a.second, b.second), take_b ? a.best : b.best);
-    return r;
-}
+typedef NnzTop2 Top2;
 
 __device__ __forceinline__ Top2 block_top2_256(Top2 t, Top2 *sh) {
     sh[threadIdx.x] = t;
     __syncthreads();
     for (uint32_t s = 128; s > 0; s >>= 1) {
-        if (threadIdx.x < s) sh[threadIdx.x] = top2_merge(sh[threadIdx.x], sh[threadIdx.x + s]);
+        if (threadIdx.x < s) sh[threadIdx.x] = nnz_top2_merge(sh[threadIdx.x], sh[threadIdx.x + s]);
         __syncthreads();
     }
     return sh[0];
@@ -255,10 +246,11 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float *x, uin
     if (threadIdx.x == 0) part[blockIdx.x] = r;
 }
 
-__global__ __launch_bounds__(256) void argmax_final_advance_kernel(const Top2 *part, NnzPick pick) {
+__global__ __launch_bounds__(256) void argmax_final_advance_kernel(const Top2 *part, uint32_t n,
+                                                                   NnzPick pick) {
     __shared__ Top2 sh[256];
     Top2 t{-INFINITY, -INFINITY, 0xFFFFFFFFu};
-    for (uint32_t i = threadIdx.x; i < (uint32_t)ARGMAX_BLOCKS; i += 256) t = top2_merge(t, part[i]);
+    for (uint32_t i = threadIdx.x; i < n; i += 256) t = nnz_top2_merge(t, part[i]);
     const Top2 r = block_top2_256(t, sh);
     if (threadIdx.x == 0) nnz_pick_advance(pick, r.idx == 0xFFFFFFFFu ? 0u : r.idx, r.best - r.second);
 }
@@ -291,7 +283,7 @@ struct nnz_model {
     float *part_o = nullptr, *part_ml = nullptr;
     uint32_t part_chunks = 0;  // capacity in chunks per query head
     float *rope_inv = nullptr;     // [head_dim/2] RoPE frequencies
-    Top2 *top2 = nullptr;          // [ARGMAX_BLOCKS] argmax partials
+    Top2 *top2 = nullptr;          // [NNZ_TOP2_MAX + ARGMAX_BLOCKS] argmax partials
     uint32_t *state = nullptr;
     uint32_t *tokens_out = nullptr;
     float *margins_out = nullptr;
@@ -418,7 +410,7 @@ int lm_head(nnz_model *m, const f16_t *x, float *logits) {
 // per layer 5 launches (norm+QKV, fused attention, O +=, norm+gate/up+SiLU,
 // down +=), then norm+LM head.  `max_seq` sizes the attention grid for every
 // position this step may be replayed at.
-int enqueue_decode_step(nnz_model *m, uint32_t max_seq) {
+int enqueue_decode_step(nnz_model *m, uint32_t max_seq, bool top2 = false) {
     nnz_ctx *ctx = m->ctx;
     const nnz_model_config &c = m->c;
     const uint32_t H = c.hidden_size;
@@ -474,7 +466,7 @@ int enqueue_decode_step(nnz_model *m, uint32_t max_seq) {
     // 1-bit LM head; the tied bf16 head keeps a separate norm)
     if (c.lm_head_kind == NNZ_LMHEAD_Q1 || c.lm_head_kind == NNZ_LMHEAD_Q4)
         return nnz_qmv_norm_f32out_launch(ctx, &m->lm.w, m->residual, m->final_norm, m->logits,
-                                          dims_of(m, m->lm), c.rms_eps);
+                                          dims_of(m, m->lm), c.rms_eps, top2 ? m->top2 : nullptr);
     RC(nnz_dispatch_rms_norm(ctx, m->residual, m->final_norm, m->xn, NNZ_F16, 0,
                              {H, 1, c.rms_eps}));
     return lm_head(m, m->xn, m->logits);
@@ -491,19 +483,36 @@ NnzPick pick_of(const nnz_model *m) {
     return p;
 }
 
-// Pick the next token from the logits into the state block: argmax (two
-// passes) or the sampler (sampleToken, transformer.zig:3860-3894).
-int enqueue_argmax_advance(nnz_model *m) {
+// Pick the next token from the logits into the state block: argmax or the
+// sampler (sampleToken, transformer.zig:3860-3894).  `partials`: the LM head
+// has written its per-block top-2 partials (NNZ_TOP2_MAX entries, the ones
+// past its block count neutral), so only the final pass runs.
+int enqueue_argmax_advance(nnz_model *m, bool partials = false) {
     const NnzPick pick = pick_of(m);
     if (m->sp.temperature != 0.f)
         return nnz_sample_launch(m->ctx, m->logits, m->c.vocab_size, m->sp, m->rng, m->sample_ws,
                                  nullptr, nullptr, &pick);
-    argmax_partial_kernel<<<ARGMAX_BLOCKS, 256, 0, m->ctx->stream>>>(m->logits, m->c.vocab_size,
-                                                                     m->top2);
-    NNZ_LAUNCHED(m->ctx);
-    argmax_final_advance_kernel<<<1, 256, 0, m->ctx->stream>>>(m->top2, pick);
+    Top2 *part = m->top2;
+    uint32_t n = NNZ_TOP2_MAX;
+    if (!partials) {
+        // the first pass writes its own slots, apart from the LM head's
+        part = m->top2 + NNZ_TOP2_MAX;
+        n = ARGMAX_BLOCKS;
+        argmax_partial_kernel<<<ARGMAX_BLOCKS, 256, 0, m->ctx->stream>>>(m->logits, m->c.vocab_size,
+                                                                         part);
+        NNZ_LAUNCHED(m->ctx);
+    }
+    argmax_final_advance_kernel<<<1, 256, 0, m->ctx->stream>>>(part, n, pick);
     NNZ_LAUNCHED(m->ctx);
     return NNZ_OK;
+}
+
+// Whether the decode step's LM head writes the greedy top-2 partials (the
+// 1-bit and 4-bit heads with whole-wave rows, hidden >= 2048; greedy
+// decoding).
+bool lm_head_top2(const nnz_model *m) {
+    return m->sp.temperature == 0.f && m->c.hidden_size >= 2048 &&
+           (m->c.lm_head_kind == NNZ_LMHEAD_Q1 || m->c.lm_head_kind == NNZ_LMHEAD_Q4);
 }
 
 void decode_plan(const nnz_model *m, uint32_t max_seq, uint32_t *chunk, uint32_t *nch) {
@@ -639,7 +648,14 @@ int nnz_model_create(nnz_ctx *ctx, const nnz_model_config *cfg, nnz_model **out)
         MALLOC(parts, (size_t)c.num_query_heads * m->part_chunks * (c.head_dim + 2) * 4);
         m->part_o = parts;
         m->part_ml = parts + (size_t)c.num_query_heads * m->part_chunks * c.head_dim;
-        MALLOC(m->top2, (size_t)ARGMAX_BLOCKS * sizeof(Top2));
+        // the LM head's partials (neutral past its block count: they are
+        // never written), then the first argmax pass's ARGMAX_BLOCKS
+        MALLOC(m->top2, ((size_t)NNZ_TOP2_MAX + ARGMAX_BLOCKS) * sizeof(Top2));
+        {
+            std::vector<Top2> neutral(NNZ_TOP2_MAX + ARGMAX_BLOCKS, Top2{-INFINITY, -INFINITY, 0xFFFFFFFFu});
+            NNZ_HIP(ctx, hipMemcpy(m->top2, neutral.data(), neutral.size() * sizeof(Top2),
+                                   hipMemcpyHostToDevice));
+        }
         MALLOC(m->state, 64);
         MALLOC(m->rng, 32);
         MALLOC(m->sample_ws, nnz_sample_ws_bytes(c.vocab_size));
@@ -879,8 +895,9 @@ int begin_decode(nnz_model *m, const uint32_t *prompt, uint32_t n_prompt, uint32
 // One decode step: forwardDecode of the state's token, then the token pick
 // and state advance.  Graph-capturable (no host data, no allocation).
 int pick_step(nnz_model *m, uint32_t max_seq) {
-    RC(enqueue_decode_step(m, max_seq));
-    return enqueue_argmax_advance(m);
+    const bool t2 = lm_head_top2(m);
+    RC(enqueue_decode_step(m, max_seq, t2));
+    return enqueue_argmax_advance(m, t2);
 }
 
 int capture_step(nnz_model *m, uint32_t max_seq, nnz_graph **g) {

@@ -84,6 +84,7 @@ struct QmvArgs {
     const void *x;         // input vector (XDT) or f32 residual (XIN_NORM)
     const float *norm_w;   // f32 [K], XIN_NORM only
     MergeIn mg;            // XIN_MERGE only
+    NnzTop2 *top2;         // f32 single-matrix stores: per-block greedy top-2, or null
     uint32_t M, K, gs;
     uint32_t lpr_log2;     // lanes per row = 1 << lpr_log2
     uint32_t sdt;          // scale/bias dtype (NNZ_F16 / NNZ_BF16)
@@ -370,6 +371,9 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
     constexpr bool NORM = XIN == XIN_NORM;
     constexpr bool MERGE = XIN == XIN_MERGE;
     constexpr int VEC = (BITS == 1) ? 1 : 4;  // u32 words per 32-column unit
+    // greedy top-2 of the stored rows (the LM head's argmax, first pass)
+    constexpr bool TOP2 = EPI == EPI_STORE && NMAT == 1 && ODT == NNZ_F32 && FULL && !STK;
+    NnzTop2 t2{-INFINITY, -INFINITY, 0xFFFFFFFFu};
     const int lane = threadIdx.x & 63;
     const int lpr_log2 = FULL ? 6 : (int)a.lpr_log2;
     const int LPR = 1 << lpr_log2;
@@ -913,6 +917,14 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
             const bool head = (lane & ((64 / V) - 1)) == 0 && (NMAT == 1 || lane < 32);
             if (head && row >= base)
                 qmv_epilogue<EPI, ODT, FAITH, NMAT, STK>(a, out0, row, row - seg_start, tot, c.res[0]);
+            if constexpr (TOP2) {
+                // the stored value; a lane's rows ascend, so a tie keeps the first
+                const float v = FAITH ? bf16_trunc(tot[0]) : tot[0];
+                if (a.top2 && head && row >= base) {
+                    if (v > t2.best) { t2.second = t2.best; t2.best = v; t2.idx = row; }
+                    else if (v > t2.second) t2.second = v;
+                }
+            }
         } else {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
@@ -932,6 +944,25 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
         if (base >= a.M) break;
         row_step(nxt, cur);
         base += stride;
+    }
+    if constexpr (TOP2) {
+        // the block's greedy top-2 (merged across the wave, then the waves)
+        if (a.top2) {
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+                NnzTop2 o;
+                o.best = __shfl_xor(t2.best, off, 64);
+                o.second = __shfl_xor(t2.second, off, 64);
+                o.idx = (uint32_t)__shfl_xor((int)t2.idx, off, 64);
+                t2 = nnz_top2_merge(t2, o);
+            }
+            __shared__ NnzTop2 t2sh[4];
+            if (lane == 0) t2sh[threadIdx.x >> 6] = t2;
+            __syncthreads();
+            if (threadIdx.x == 0)
+                a.top2[blockIdx.x] = nnz_top2_merge(nnz_top2_merge(t2sh[0], t2sh[1]),
+                                                    nnz_top2_merge(t2sh[2], t2sh[3]));
+        }
     }
 }
 
@@ -1211,7 +1242,7 @@ template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH>
 int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg_rows, int nw,
                   const void *x, const float *norm_w, void *const *out, nnz_qmv_dims d,
                   const char *name, const MergeIn *merge = nullptr, float eps = 1e-6f,
-                  const nnz_qmv_stack *stk = nullptr) {
+                  const nnz_qmv_stack *stk = nullptr, NnzTop2 *top2 = nullptr) {
     constexpr bool NORM = XIN == XIN_NORM;
     constexpr bool MERGE = XIN == XIN_MERGE;
     constexpr bool STACKABLE = stackable<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH>();
@@ -1266,8 +1297,10 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
 
     // 1-bit rows of K = 2048, group size 128: the block-scaled MFMA kernel
     // (qmv_mfma.hip) where the context's policy picks it.
+    NNZ_REQUIRE(ctx, !top2 || (EPI == EPI_STORE && NMAT == 1 && ODT == NNZ_F32 && nw == 1 && !stk),
+                NNZ_EUNSUPPORTED, "%s: top-2 partials need one f32-output matrix", name);
     if constexpr (BITS == 1 && !FAITH && !MERGE) {
-        if (q1_matrix_cores_wanted(ctx, d, stk != nullptr) && (NMAT == 2 || nw == 1)) {
+        if (!top2 && q1_matrix_cores_wanted(ctx, d, stk != nullptr) && (NMAT == 2 || nw == 1)) {
             NnzQ1Mfma c;
             for (int i = 0; i < NMAT; ++i) {
                 c.codes[i] = w[i]->codes;
@@ -1423,6 +1456,12 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
     a.x = x;
     a.norm_w = norm_w;
     if (MERGE) a.mg = *merge;
+    if (top2) {
+        // whole-wave rows only (the partial is built from the row heads)
+        NNZ_REQUIRE(ctx, lpr == 64 && blocks <= NNZ_TOP2_MAX, NNZ_EUNSUPPORTED,
+                    "%s: top-2 partials need K >= 2048 and at most %u blocks", name, NNZ_TOP2_MAX);
+        a.top2 = top2;
+    }
     a.M = d.M;
     a.K = d.K;
     a.gs = d.group_size;
@@ -1441,13 +1480,13 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
 template <int BITS, int XDT, int NMAT, int XIN, int EPI, int ODT, bool FAITH>
 int launch_qmv(nnz_ctx *ctx, const nnz_qweight *wa, const nnz_qweight *wb, const void *x,
                const float *norm_w, void *out0, void *out1, nnz_qmv_dims d, const char *name,
-               float eps = 1e-6f) {
+               float eps = 1e-6f, NnzTop2 *top2 = nullptr) {
     const nnz_qweight *w[2] = {wa, wb};
     void *out[2] = {out0, out1};
     const uint32_t rows[1] = {d.M};
     if (NMAT == 2) NNZ_REQUIRE(ctx, wb != nullptr, NNZ_EINVAL, "%s: null second weight", name);
     return launch_qmv_ex<BITS, XDT, NMAT, XIN, EPI, ODT, FAITH>(ctx, w, rows, NMAT, x, norm_w, out, d,
-                                                                  name, nullptr, eps);
+                                                                  name, nullptr, eps, nullptr, top2);
 }
 
 }  // namespace
@@ -1501,14 +1540,15 @@ int nnz_qmv_norm_pair_silu_launch(nnz_ctx *ctx, const nnz_qweight *wg, const nnz
 // reference's final norm + qmv_spec_f16in / q4mv_spec_f16in pair
 // (transformer.zig:2730-2785) in one launch.
 int nnz_qmv_norm_f32out_launch(nnz_ctx *ctx, const nnz_qweight *w, const float *residual,
-                               const float *norm_w, float *out, nnz_qmv_dims d, float eps) {
+                               const float *norm_w, float *out, nnz_qmv_dims d, float eps,
+                               NnzTop2 *top2) {
     NNZ_REQUIRE(ctx, w != nullptr, NNZ_EINVAL, "norm_lm_head: null weight");
     if (w->bits == 4)
         return launch_qmv<4, NNZ_F32, 1, true, EPI_STORE, NNZ_F32, true>(
-            ctx, w, nullptr, residual, norm_w, out, nullptr, d, "q4_norm_lm_head", eps);
+            ctx, w, nullptr, residual, norm_w, out, nullptr, d, "q4_norm_lm_head", eps, top2);
     return launch_qmv<1, NNZ_F32, 1, true, EPI_STORE, NNZ_F32, false>(ctx, w, nullptr, residual,
                                                                        norm_w, out, nullptr, d,
-                                                                       "norm_lm_head", eps);
+                                                                       "norm_lm_head", eps, top2);
 }
 
 // O-projection with residual += whose input is merged from split-sequence

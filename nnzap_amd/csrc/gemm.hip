@@ -459,8 +459,9 @@ __global__ __launch_bounds__(128 * KQ) void dq4_gemm_kernel(const f16_t *A, cons
                 for (int i = 0; i < 4; ++i) {
                     float4v t = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[0][i], b0, (float4v){0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                     t = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[1][i], b1, t, 0, 0, 0);
+                    // two multiply-adds per element: + b (row sum), then + s (A . n)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) acc[m][i][j][r] += fmaf(sc, t[r], bi * xs[i][r]);
+                    for (int r = 0; r < 4; ++r) acc[m][i][j][r] = fmaf(sc, t[r], fmaf(bi, xs[i][r], acc[m][i][j][r]));
                 }
             }
     };

@@ -640,7 +640,6 @@ def _kernel_cases():
         "q1_big_valu": cores(q1_big, 2),
         "stacked_q1_6144x2048_bpm4": stacked("q1_6144x2048", 0, 4),
         "stacked_config3_bpm4": stacked("config3", 0, 4),
-        "stacked_config1_bpm32": stacked("config1", 0, 32),
         "stacked_q1_6144x2048_valu": cores(stacked("q1_6144x2048"), 2),
         "dec_lm_head_norm_valu": cores(dec_lm_head, 2),
         "dec_lm_head_norm_mfma": cores(dec_lm_head, 1),

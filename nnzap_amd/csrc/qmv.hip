@@ -1397,6 +1397,10 @@ int launch_qmv_ex(nnz_ctx *ctx, const nnz_qweight *const *w, const uint32_t *seg
     // lane holds in flight (two steps are live).
     const uint32_t min_blocks = NMAT == 2 || BITS == 4 ? 512u : 256u;
     while (R > 1 && (ceil_div(d.M, 4u * R * rpw) < min_blocks || NMAT * R * (int)nv * vec > 32)) R >>= 1;
+    // a stacked launch has blocks enough: four rows per step, twice the
+    // bytes in flight per wave (stacked 4-bit config-1 matrices: 0.68-0.70 ->
+    // 0.71-0.73 of 8 TB/s; eight rows: 0.67-0.71)
+    if (stk && NMAT * 4 * (int)nv * vec <= 32) R = 4;
     // 1-bit full-wave rows may use the nibble tables.  Building them is a
     // fixed cost per block that pays off from about four matrix rows per
     // wave: pairs take two rows per wave.

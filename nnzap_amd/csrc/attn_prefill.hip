@@ -27,8 +27,11 @@
 // Precision: the queries are kept unrounded (float32, as the reference
 // keeps q), so each MFMA operand that is not already f16 is split into an
 // f16 high part and an f16 remainder -- q and the probabilities p -- and
-// both products are accumulated: the scores and P.V carry ~2^-22 relative
-// error, the same as float32 arithmetic on these f16 keys and values.
+// both products are accumulated: the scores carry ~2^-22 and P.V ~2^-20
+// relative error, float32-level arithmetic on these f16 keys and values.
+// The prep kernel writes q pre-scaled by log2(e)/sqrt(D) and already split
+// (hi = f16(x), lo = f16(x - hi)), so the scores come out in log2 units and
+// the softmax runs in base 2 (v_exp_f32) with the same probabilities.
 #include "internal.h"
 
 namespace {
@@ -43,18 +46,12 @@ constexpr int KT = 64;  // keys per LDS tile
 constexpr int S_G2 = 4;
 
 struct PrefillArgs {
-    const float *q;      // [n][hq][D] f32
+    const f16_t *q;      // [n][hq][2][D]: hi and lo f16 rows of q log2(e)/sqrt(D)
     const f16_t *kc;     // [hkv][max_ctx][D]
     const f16_t *vc;     // [hkv][D][max_ctx]
     f16_t *out;          // [n][hq][D]
     uint32_t start, n, hq, max_ctx;
-    float scale;
 };
-
-__device__ __forceinline__ void split_f16(float v, _Float16 &hi, _Float16 &lo) {
-    hi = (_Float16)v;
-    lo = (_Float16)(v - (float)hi);
-}
 
 // S key splits: the block holds S x G waves; wave (ws, w) walks the key
 // tiles ws, ws + S, ... of query head w and the S partial softmax states
@@ -86,22 +83,50 @@ __global__ __launch_bounds__(64 * G * S) void attn_prefill_kernel(PrefillArgs a)
     const uint32_t qlast = (q0 + 15u < a.n ? q0 + 15u : a.n - 1u) + a.start;
     const uint32_t ntiles = qlast / KT + 1u, nsteps = (ntiles + S - 1) / S;
 
-    // Q^T fragments: lane (g, c) holds dims 32 ks + 8 g .. +8 of query c
+    // Q^T fragments: lane (g, c) holds dims 32 ks + 8 g .. +8 of query c,
+    // the f16 hi and lo parts the prep kernel wrote (zero past the batch).
+    // With key splits the S waves of a head share one copy: the block loads
+    // its 16 queries x G heads once into LDS (row pitch 2D + 8 halves: the
+    // 16 rows of a fragment read hit distinct banks; the buffer is the tile
+    // area, free until the first tile is stored) and each wave reads its
+    // fragments from there.
     half8 qh[NKS], ql[NKS];
-    {
-        const float *qp = a.q + ((size_t)(qvalid ? qi : 0u) * a.hq + h) * D;
+    const half8 zero = {};
+    if constexpr (S > 1) {
+        constexpr int QP = 2 * D + 8, QROW = G * 2 * D / 8, QPT = 16 * QROW / NT;   // pieces
+        static_assert(16 * QROW % NT == 0, "Q staging layout");
+        static_assert(16 * G * QP * 2 <= SMEM, "Q fits the tile area");
+        _Float16 *Qs = (_Float16 *)smem;
+        uint4 qr[QPT];
+#pragma unroll
+        for (int i = 0; i < QPT; ++i) {
+            const uint32_t p = (uint32_t)(tid + i * NT), qc = p / QROW, e = p % QROW;
+            const uint32_t qq = q0 + qc < a.n ? q0 + qc : 0u;
+            const uint4 v = *(const uint4 *)(a.q + ((size_t)qq * a.hq + hkv * G) * (2 * D) + e * 8);
+            qr[i] = q0 + qc < a.n ? v : make_uint4(0u, 0u, 0u, 0u);
+        }
+#pragma unroll
+        for (int i = 0; i < QPT; ++i) {
+            const uint32_t p = (uint32_t)(tid + i * NT), qc = p / QROW, e = p % QROW;
+            const uint32_t hw = e / (2 * D / 8), col = e % (2 * D / 8);
+            *(uint4 *)(Qs + (hw * 16 + qc) * QP + col * 8) = qr[i];
+        }
+        __syncthreads();
+        const _Float16 *qrow = Qs + (w * 16 + c) * QP;
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) {
-            const float4 v0 = *(const float4 *)(qp + 32 * ks + 8 * g);
-            const float4 v1 = *(const float4 *)(qp + 32 * ks + 8 * g + 4);
-            const float v[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            qh[ks] = *(const half8 *)(qrow + 32 * ks + 8 * g);
+            ql[ks] = *(const half8 *)(qrow + D + 32 * ks + 8 * g);
+        }
+        __syncthreads();   // before the tiles overwrite Qs
+    } else {
+        const f16_t *qp = a.q + ((size_t)(qvalid ? qi : 0u) * a.hq + h) * (2 * D);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                _Float16 hi, lo;
-                split_f16(qvalid ? v[e] : 0.f, hi, lo);
-                qh[ks][e] = hi;
-                ql[ks][e] = lo;
-            }
+        for (int ks = 0; ks < NKS; ++ks) {
+            const half8 hv = *(const half8 *)(qp + 32 * ks + 8 * g);
+            const half8 lv = *(const half8 *)(qp + D + 32 * ks + 8 * g);
+            qh[ks] = qvalid ? hv : zero;
+            ql[ks] = qvalid ? lv : zero;
         }
     }
     float4v o[NDT];
@@ -112,29 +137,53 @@ __global__ __launch_bounds__(64 * G * S) void attn_prefill_kernel(PrefillArgs a)
     const f16_t *kbase = a.kc + (size_t)hkv * a.max_ctx * D;
     const f16_t *vbase = a.vc + (size_t)hkv * D * a.max_ctx;
     // Tiles are staged through registers, one ahead: the next tile's loads
-    // are in flight while the current one is computed.  The loads are never
-    // branched around: addresses are clamped into the cache and keys past
-    // the sequence are zeroed by selects (8-key V pieces never cross
-    // max_ctx: max_ctx % 8 == 0).
-    // A step stages S consecutive tiles, tile j of the step in LDS slot j.
+    // are in flight while the current one is computed.  A step stages S
+    // consecutive tiles, tile j of the step in LDS slot j.  A step inside
+    // the batch (the common case) loads without checks; one that crosses
+    // its end clamps the addresses into the cache and zeroes the keys past
+    // it by selects (8-key V pieces never cross max_ctx: max_ctx % 8 == 0).
+    // Lane offsets: staging piece i of lane tid is K row krow + i NT/(D/8)
+    // of the step, dims kcol..+8, and V^T row vrow + (i NT mod D KT/8)/(KT/8)
+    // of tile (i NT)/(D KT/8), keys vcol..+8.
     constexpr int KPT = S * KT * D / 8 / NT, VPT = S * D * KT / 8 / NT;
+    constexpr int RPI = NT / (D / 8);   // K rows per staging piece index
+    static_assert(NT % (D / 8) == 0 && (D * KT / 8) % NT == 0, "staging layout");
+    static_assert(KT % RPI == 0 || RPI % KT == 0, "a K piece lies in one tile");
+    const uint32_t krow = (uint32_t)tid / (D / 8), kcol = ((uint32_t)tid % (D / 8)) * 8u;
+    const uint32_t vrow = (uint32_t)tid / (KT / 8), vcol = ((uint32_t)tid % (KT / 8)) * 8u;
+    const uint32_t voff = vrow * a.max_ctx + vcol;
     uint4 kr[KPT], vr[VPT];
     auto load_tile = [&](uint32_t k0) __attribute__((always_inline)) {
+        if (k0 + (uint32_t)(S * KT) <= seq_end) {   // block-uniform
+            // pieces of tiles no query of the block reaches stay unloaded
+            // (their LDS slots are never read)
+#pragma unroll
+            for (int i = 0; i < KPT; ++i)
+                if (k0 + (uint32_t)((i * RPI) / KT * KT) <= qlast)
+                    kr[i] = *(const uint4 *)(kbase + (k0 + (uint32_t)(i * RPI) + krow) * D + kcol);
+#pragma unroll
+            for (int i = 0; i < VPT; ++i) {
+                constexpr uint32_t TS = D * KT / 8;
+                const uint32_t j = (uint32_t)(i * NT) / TS, dr = ((uint32_t)(i * NT) % TS) / (KT / 8);
+                if (k0 + j * KT <= qlast)
+                    vr[i] = *(const uint4 *)(vbase + voff + dr * a.max_ctx + k0 + j * KT);
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
-            const int p = tid + i * NT;
-            const uint32_t key = k0 + (uint32_t)(p / (D / 8));   // p / (D/8) spans the S tiles
+            const uint32_t key = k0 + (uint32_t)(i * RPI) + krow;
             const uint32_t kc = key < seq_end ? key : 0u;
-            const uint4 v = *(const uint4 *)(kbase + (size_t)kc * D + (p % (D / 8)) * 8);
+            const uint4 v = *(const uint4 *)(kbase + kc * D + kcol);
             kr[i] = key < seq_end ? v : make_uint4(0u, 0u, 0u, 0u);
         }
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
-            const int p = tid + i * NT;
-            const int j = p / (D * KT / 8), pp = p % (D * KT / 8);   // tile j of the step
-            const uint32_t key = k0 + (uint32_t)(j * KT) + (uint32_t)(pp % (KT / 8)) * 8u;
+            constexpr uint32_t TS = D * KT / 8;
+            const uint32_t j = (uint32_t)(i * NT) / TS, dr = ((uint32_t)(i * NT) % TS) / (KT / 8);
+            const uint32_t key = k0 + j * KT + vcol;
             const uint32_t kc = key < seq_end ? key : 0u;
-            uint4 v = *(const uint4 *)(vbase + (size_t)(pp / (KT / 8)) * a.max_ctx + kc);
+            uint4 v = *(const uint4 *)(vbase + (vrow + dr) * a.max_ctx + kc);
             // halves e with key + e >= seq_end become 0
             const int keep = key >= seq_end ? 0 : (int)(seq_end - key < 8u ? seq_end - key : 8u);
             const uint32_t m[4] = {keep >= 2 ? ~0u : (keep >= 1 ? 0xFFFFu : 0u),
@@ -165,7 +214,7 @@ __global__ __launch_bounds__(64 * G * S) void attn_prefill_kernel(PrefillArgs a)
     for (uint32_t step = 0; step < nsteps; ++step) {
         store_tile();
         __syncthreads();
-        load_tile((step + 1 < nsteps ? step + 1 : step) * (S * KT));
+        if (step + 1 < nsteps) load_tile((step + 1) * (S * KT));
         const uint32_t t = step * S + (uint32_t)ws;   // this wave's tile
         if (t < ntiles) {   // wave-uniform
         const uint32_t k0 = t * KT;
@@ -183,49 +232,66 @@ __global__ __launch_bounds__(64 * G * S) void attn_prefill_kernel(PrefillArgs a)
                 s[st] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[ks], s[st], 0, 0, 0);
             }
         }
-        // scale, causal mask, online softmax of query c
-        float mx = -INFINITY;
+        // causal mask (tiles that end before the block's first query need
+        // none; keys past the batch end are masked there too), online
+        // softmax of query c in log2 units: p = 2^(s - m)
+        if (k0 + (uint32_t)(KT - 1) > a.start + q0) {   // wave-uniform
+#pragma unroll
+            for (int st = 0; st < KT / 16; ++st)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const uint32_t key = k0 + (uint32_t)(st * 16 + 4 * g + r);
+                    s[st][r] = key <= qpos ? s[st][r] : -INFINITY;
+                }
+        }
+        float mx = s[0][0];
 #pragma unroll
         for (int st = 0; st < KT / 16; ++st)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t key = k0 + (uint32_t)(st * 16 + 4 * g + r);
-                const float v = (qvalid && key <= qpos) ? s[st][r] * a.scale : -INFINITY;
-                s[st][r] = v;
-                mx = fmaxf(mx, v);
-            }
+            for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[st][r]);
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         const float m_new = fmaxf(m_run, mx);
-        const float alpha = m_new == -INFINITY ? 1.f : expf(m_run - m_new);
+        // a query with every key so far masked keeps p = 0 (2^-inf)
+        const float m_use = m_new == -INFINITY ? 0.f : m_new;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
         float ls = 0.f;
 #pragma unroll
         for (int st = 0; st < KT / 16; ++st)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float p = s[st][r] == -INFINITY ? 0.f : expf(s[st][r] - m_new);
+                const float p = __builtin_amdgcn_exp2f(s[st][r] - m_use);
                 s[st][r] = p;
                 ls += p;
             }
         ls += __shfl_xor(ls, 16);
         ls += __shfl_xor(ls, 32);
-        l_run = l_run * alpha + ls;
         m_run = m_new;
+        if (step == 0) {   // wave-uniform: nothing accumulated yet
+            l_run = ls;
+        } else {
+            l_run = l_run * alpha + ls;
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
+            for (int dt = 0; dt < NDT; ++dt) o[dt] *= alpha;
+        }
 
-        // P^T as B operands: slot 8g + 4 sb + r = key 16 (2 kk + sb) + 4 g + r
+        // P^T as B operands: slot 8g + 4 sb + r = key 16 (2 kk + sb) + 4 g + r,
+        // p = hi + lo with both halves rounded toward zero (|p - hi - lo| <
+        // 2^-20 p)
         half8 ph[KT / 32], pl[KT / 32];
 #pragma unroll
         for (int kk = 0; kk < KT / 32; ++kk)
 #pragma unroll
             for (int sb = 0; sb < 2; ++sb)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    _Float16 hi, lo;
-                    split_f16(s[2 * kk + sb][r], hi, lo);
-                    ph[kk][4 * sb + r] = hi;
-                    pl[kk][4 * sb + r] = lo;
+                for (int r = 0; r < 4; r += 2) {
+                    const float p0 = s[2 * kk + sb][r], p1 = s[2 * kk + sb][r + 1];
+                    const auto hi = __builtin_amdgcn_cvt_pkrtz(p0, p1);
+                    const auto lo = __builtin_amdgcn_cvt_pkrtz(p0 - (float)hi[0], p1 - (float)hi[1]);
+                    ph[kk][4 * sb + r] = hi[0];
+                    ph[kk][4 * sb + r + 1] = hi[1];
+                    pl[kk][4 * sb + r] = lo[0];
+                    pl[kk][4 * sb + r + 1] = lo[1];
                 }
         // O^T += V^T . P^T
 #pragma unroll
@@ -263,7 +329,7 @@ __global__ __launch_bounds__(64 * G * S) void attn_prefill_kernel(PrefillArgs a)
         float m = m_run;
 #pragma unroll
         for (int s2 = 1; s2 < S; ++s2) m = fmaxf(m, mrg[((s2 - 1) * G + w) * MSLOT + (NDT * 4) * 64 + lane]);
-        const float c0 = m_run == -INFINITY ? 0.f : expf(m_run - m);
+        const float c0 = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - m);
         l_run *= c0;
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) o[dt] *= c0;
@@ -271,7 +337,7 @@ __global__ __launch_bounds__(64 * G * S) void attn_prefill_kernel(PrefillArgs a)
         for (int s2 = 1; s2 < S; ++s2) {
             const float *slot = mrg + ((s2 - 1) * G + w) * MSLOT + lane;
             const float ms = slot[(NDT * 4) * 64];
-            const float cs = ms == -INFINITY ? 0.f : expf(ms - m);
+            const float cs = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - m);
             l_run += slot[(NDT * 4 + 1) * 64] * cs;
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt)
@@ -315,7 +381,11 @@ bool nnz_attn_prefill_supported(uint32_t head_dim, uint32_t hq, uint32_t hkv, ui
     return (G == 2 || G == 4 || G == 8) && max_ctx % 8 == 0;
 }
 
-int nnz_attn_prefill_launch(nnz_ctx *ctx, const float *q, const void *kc, const void *vc, void *out,
+float nnz_attn_prefill_qscale(uint32_t head_dim) {
+    return 1.44269504088896341f / sqrtf((float)head_dim);
+}
+
+int nnz_attn_prefill_launch(nnz_ctx *ctx, const void *q, const void *kc, const void *vc, void *out,
                             uint32_t start, uint32_t n, uint32_t hq, uint32_t hkv,
                             uint32_t head_dim, uint32_t max_ctx) {
     NNZ_REQUIRE(ctx, q && kc && vc && out && n > 0, NNZ_EINVAL, "attn_prefill: bad arguments");
@@ -326,7 +396,7 @@ int nnz_attn_prefill_launch(nnz_ctx *ctx, const float *q, const void *kc, const 
                 "attn_prefill: positions %u..%u beyond max_ctx %u", start, start + n - 1, max_ctx);
     NNZ_REQUIRE(ctx, (((uintptr_t)q | (uintptr_t)kc | (uintptr_t)vc | (uintptr_t)out) & 15) == 0,
                 NNZ_EINVAL, "attn_prefill: buffers must be 16-byte aligned");
-    PrefillArgs a{(const float *)q, (const f16_t *)kc, (const f16_t *)vc, (f16_t *)out,
-                  start, n, hq, max_ctx, 1.0f / sqrtf((float)head_dim)};
+    PrefillArgs a{(const f16_t *)q, (const f16_t *)kc, (const f16_t *)vc, (f16_t *)out,
+                  start, n, hq, max_ctx};
     return head_dim == 128 ? launch_d<128>(ctx, a, hkv, hq / hkv) : launch_d<64>(ctx, a, hkv, hq / hkv);
 }

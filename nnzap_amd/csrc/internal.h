@@ -135,19 +135,25 @@ int nnz_sample_launch(nnz_ctx *ctx, const float *logits, uint32_t n, const nnz_s
                       uint64_t *rng, void *ws, uint32_t *out_index, float *out_prob,
                       const NnzPick *pick);
 
-// Causal GQA attention of a prefill batch on MFMA (attn_prefill.hip): f32
-// queries [n][hq][D], f16 KV cache (V transposed), f16 output [n][hq][D].
+// Causal GQA attention of a prefill batch on MFMA (attn_prefill.hip):
+// queries as the prep kernel writes them with qsplit = nnz_attn_prefill_qscale
+// (f16 hi/lo rows [n][hq][2][D]), f16 KV cache (V transposed), f16 output
+// [n][hq][D].
 bool nnz_attn_prefill_supported(uint32_t head_dim, uint32_t hq, uint32_t hkv, uint32_t max_ctx);
-int nnz_attn_prefill_launch(nnz_ctx *ctx, const float *q, const void *kc, const void *vc, void *out,
+float nnz_attn_prefill_qscale(uint32_t head_dim);
+int nnz_attn_prefill_launch(nnz_ctx *ctx, const void *q, const void *kc, const void *vc, void *out,
                             uint32_t start, uint32_t n, uint32_t hq, uint32_t hkv,
                             uint32_t head_dim, uint32_t max_ctx);
 
 // Per-head q/k RMSNorm + RoPE and the KV append of a prefill batch, one wave
 // per (head, token) (transformer.hip); frequencies from a [head_dim/2] table.
+// q out: float32 [nq][hq][D] (qsplit 0), or pre-scaled by qsplit and split
+// into f16 hi/lo rows [nq][hq][2][D] (the MFMA prefill attention's operands).
 int nnz_attn_prep_waves_launch(nnz_ctx *ctx, const void *q, const void *kr, const void *vr,
-                               const float *qn, const float *kn, float *qout, void *kc, void *vc,
+                               const float *qn, const float *kn, void *qout, void *kc, void *vc,
                                const float *inv_freq, uint32_t hq, uint32_t hkv, uint32_t head_dim,
-                               uint32_t pos0, uint32_t nq, uint32_t max_ctx, float eps);
+                               uint32_t pos0, uint32_t nq, uint32_t max_ctx, float eps,
+                               float qsplit = 0.f);
 
 // One prefill GEMM launch over up to three 1-bit matrices that share K and
 // the f16 A operand, each written to its own f16 output [P][rows] (gemm.hip).

@@ -813,11 +813,13 @@ int nnz_model_prefill(nnz_model *m, const uint32_t *tokens_host, uint32_t n, uin
             void *outs[3] = {m->p_q, m->p_k, m->p_v};
             RC(nnz_gemm_segments_launch(ctx, ws, outs, 3, m->p_xn, n, H, c.group_size));
         }
+        const bool mfma_attn = nnz_attn_prefill_supported(c.head_dim, c.num_query_heads,
+                                                          c.num_kv_heads, c.max_context_length);
         RC(nnz_attn_prep_waves_launch(ctx, m->p_q, m->p_k, m->p_v, Ly.q_norm, Ly.k_norm, m->p_qf,
                                       Ly.kc, Ly.vc, m->rope_inv, c.num_query_heads, c.num_kv_heads,
-                                      c.head_dim, start, n, c.max_context_length, c.rms_eps));
-        if (nnz_attn_prefill_supported(c.head_dim, c.num_query_heads, c.num_kv_heads,
-                                       c.max_context_length)) {
+                                      c.head_dim, start, n, c.max_context_length, c.rms_eps,
+                                      mfma_attn ? nnz_attn_prefill_qscale(c.head_dim) : 0.f));
+        if (mfma_attn) {
             RC(nnz_attn_prefill_launch(ctx, m->p_qf, Ly.kc, Ly.vc, m->p_att, start, n,
                                        c.num_query_heads, c.num_kv_heads, c.head_dim,
                                        c.max_context_length));

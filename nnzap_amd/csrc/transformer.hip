@@ -274,10 +274,13 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(
 // The same prologue for a prefill batch: one wave per (head, token), lane p
 // holding the rotation pair (2p, 2p+1), so the norm is one wave reduction
 // and the rotation needs no shuffle; frequencies from the model's table.
+// q goes out as float32 [nq][hq][D], or, with qsplit > 0, as the operands
+// of the MFMA prefill attention: x = q * qsplit as f16 hi = f16(x) and
+// lo = f16(x - hi), [nq][hq][2][D] (hi row, then lo row).
 __global__ __launch_bounds__(256) void attn_prep_waves_kernel(
     const f16_t *q, const f16_t *kr, const f16_t *vr, const float *qn, const float *kn,
-    float *qout, f16_t *kc, f16_t *vc, const float *inv_freq, uint32_t hq, uint32_t hkv,
-    uint32_t head_dim, uint32_t pos0, uint32_t nq, uint32_t max_ctx, float eps) {
+    void *qout, f16_t *kc, f16_t *vc, const float *inv_freq, uint32_t hq, uint32_t hkv,
+    uint32_t head_dim, uint32_t pos0, uint32_t nq, uint32_t max_ctx, float eps, float qsplit) {
     const uint32_t heads = hq + hkv;
     const uint32_t u = blockIdx.x * 4u + (threadIdx.x >> 6);
     if (u >= heads * nq) return;   // whole waves only
@@ -302,8 +305,17 @@ __global__ __launch_bounds__(256) void attn_prep_waves_kernel(
     float sn, cs;
     sincosf(ang, &sn, &cs);
     const float r0 = fmaf(v0, cs, -v1 * sn), r1 = fmaf(v0, sn, v1 * cs);
-    if (isq) {
-        *(float2 *)(qout + ((size_t)z * hq + h) * head_dim + 2u * p) = make_float2(r0, r1);
+    if (isq && qsplit > 0.f) {
+        const float x0 = r0 * qsplit, x1 = r1 * qsplit;
+        const f16_t h0 = (f16_t)x0, h1 = (f16_t)x1;
+        const f16_t l0 = (f16_t)(x0 - (float)h0), l1 = (f16_t)(x1 - (float)h1);
+        f16_t *row = (f16_t *)qout + ((size_t)z * hq + h) * 2u * head_dim + 2u * p;
+        *(uint32_t *)row = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
+                           (uint32_t)__builtin_bit_cast(uint16_t, h1) << 16;
+        *(uint32_t *)(row + head_dim) = (uint32_t)__builtin_bit_cast(uint16_t, l0) |
+                                        (uint32_t)__builtin_bit_cast(uint16_t, l1) << 16;
+    } else if (isq) {
+        *(float2 *)((float *)qout + ((size_t)z * hq + h) * head_dim + 2u * p) = make_float2(r0, r1);
     } else {
         const size_t stride = (size_t)max_ctx * head_dim;
         const uint32_t kw = (uint32_t)__builtin_bit_cast(uint16_t, (f16_t)r0) |
@@ -2192,15 +2204,15 @@ int nnz_attn_prep_launch(nnz_ctx *ctx, const void *q, const void *kr, const void
 }
 
 int nnz_attn_prep_waves_launch(nnz_ctx *ctx, const void *q, const void *kr, const void *vr,
-                               const float *qn, const float *kn, float *qout, void *kc, void *vc,
+                               const float *qn, const float *kn, void *qout, void *kc, void *vc,
                                const float *inv_freq, uint32_t hq, uint32_t hkv, uint32_t head_dim,
-                               uint32_t pos0, uint32_t nq, uint32_t max_ctx, float eps) {
+                               uint32_t pos0, uint32_t nq, uint32_t max_ctx, float eps, float qsplit) {
     NNZ_REQUIRE(ctx, head_dim % 2 == 0 && head_dim <= 128, NNZ_EUNSUPPORTED,
                 "attn_prep: head_dim %u (even, <= 128)", head_dim);
     const uint32_t units = (hq + hkv) * nq;
     attn_prep_waves_kernel<<<ceil_div(units, 4u), 256, 0, ctx->stream>>>(
         (const f16_t *)q, (const f16_t *)kr, (const f16_t *)vr, qn, kn, qout, (f16_t *)kc,
-        (f16_t *)vc, inv_freq, hq, hkv, head_dim, pos0, nq, max_ctx, eps);
+        (f16_t *)vc, inv_freq, hq, hkv, head_dim, pos0, nq, max_ctx, eps, qsplit);
     NNZ_LAUNCHED(ctx);
     return NNZ_OK;
 }

@@ -105,6 +105,25 @@ def test_tiny_prefill_chunks_match_single_prefill(mdev, tiny):
         b.close()
 
 
+def test_tiny_long_prefill_matches_oracle(mdev):
+    """Prompts longer than one 256-key staging step of the MFMA prefill
+    attention: a 512-token batch (every step inside the batch) and a second
+    batch of 88 tokens at start 512 (its last step crosses the batch end),
+    each against the oracle."""
+    cfg = cf.DecoderConfig(**{**cf.TINY.__dict__, "max_context_length": 1024,
+                              "max_prefill_length": 512})
+    w = cf.decoder_weights(cfg, norm_mode="unit")
+    ids = cf.prompt_ids(cfg, 600)
+    ref = OracleDecoder(w).forward(list(ids), 0)
+    m = DecoderModel(mdev, cfg)
+    try:
+        m.load(w)
+        assert_close_normwise(m.prefill(ids[:512], 0), ref[511], what="512-token prefill")
+        assert_close_normwise(m.prefill(ids[512:], 512), ref[599], what="prefill at start 512")
+    finally:
+        m.close()
+
+
 @pytest.mark.parametrize("use_graph", [True, False])
 def test_tiny_generate_matches_oracle(mdev, tiny, use_graph):
     cfg, w = tiny

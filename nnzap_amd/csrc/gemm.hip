@@ -339,8 +339,11 @@ __device__ __forceinline__ half8 expand_nibbles(uint32_t w) {
     return r;
 }
 
+// At most 256 registers (two waves per SIMD): the pair kernel otherwise
+// takes 222 VGPRs + 64 AGPRs, one wave per SIMD, and copies every MFMA
+// result out of the AGPRs before its scaling.
 template <int MODE, int NMAT, int KQ>
-__global__ __launch_bounds__(128 * KQ) void dq4_gemm_kernel(const f16_t *A, const uint32_t *codes0,
+__global__ __launch_bounds__(128 * KQ) __attribute__((amdgpu_waves_per_eu(2))) void dq4_gemm_kernel(const f16_t *A, const uint32_t *codes0,
                                                               const uint16_t *scales0,
                                                               const uint16_t *biases0,
                                                               const uint32_t *codes1,

@@ -399,8 +399,11 @@ __global__ __launch_bounds__(128 * KQ) __attribute__((amdgpu_waves_per_eu(2))) v
     const uint16_t *wl_b = (NMAT == 2 && wl_m == 1 ? biases1 : biases0) + (size_t)wrow_g * groups_per_row;
     const int gsel = lane >> 4;   // the lane's code word within a 32-k half step
 
+    // scale and bias stay two registers until the stage: joining them at
+    // the issue would wait there for their loads, and with them (vmcnt is
+    // in order) for the A loads of the stage being prefetched
     u32x4 areg[A_LOADS], wc0 = {0u, 0u, 0u, 0u}, wc1 = {0u, 0u, 0u, 0u};
-    uint32_t sbreg = 0;
+    uint32_t sreg = 0, breg = 0;
     auto issue = [&](uint32_t st) __attribute__((always_inline)) {
         const uint32_t ka = min(st * Q4_KQ + (uint32_t)(lp >> 3), nk - 1) * BK;
 #pragma unroll
@@ -410,7 +413,8 @@ __global__ __launch_bounds__(128 * KQ) __attribute__((amdgpu_waves_per_eu(2))) v
             wc0 = *(const u32x4 *)(wl_codes + 8 * ks);
             wc1 = *(const u32x4 *)(wl_codes + 8 * ks + 4);
             const uint32_t g = (ks * BK) >> gs_log2;
-            sbreg = (uint32_t)wl_s[g] | ((uint32_t)wl_b[g] << 16);
+            sreg = wl_s[g];
+            breg = wl_b[g];
         }
     };
     auto stage = [&](uint32_t st) __attribute__((always_inline)) {
@@ -424,7 +428,7 @@ __global__ __launch_bounds__(128 * KQ) __attribute__((amdgpu_waves_per_eu(2))) v
             uint32_t *row = Ws[st & 1][wl_m] + wl_row * WR;
             *(u32x4 *)(row + 8 * wl_q) = wc0;
             *(u32x4 *)(row + 8 * wl_q + 4) = wc1;
-            row[8 * KQ + wl_q] = sbreg;
+            row[8 * KQ + wl_q] = sreg | (breg << 16);
         }
     };
     const half8 ones = {(_Float16)1.f, (_Float16)1.f, (_Float16)1.f, (_Float16)1.f,

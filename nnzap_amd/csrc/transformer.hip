@@ -1593,11 +1593,21 @@ void attn_stream_kernel(DecAttnArgs a) {
         __builtin_amdgcn_wave_barrier();   // the next group rewrites pw[w]
     };
 
-    for (uint32_t i = 0; i < nit; i += 2) {
-        load(kB, vB, i + 1);
-        compute(kA, vA, i);
-        load(kA, vA, i + 2);
-        if (i + 1 < nit) compute(kB, vB, i + 1);
+    // group i + 1 in flight while group i is computed.  The loads in the
+    // loop are unconditional (past the wave's last group they re-read it):
+    // skipping them by branches leaves the compiler a full wait at every
+    // join (L = 32768 27.8 -> 30.0 us); a third register set with two
+    // groups in flight measured slower too (29.0 us).  A wave with one
+    // group (short chunks) loads it alone.
+    if (nit <= 1) {
+        if (nit == 1) compute(kA, vA, 0);
+    } else {
+        for (uint32_t i = 0; i < nit; i += 2) {
+            load(kB, vB, i + 1);
+            compute(kA, vA, i);
+            load(kA, vA, i + 2);
+            if (i + 1 < nit) compute(kB, vB, i + 1);
+        }
     }
 
     // the 4 waves' states -> one (m, l, o) per query head

@@ -37,6 +37,9 @@
 namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+// 16-byte staging pieces as a native vector (a struct type is copied by
+// memcpy, which can keep the staging arrays in scratch memory)
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 
 constexpr int KT = 64;  // keys per LDS tile
@@ -70,6 +73,10 @@ __global__ __launch_bounds__(64 * G * S) void attn_prefill_kernel(PrefillArgs a)
     __shared__ __align__(16) unsigned char smem[SMEM];
     _Float16 *Ks = (_Float16 *)smem;              // [S][KT][KP]
     _Float16 *Vs = (_Float16 *)smem + S * KTILE;  // [S][D][VP]
+    // the queries of the block with key splits: [G][16][QP], row pitch
+    // 2D + 8 halves (the 16 rows of a fragment read hit distinct banks)
+    constexpr int QP = 2 * D + 8;
+    __shared__ __align__(16) _Float16 Qs[S > 1 ? G * 16 * QP : 8];
 
     const int tid = threadIdx.x, lane = tid & 63, w = (tid >> 6) % G, ws = (tid >> 6) / G;
     const int g = lane >> 4, c = lane & 15;
@@ -86,47 +93,28 @@ __global__ __launch_bounds__(64 * G * S) void attn_prefill_kernel(PrefillArgs a)
     // Q^T fragments: lane (g, c) holds dims 32 ks + 8 g .. +8 of query c,
     // the f16 hi and lo parts the prep kernel wrote (zero past the batch).
     // With key splits the S waves of a head share one copy: the block loads
-    // its 16 queries x G heads once into LDS (row pitch 2D + 8 halves: the
-    // 16 rows of a fragment read hit distinct banks; the buffer is the tile
-    // area, free until the first tile is stored) and each wave reads its
-    // fragments from there.
+    // its 16 queries x G heads once into Qs and each wave reads its
+    // fragments from there.  The query loads are issued first and the first
+    // tile's right after them; both are used only at the first stage, so
+    // their latencies overlap.
+    constexpr int QROW = G * 2 * D / 8;   // Q staging: 16-byte pieces per query
+    constexpr int QPT = S > 1 ? 16 * QROW / NT : 1;
+    static_assert(S == 1 || 16 * QROW % NT == 0, "Q staging layout");
+    v4u qr[QPT];
     half8 qh[NKS], ql[NKS];
-    const half8 zero = {};
     if constexpr (S > 1) {
-        constexpr int QP = 2 * D + 8, QROW = G * 2 * D / 8, QPT = 16 * QROW / NT;   // pieces
-        static_assert(16 * QROW % NT == 0, "Q staging layout");
-        static_assert(16 * G * QP * 2 <= SMEM, "Q fits the tile area");
-        _Float16 *Qs = (_Float16 *)smem;
-        uint4 qr[QPT];
 #pragma unroll
         for (int i = 0; i < QPT; ++i) {
             const uint32_t p = (uint32_t)(tid + i * NT), qc = p / QROW, e = p % QROW;
             const uint32_t qq = q0 + qc < a.n ? q0 + qc : 0u;
-            const uint4 v = *(const uint4 *)(a.q + ((size_t)qq * a.hq + hkv * G) * (2 * D) + e * 8);
-            qr[i] = q0 + qc < a.n ? v : make_uint4(0u, 0u, 0u, 0u);
+            qr[i] = *(const v4u *)(a.q + ((size_t)qq * a.hq + hkv * G) * (2 * D) + e * 8);
         }
-#pragma unroll
-        for (int i = 0; i < QPT; ++i) {
-            const uint32_t p = (uint32_t)(tid + i * NT), qc = p / QROW, e = p % QROW;
-            const uint32_t hw = e / (2 * D / 8), col = e % (2 * D / 8);
-            *(uint4 *)(Qs + (hw * 16 + qc) * QP + col * 8) = qr[i];
-        }
-        __syncthreads();
-        const _Float16 *qrow = Qs + (w * 16 + c) * QP;
-#pragma unroll
-        for (int ks = 0; ks < NKS; ++ks) {
-            qh[ks] = *(const half8 *)(qrow + 32 * ks + 8 * g);
-            ql[ks] = *(const half8 *)(qrow + D + 32 * ks + 8 * g);
-        }
-        __syncthreads();   // before the tiles overwrite Qs
     } else {
         const f16_t *qp = a.q + ((size_t)(qvalid ? qi : 0u) * a.hq + h) * (2 * D);
 #pragma unroll
         for (int ks = 0; ks < NKS; ++ks) {
-            const half8 hv = *(const half8 *)(qp + 32 * ks + 8 * g);
-            const half8 lv = *(const half8 *)(qp + D + 32 * ks + 8 * g);
-            qh[ks] = qvalid ? hv : zero;
-            ql[ks] = qvalid ? lv : zero;
+            qh[ks] = *(const half8 *)(qp + 32 * ks + 8 * g);
+            ql[ks] = *(const half8 *)(qp + D + 32 * ks + 8 * g);
         }
     }
     float4v o[NDT];
@@ -138,11 +126,8 @@ __global__ __launch_bounds__(64 * G * S) void attn_prefill_kernel(PrefillArgs a)
     const f16_t *vbase = a.vc + (size_t)hkv * D * a.max_ctx;
     // Tiles are staged through registers, one ahead: the next tile's loads
     // are in flight while the current one is computed.  A step stages S
-    // consecutive tiles, tile j of the step in LDS slot j.  A step inside
-    // the batch (the common case) loads without checks; one that crosses
-    // its end clamps the addresses into the cache and zeroes the keys past
-    // it by selects (8-key V pieces never cross max_ctx: max_ctx % 8 == 0).
-    // Lane offsets: staging piece i of lane tid is K row krow + i NT/(D/8)
+    // consecutive tiles, tile j of the step in LDS slot j (8-key V pieces
+    // never cross max_ctx: max_ctx % 8 == 0).  Lane offsets: staging piece i of lane tid is K row krow + i NT/(D/8)
     // of the step, dims kcol..+8, and V^T row vrow + (i NT mod D KT/8)/(KT/8)
     // of tile (i NT)/(D KT/8), keys vcol..+8.
     constexpr int KPT = S * KT * D / 8 / NT, VPT = S * D * KT / 8 / NT;
@@ -151,70 +136,92 @@ __global__ __launch_bounds__(64 * G * S) void attn_prefill_kernel(PrefillArgs a)
     static_assert(KT % RPI == 0 || RPI % KT == 0, "a K piece lies in one tile");
     const uint32_t krow = (uint32_t)tid / (D / 8), kcol = ((uint32_t)tid % (D / 8)) * 8u;
     const uint32_t vrow = (uint32_t)tid / (KT / 8), vcol = ((uint32_t)tid % (KT / 8)) * 8u;
-    const uint32_t voff = vrow * a.max_ctx + vcol;
-    uint4 kr[KPT], vr[VPT];
-    auto load_tile = [&](uint32_t k0) __attribute__((always_inline)) {
-        if (k0 + (uint32_t)(S * KT) <= seq_end) {   // block-uniform
-            // pieces of tiles no query of the block reaches stay unloaded
-            // (their LDS slots are never read)
-#pragma unroll
-            for (int i = 0; i < KPT; ++i)
-                if (k0 + (uint32_t)((i * RPI) / KT * KT) <= qlast)
-                    kr[i] = *(const uint4 *)(kbase + (k0 + (uint32_t)(i * RPI) + krow) * D + kcol);
-#pragma unroll
-            for (int i = 0; i < VPT; ++i) {
-                constexpr uint32_t TS = D * KT / 8;
-                const uint32_t j = (uint32_t)(i * NT) / TS, dr = ((uint32_t)(i * NT) % TS) / (KT / 8);
-                if (k0 + j * KT <= qlast)
-                    vr[i] = *(const uint4 *)(vbase + voff + dr * a.max_ctx + k0 + j * KT);
-            }
-            return;
-        }
+    v4u kr[KPT], vr[VPT];
+    // live = false: nothing to stage (the loop's look-ahead past the last
+    // step).  Nothing uses the loaded data before the stage (an early use
+    // would wait there for every older load, the query loads' wait for the
+    // first tile's).  Pieces of tiles no query of the block reaches are not
+    // loaded (block-uniform branches; their LDS slots are never read);
+    // pieces of keys past the batch read the head's key 0 instead (in
+    // bounds for any max_ctx): such K rows are finite and their scores
+    // masked, and V pieces past the batch are zeroed at the stage, since
+    // p = 0 must not meet a non-finite value.
+    auto load_tile = [&](uint32_t k0, bool live) __attribute__((always_inline)) {
+        if (!live) return;
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
+            if (k0 + (uint32_t)((i * RPI) / KT * KT) > qlast) continue;
             const uint32_t key = k0 + (uint32_t)(i * RPI) + krow;
-            const uint32_t kc = key < seq_end ? key : 0u;
-            const uint4 v = *(const uint4 *)(kbase + kc * D + kcol);
-            kr[i] = key < seq_end ? v : make_uint4(0u, 0u, 0u, 0u);
+            kr[i] = *(const v4u *)(kbase + (key < seq_end ? key * D + kcol : kcol));
         }
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             constexpr uint32_t TS = D * KT / 8;
             const uint32_t j = (uint32_t)(i * NT) / TS, dr = ((uint32_t)(i * NT) % TS) / (KT / 8);
+            if (k0 + j * KT > qlast) continue;
             const uint32_t key = k0 + j * KT + vcol;
-            const uint32_t kc = key < seq_end ? key : 0u;
-            uint4 v = *(const uint4 *)(vbase + (vrow + dr) * a.max_ctx + kc);
-            // halves e with key + e >= seq_end become 0
-            const int keep = key >= seq_end ? 0 : (int)(seq_end - key < 8u ? seq_end - key : 8u);
-            const uint32_t m[4] = {keep >= 2 ? ~0u : (keep >= 1 ? 0xFFFFu : 0u),
-                                   keep >= 4 ? ~0u : (keep >= 3 ? 0xFFFFu : 0u),
-                                   keep >= 6 ? ~0u : (keep >= 5 ? 0xFFFFu : 0u),
-                                   keep >= 8 ? ~0u : (keep >= 7 ? 0xFFFFu : 0u)};
-            v.x &= m[0];
-            v.y &= m[1];
-            v.z &= m[2];
-            v.w &= m[3];
-            vr[i] = v;
+            vr[i] = *(const v4u *)(vbase + (vrow + dr) * a.max_ctx + (key < seq_end ? key : 0u));
         }
     };
-    auto store_tile = [&]() __attribute__((always_inline)) {
+    auto store_tile = [&](uint32_t k0) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
             const int p = tid + i * NT;
-            *(uint4 *)(Ks + (p / (D / 8)) * KP + (p % (D / 8)) * 8) = kr[i];
+            *(v4u *)(Ks + (p / (D / 8)) * KP + (p % (D / 8)) * 8) = kr[i];
+        }
+        if (k0 + (uint32_t)(S * KT) > seq_end) {   // block-uniform: the step crosses the batch end
+#pragma unroll
+            for (int i = 0; i < VPT; ++i) {   // halves e with key + e >= seq_end become 0
+                const uint32_t key = k0 + (uint32_t)((i * NT) / (D * KT / 8) * KT) + vcol;
+                const int keep = key >= seq_end ? 0 : (int)(seq_end - key < 8u ? seq_end - key : 8u);
+                vr[i].x &= keep >= 2 ? ~0u : (keep >= 1 ? 0xFFFFu : 0u);
+                vr[i].y &= keep >= 4 ? ~0u : (keep >= 3 ? 0xFFFFu : 0u);
+                vr[i].z &= keep >= 6 ? ~0u : (keep >= 5 ? 0xFFFFu : 0u);
+                vr[i].w &= keep >= 8 ? ~0u : (keep >= 7 ? 0xFFFFu : 0u);
+            }
         }
 #pragma unroll
         for (int i = 0; i < VPT; ++i) {
             const int p = tid + i * NT;
             const int j = p / (D * KT / 8), pp = p % (D * KT / 8);
-            *(uint4 *)(Vs + j * VTILE + (pp / (KT / 8)) * VP + (pp % (KT / 8)) * 8) = vr[i];
+            *(v4u *)(Vs + j * VTILE + (pp / (KT / 8)) * VP + (pp % (KT / 8)) * 8) = vr[i];
         }
     };
-    load_tile(0);
+    load_tile(0, true);
+
+    // The first stage also stages the queries (zeros past the batch): with
+    // key splits into their own LDS rows, read back after its barrier.
+    store_tile(0u);
+    if constexpr (S > 1) {
+#pragma unroll
+        for (int i = 0; i < QPT; ++i) {
+            const uint32_t p = (uint32_t)(tid + i * NT), qc = p / QROW, e = p % QROW;
+            const uint32_t hw = e / (2 * D / 8), col = e % (2 * D / 8);
+            *(v4u *)(Qs + (hw * 16 + qc) * QP + col * 8) = q0 + qc < a.n ? qr[i] : (v4u){0u, 0u, 0u, 0u};
+        }
+    }
+    __syncthreads();
+    if constexpr (S > 1) {
+        const _Float16 *qrow = Qs + (w * 16 + c) * QP;
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+            qh[ks] = *(const half8 *)(qrow + 32 * ks + 8 * g);
+            ql[ks] = *(const half8 *)(qrow + D + 32 * ks + 8 * g);
+        }
+    } else {
+        const half8 zero = {};
+#pragma unroll
+        for (int ks = 0; ks < NKS; ++ks) {
+            qh[ks] = qvalid ? qh[ks] : zero;
+            ql[ks] = qvalid ? ql[ks] : zero;
+        }
+    }
     for (uint32_t step = 0; step < nsteps; ++step) {
-        store_tile();
-        __syncthreads();
-        if (step + 1 < nsteps) load_tile((step + 1) * (S * KT));
+        if (step > 0) {   // block-uniform
+            store_tile(step * (S * KT));
+            __syncthreads();
+        }
+        load_tile((step + 1) * (S * KT), step + 1 < nsteps);
         const uint32_t t = step * S + (uint32_t)ws;   // this wave's tile
         if (t < ntiles) {   // wave-uniform
         const uint32_t k0 = t * KT;

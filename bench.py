@@ -541,6 +541,12 @@ def _kernel_cases():
         # floor.  HIP events on the library stream around single launches,
         # best of 5 after a warm-up.
         def run(dev, n):
+            # The working set comes from fresh device memory: served from
+            # segments the allocator cached for the cases before it, the
+            # 1.8 GB config-1 stack streamed 20-25 % slower (399.6 against
+            # 326.0 us after an empty_cache, 318.8 us run alone).
+            torch.cuda.synchronize()
+            torch.cuda.empty_cache()
             shp = {"config1": (6144, 2048, 64, 4), "config2": (2048, 6144, 128, 1),
                    "config3": (6144, 2048, 128, 1), "q1_6144x2048": (6144, 2048, 128, 1)}[kind]
             M_, K_, gs, bits = shp

@@ -35,6 +35,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // register arrays of 16-byte pieces
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+template <int V> struct IC { static constexpr int value = V; };   // a compile-time index argument
 
 constexpr int BM = 64, BN = 64, BK = 64;
 // KQ k-phases (2 KQ waves, 128 KQ threads); an LDS stage holds KQ k-steps.
@@ -263,19 +264,49 @@ __global__ __launch_bounds__(64 * WN * KQ) void dq_gemm_kernel(const f16_t *A, c
                 for (int j = 0; j < NJ; ++j) acc[m][i][j] += red[(slot * NF + (m * 4 + i) * NJ + j) * 64 + lane];
     };
     static_assert(KQ / 2 * WN * NF * 64 * 16 <= (int)sizeof(As), "reduction slots fit the stage buffers");
-    // tree over the k-phases: phases [h, 2h) hand their tiles to [0, h)
+    // tree over the k-phases: phases [h, 2h) hand their tiles to [0, h),
+    // down to phases 0 and 1
 #pragma unroll
-    for (int h = KQ / 2; h >= 1; h /= 2) {
+    for (int h = KQ / 2; h >= 2; h /= 2) {
         if (kq >= h && kq < 2 * h) put((kq - h) * WN + wn);
         __syncthreads();
         if (kq < h) add(kq * WN + wn);
         __syncthreads();
     }
-    if (kq != 0) return;   // after the last barrier
+    // Phases 0 and 1 swap halves and both finish the block: phase 0 the
+    // 16-row tiles i = 0, 1, phase 1 the tiles i = 2, 3.  (With phase 0
+    // finishing everything, the waves of phase 0 -- the same SIMDs in every
+    // block -- carried the whole epilogue.)  Half slots: NF / 2 float4.
+    auto put_half = [&](int slot, auto hh) __attribute__((always_inline)) {
+        constexpr int H = decltype(hh)::value;
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+                    red[(slot * (NF / 2) + (m * 2 + ii) * NJ + j) * 64 + lane] = acc[m][2 * H + ii][j];
+    };
+    auto add_half = [&](int slot, auto hh) __attribute__((always_inline)) {
+        constexpr int H = decltype(hh)::value;
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
+                    acc[m][2 * H + ii][j] += red[(slot * (NF / 2) + (m * 2 + ii) * NJ + j) * 64 + lane];
+    };
+    if (kq == 0) put_half(WN + wn, IC<1>{});   // phase 1's tiles
+    else if (kq == 1) put_half(wn, IC<0>{});  // phase 0's tiles
+    __syncthreads();
+    if (kq >= 2) return;   // after the last barrier
+    if (kq == 0) add_half(wn, IC<0>{});
+    else add_half(WN + wn, IC<1>{});
 
     // D layout: lane holds rows 4*(lane/16)+r, column lane%16 of each 16x16 tile.
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
+    auto epilogue = [&](auto ti) __attribute__((always_inline)) {
+        constexpr int i = decltype(ti)::value;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint32_t p = p0 + i * 16 + 4 * (lane >> 4) + r;
@@ -294,6 +325,14 @@ __global__ __launch_bounds__(64 * WN * KQ) void dq_gemm_kernel(const f16_t *A, c
                 }
             }
         }
+    };
+    if (kq == 0) {
+        epilogue(IC<0>{});
+        epilogue(IC<1>{});
+    } else {
+        epilogue(IC<2>{});
+        epilogue(IC<3>{});
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -484,12 +523,12 @@ __global__ __launch_bounds__(128 * KQ) __attribute__((amdgpu_waves_per_eu(2))) v
     }
 
     // k-phase tree through the (free) A buffers: phases [h, 2h) hand their
-    // tiles to [0, h)
+    // tiles to [0, h), down to phases 0 and 1
     constexpr int NF = NMAT * 8;
     static_assert(KQ / 2 * 2 * NF * 64 * 16 <= (int)sizeof(As), "reduction slots fit the stage buffers");
     float4v *red = (float4v *)&As[0][0];
 #pragma unroll
-    for (int h = KQ / 2; h >= 1; h /= 2) {
+    for (int h = KQ / 2; h >= 2; h /= 2) {
         if (kq >= h && kq < 2 * h) {
 #pragma unroll
             for (int m = 0; m < NMAT; ++m)
@@ -511,10 +550,38 @@ __global__ __launch_bounds__(128 * KQ) __attribute__((amdgpu_waves_per_eu(2))) v
         }
         __syncthreads();
     }
-    if (kq != 0) return;   // after the last barrier
-
+    // Phases 0 and 1 swap halves and both finish the block: phase 0 the
+    // 16-row tiles i = 0, 1, phase 1 the tiles i = 2, 3 (half slots of
+    // NF / 2 float4).
+    auto put_half = [&](int slot, auto hh) __attribute__((always_inline)) {
+        constexpr int H = decltype(hh)::value;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+        for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    red[(slot * (NF / 2) + (m * 2 + ii) * 2 + j) * 64 + lane] = acc[m][2 * H + ii][j];
+    };
+    auto add_half = [&](int slot, auto hh) __attribute__((always_inline)) {
+        constexpr int H = decltype(hh)::value;
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+            for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[m][2 * H + ii][j] += red[(slot * (NF / 2) + (m * 2 + ii) * 2 + j) * 64 + lane];
+    };
+    if (kq == 0) put_half(2 + wn, IC<1>{});   // phase 1's tiles
+    else if (kq == 1) put_half(wn, IC<0>{});  // phase 0's tiles
+    __syncthreads();
+    if (kq >= 2) return;   // after the last barrier
+    if (kq == 0) add_half(wn, IC<0>{});
+    else add_half(2 + wn, IC<1>{});
+
+    auto epilogue = [&](auto ti) __attribute__((always_inline)) {
+        constexpr int i = decltype(ti)::value;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const uint32_t p = p0 + i * 16 + 4 * (lane >> 4) + r;
@@ -533,6 +600,14 @@ __global__ __launch_bounds__(128 * KQ) __attribute__((amdgpu_waves_per_eu(2))) v
                 }
             }
         }
+    };
+    if (kq == 0) {
+        epilogue(IC<0>{});
+        epilogue(IC<1>{});
+    } else {
+        epilogue(IC<2>{});
+        epilogue(IC<3>{});
+    }
 }
 
 // k-phases and W-row groups of the single-matrix launches.  Measured at P =

@@ -105,13 +105,16 @@ def test_tiny_prefill_chunks_match_single_prefill(mdev, tiny):
         b.close()
 
 
-def test_tiny_long_prefill_matches_oracle(mdev):
-    """Prompts longer than one 256-key staging step of the MFMA prefill
-    attention: a 512-token batch (every step inside the batch) and a second
-    batch of 88 tokens at start 512 (its last step crosses the batch end),
-    each against the oracle."""
+@pytest.mark.parametrize("hq,hkv,hd", [(4, 2, 64), (8, 2, 128), (16, 2, 64)])
+def test_tiny_long_prefill_matches_oracle(mdev, hq, hkv, hd):
+    """Prompts longer than one staging step of the MFMA prefill attention
+    (256 keys with key splits, G = 2; 64 keys for G = 4 and 8): a 512-token
+    batch (every step inside the batch) and a second batch of 88 tokens at
+    start 512 (its last step crosses the batch end), each against the
+    oracle."""
     cfg = cf.DecoderConfig(**{**cf.TINY.__dict__, "max_context_length": 1024,
-                              "max_prefill_length": 512})
+                              "max_prefill_length": 512, "num_query_heads": hq,
+                              "num_kv_heads": hkv, "head_dim": hd})
     w = cf.decoder_weights(cfg, norm_mode="unit")
     ids = cf.prompt_ids(cfg, 600)
     ref = OracleDecoder(w).forward(list(ids), 0)

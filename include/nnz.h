@@ -575,11 +575,12 @@ int nnz_model_generate(nnz_model *m, const uint32_t *prompt_host, uint32_t n_pro
 /* The same loop split for streaming callers and benchmarks (decodeOneToken,
  * transformer.zig:4072, without the per-token host sync):
  *   nnz_model_decode_begin: prefill the prompt, take the greedy first token,
- *     capture the decode-step graph for up to `max_new` steps;
+ *     capture the decode-step graphs for up to `max_new` steps (at most 8,
+ *     each sized for the sequence lengths of the steps it serves);
  *   nnz_model_decode_steps: enqueue `n` graph replays (asynchronous);
  *   nnz_model_decode_read: copy the first `n` emitted tokens (and margins)
  *     to the host after a bounded sync;
- *   nnz_model_decode_end: release the graph. */
+ *   nnz_model_decode_end: release the graphs. */
 int nnz_model_decode_begin(nnz_model *m, const uint32_t *prompt_host, uint32_t n_prompt,
                            uint32_t max_new);
 int nnz_model_decode_steps(nnz_model *m, uint32_t n);

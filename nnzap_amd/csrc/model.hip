@@ -267,6 +267,30 @@ struct Layer {
     void *kc = nullptr, *vc = nullptr;
 };
 
+// The decode steps of one plan as a few captured graphs.  Step i attends
+// over first + i keys; the graph serving it sizes the attention grid and the
+// O projection's merge for the longest sequence of its bucket (top), so the
+// partials of attention chunks past the live length are neither launched
+// for nor read.  Buckets are whole attention chunks, at most
+// MAX_STEP_GRAPHS graphs per plan.
+constexpr uint32_t MAX_STEP_GRAPHS = 8;
+struct StepGraphs {
+    std::vector<nnz_graph *> g;
+    std::vector<uint32_t> top;
+    uint32_t first = 0;
+    bool empty() const { return g.empty(); }
+    nnz_graph *for_seq(uint32_t seq) const {
+        size_t b = 0;
+        while (b + 1 < g.size() && seq > top[b]) ++b;
+        return g[b];
+    }
+    void destroy() {
+        for (nnz_graph *x : g) nnz_graph_destroy(x);
+        g.clear();
+        top.clear();
+    }
+};
+
 }  // namespace
 
 struct nnz_model {
@@ -301,9 +325,9 @@ struct nnz_model {
     uint32_t *p_ids = nullptr;
     std::vector<void *> allocs;
     // streaming decode (decode_begin / steps / read / end)
-    nnz_graph *step_graph = nullptr;
+    StepGraphs steps;
     uint32_t stream_steps_left = 0;
-    uint32_t stream_emitted = 0;
+    uint32_t stream_step = 0;       // steps queued so far
 };
 
 namespace {
@@ -676,7 +700,7 @@ int nnz_model_create(nnz_ctx *ctx, const nnz_model_config *cfg, nnz_model **out)
 int nnz_model_destroy(nnz_model *m) {
     if (!m) return NNZ_EINVAL;
     hipStreamSynchronize(m->ctx->stream);
-    if (m->step_graph) nnz_graph_destroy(m->step_graph);
+    m->steps.destroy();
     for (void *p : m->allocs) hipFree(p);
     delete m;
     return NNZ_OK;
@@ -756,7 +780,7 @@ int nnz_model_forward_decode(nnz_model *m, uint32_t token_id, uint32_t position)
                 "forward_decode: position %u >= max_context_length", position);
     NNZ_REQUIRE(ctx, token_id < m->c.vocab_size, NNZ_EINVAL, "forward_decode: token id out of range");
     NNZ_REQUIRE(ctx, !ctx->capturing, NNZ_ESTATE, "forward_decode: use generate() for graphs");
-    NNZ_REQUIRE(ctx, !m->step_graph, NNZ_ESTATE,
+    NNZ_REQUIRE(ctx, m->steps.empty(), NNZ_ESTATE,
                 "forward_decode: a decode stream is active (call decode_end first)");
     const uint32_t st[ST_WORDS] = {token_id, position, position + 1, 0, 0};
     NNZ_HIP(ctx, hipMemcpyAsync(m->state, st, sizeof(st), hipMemcpyHostToDevice, ctx->stream));
@@ -776,7 +800,7 @@ int nnz_model_prefill(nnz_model *m, const uint32_t *tokens_host, uint32_t n, uin
     // A captured decode stream replays an attention plan sized for its own
     // sequence; rewriting the KV cache or the state block under it would
     // make its later steps silently wrong.
-    NNZ_REQUIRE(ctx, !m->step_graph, NNZ_ESTATE,
+    NNZ_REQUIRE(ctx, m->steps.empty(), NNZ_ESTATE,
                 "prefill: a decode stream is active (call decode_end first)");
     for (uint32_t i = 0; i < n; ++i)
         NNZ_REQUIRE(ctx, tokens_host[i] < c.vocab_size, NNZ_EINVAL, "prefill: token id out of range");
@@ -909,6 +933,28 @@ int capture_step(nnz_model *m, uint32_t max_seq, nnz_graph **g) {
     return brc ? brc : erc;
 }
 
+// The step graphs of a plan whose steps attend over first .. last keys: one
+// per run of `per` attention-chunk counts, `per` the smallest that keeps the
+// plan within MAX_STEP_GRAPHS graphs.
+int capture_steps(nnz_model *m, uint32_t first, uint32_t last, StepGraphs &s) {
+    const uint32_t chunk = nnz_attn_fused_chunk(last, m->c.num_kv_heads);
+    const uint32_t c0 = ceil_div(first, chunk), c1 = ceil_div(last, chunk);
+    const uint32_t per = ceil_div(c1 - c0 + 1, MAX_STEP_GRAPHS);
+    s.first = first;
+    for (uint32_t c = c0; c <= c1; c += per) {
+        const uint32_t top = std::min(last, (c + per - 1) * chunk);
+        nnz_graph *g = nullptr;
+        const int rc = capture_step(m, top, &g);
+        if (rc) {
+            s.destroy();
+            return rc;
+        }
+        s.g.push_back(g);
+        s.top.push_back(top);
+    }
+    return NNZ_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -919,7 +965,7 @@ int nnz_model_generate(nnz_model *m, const uint32_t *prompt, uint32_t n_prompt, 
     if (!m) return NNZ_EINVAL;
     nnz_ctx *ctx = m->ctx;
     NNZ_REQUIRE(ctx, out_tokens, NNZ_EINVAL, "generate: null output");
-    NNZ_REQUIRE(ctx, !m->step_graph, NNZ_ESTATE,
+    NNZ_REQUIRE(ctx, m->steps.empty(), NNZ_ESTATE,
                 "generate: a decode stream is active (call decode_end first)");
     uint32_t max_seq;
     RC(begin_decode(m, prompt, n_prompt, n_new, &max_seq));
@@ -935,8 +981,8 @@ int nnz_model_generate(nnz_model *m, const uint32_t *prompt, uint32_t n_prompt, 
     // host looks at the state block every POLL steps and stops queueing
     // once the stream has ended.
     constexpr uint32_t POLL = 8;
-    nnz_graph *g = nullptr;
-    if (!rc && use_graph) rc = capture_step(m, max_seq, &g);
+    StepGraphs sg;
+    if (!rc && use_graph) rc = capture_steps(m, n_prompt + 1, max_seq, sg);
     if (!rc && out_step_ms && hipEventRecord(ev[0], ctx->stream) != hipSuccess) rc = NNZ_EHIP;
     uint32_t done_steps = 0;
     for (uint32_t i = 0; i < n_new && !rc; ++i) {
@@ -947,7 +993,8 @@ int nnz_model_generate(nnz_model *m, const uint32_t *prompt, uint32_t n_prompt, 
                 rc = NNZ_EHIP;
             if (rc || st[ST_DONE]) break;
         }
-        rc = use_graph ? nnz_graph_replay(ctx, g) : pick_step(m, max_seq);
+        // step i attends over n_prompt + 1 + i keys (fewer once a stop token ended the stream)
+        rc = use_graph ? nnz_graph_replay(ctx, sg.for_seq(n_prompt + 1 + i)) : pick_step(m, n_prompt + 1 + i);
         if (!rc && out_step_ms && hipEventRecord(ev[i + 1], ctx->stream) != hipSuccess) rc = NNZ_EHIP;
         done_steps = i + 1;
     }
@@ -958,7 +1005,7 @@ int nnz_model_generate(nnz_model *m, const uint32_t *prompt, uint32_t n_prompt, 
             else out_step_ms[i] = 0.f;
     for (auto &e : ev)
         if (e) hipEventDestroy(e);
-    if (g) nnz_graph_destroy(g);
+    sg.destroy();
     if (rc) return rc;
     uint32_t emitted;
     int stopped;
@@ -975,7 +1022,7 @@ int nnz_model_set_sampling(nnz_model *m, const nnz_sampling_params *p) {
                 "set_sampling: temperature must be >= 0");
     NNZ_REQUIRE(m->ctx, p->top_p > 0.f, NNZ_EINVAL,
                 "set_sampling: top_p must be > 0 (>= 1 disables it)");
-    NNZ_REQUIRE(m->ctx, !m->step_graph, NNZ_ESTATE, "set_sampling: a decode stream is active");
+    NNZ_REQUIRE(m->ctx, m->steps.empty(), NNZ_ESTATE, "set_sampling: a decode stream is active");
     m->sp = *p;
     return NNZ_OK;
 }
@@ -984,7 +1031,7 @@ int nnz_model_set_eos(nnz_model *m, const uint32_t *ids, uint32_t n) {
     if (!m) return NNZ_EINVAL;
     NNZ_REQUIRE(m->ctx, n <= NNZ_MAX_EOS && (n == 0 || ids), NNZ_EINVAL,
                 "set_eos: at most %u stop tokens", NNZ_MAX_EOS);
-    NNZ_REQUIRE(m->ctx, !m->step_graph, NNZ_ESTATE, "set_eos: a decode stream is active");
+    NNZ_REQUIRE(m->ctx, m->steps.empty(), NNZ_ESTATE, "set_eos: a decode stream is active");
     m->n_eos = n;
     for (uint32_t i = 0; i < n; ++i) m->eos[i] = ids[i];
     return NNZ_OK;
@@ -1004,21 +1051,25 @@ int nnz_model_decode_status(nnz_model *m, uint32_t *emitted, int *stopped) {
 int nnz_model_decode_begin(nnz_model *m, const uint32_t *prompt, uint32_t n_prompt,
                            uint32_t max_new) {
     if (!m) return NNZ_EINVAL;
-    NNZ_REQUIRE(m->ctx, !m->step_graph, NNZ_ESTATE, "decode_begin: a decode stream is active");
+    NNZ_REQUIRE(m->ctx, m->steps.empty(), NNZ_ESTATE, "decode_begin: a decode stream is active");
     uint32_t max_seq;
     RC(begin_decode(m, prompt, n_prompt, max_new, &max_seq));
-    RC(capture_step(m, max_seq, &m->step_graph));
+    RC(capture_steps(m, n_prompt + 1, max_seq, m->steps));
     m->stream_steps_left = max_new;
+    m->stream_step = 0;
     return NNZ_OK;
 }
 
 int nnz_model_decode_steps(nnz_model *m, uint32_t n) {
     if (!m) return NNZ_EINVAL;
-    NNZ_REQUIRE(m->ctx, m->step_graph, NNZ_ESTATE, "decode_steps: call decode_begin first");
+    NNZ_REQUIRE(m->ctx, !m->steps.empty(), NNZ_ESTATE, "decode_steps: call decode_begin first");
     NNZ_REQUIRE(m->ctx, n <= m->stream_steps_left, NNZ_EINVAL,
                 "decode_steps: %u steps requested, %u left in the plan", n, m->stream_steps_left);
-    for (uint32_t i = 0; i < n; ++i) RC(nnz_graph_replay(m->ctx, m->step_graph));
-    m->stream_steps_left -= n;
+    for (uint32_t i = 0; i < n; ++i) {
+        RC(nnz_graph_replay(m->ctx, m->steps.for_seq(m->steps.first + m->stream_step)));
+        ++m->stream_step;
+        --m->stream_steps_left;
+    }
     return NNZ_OK;
 }
 
@@ -1035,12 +1086,12 @@ int nnz_model_decode_read(nnz_model *m, uint32_t n, uint32_t *out_tokens, float 
 
 int nnz_model_decode_end(nnz_model *m) {
     if (!m) return NNZ_EINVAL;
-    if (m->step_graph) {
+    if (!m->steps.empty()) {
         RC(nnz_stream_sync(m->ctx, 600000));
-        nnz_graph_destroy(m->step_graph);
-        m->step_graph = nullptr;
+        m->steps.destroy();
     }
     m->stream_steps_left = 0;
+    m->stream_step = 0;
     return NNZ_OK;
 }
 

@@ -695,13 +695,15 @@ def bench_kernels(dev, quick=False, only=None):
 
 def sources_digest():
     """sha256 (first 16 hex digits) of the HIP sources the library is built
-    from (nnzap_amd/csrc/*.hip, *.h and include/nnz.h, sorted by name): the
-    profiles under profiles/ record the digest of the sources they measured."""
+    from and of its build flags (nnzap_amd/csrc/*.hip, *.h, include/nnz.h and
+    nnzap_amd/build.py, sorted by name): the profiles under profiles/ record
+    the digest of the sources they measured."""
     import hashlib
     h = hashlib.sha256()
     files = sorted(glob.glob(os.path.join(ROOT, "nnzap_amd", "csrc", "*.hip")) +
                    glob.glob(os.path.join(ROOT, "nnzap_amd", "csrc", "*.h")) +
-                   [os.path.join(ROOT, "include", "nnz.h")], key=os.path.basename)
+                   [os.path.join(ROOT, "include", "nnz.h"),
+                    os.path.join(ROOT, "nnzap_amd", "build.py")], key=os.path.basename)
     for f in files:
         h.update(os.path.basename(f).encode())
         h.update(open(f, "rb").read())

@@ -45,9 +45,18 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found; the HIP toolchain is required to build nnzap_amd")
 
 
+# Per-source additions.  gemm.hip: MFMA accumulators in VGPRs rather than
+# AGPRs (the gate/up GEMM otherwise moves its 64 accumulator registers
+# through v_accvgpr_read/mov around the k-phase reduction and the epilogue:
+# ~300 instructions per wave; same total register count).
+EXTRA_FLAGS = {
+    "gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")

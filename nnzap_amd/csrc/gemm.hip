@@ -15,8 +15,9 @@
 //     from LDS feeds 2, and the KQ partial tiles are summed through LDS at
 //     the end.
 //   * A is staged in LDS KQ k-steps (64 KQ k) at a time, double-buffered, with
-//     one barrier per stage; the 16-byte piece p of row r sits at slot
-//     p ^ (r & 15), so the 16 rows of an MFMA fragment read hit distinct banks.
+//     one barrier per stage, by loads straight into LDS (global_load_lds,
+//     no registers); the 16-byte piece p of row r sits at slot p ^ (r & 15),
+//     so the 16 rows of an MFMA fragment read hit distinct banks.
 //   * W is staged as packed bits (a 16-byte entry per row and k-step: two
 //     code words and the group scale); each lane reads the 8 bits of its B
 //     fragment and expands them in registers to f16 +-s (two ALU operations
@@ -43,15 +44,41 @@ template <int KQ> constexpr int SK = BK * KQ;        // k per LDS stage
 template <int KQ> constexpr int PIECES = SK<KQ> / 8; // 16-byte pieces per A row and stage
 template <int KQ> constexpr int WROW = KQ + 1;       // W entries per LDS row (one of padding)
 
-// waitcnt immediate for gfx9: lgkmcnt = 0 only (the wave's LDS stores done)
-constexpr int LGKM0_IMM = 15 | (3 << 14) | (7 << 4);
+// One 16-byte global load per lane straight into LDS: lane l's bytes land
+// at LDS address lds + 16 l (lds wave-uniform, in M0).  In asm rather than
+// the builtin: for the builtin the compiler waits for every such load in
+// flight before any LDS read it cannot prove apart (here: the fragment reads
+// of the other stage buffer), which would serialise the pipeline.  Its
+// completion is waited for explicitly (load_barrier); the compiler's own
+// vmcnt waits stay correct, only more conservative, with these loads
+// unknown to it (loads complete in order).  The s_nop is the one wait state
+// gfx9 requires between an SALU write of M0 and an LDS DMA reading it (the
+// compiler's hazard check does not look into asm).
+__device__ __forceinline__ void global_load_lds16(const void *g, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds) : "memory");
+}
 
-// Workgroup barrier for the pipelined loop: the wave's own LDS stores are
-// waited for, then s_barrier.  __syncthreads() would add a release fence,
-// which also waits for the next stage's global loads still in flight.  The
-// empty asm statements keep the compiler from moving LDS accesses across.
+// Workgroup barrier for a pipelined loop staging through registers: the
+// wave's own LDS stores are waited for, then s_barrier.  __syncthreads()
+// would add a release fence, which also waits for the next stage's global
+// loads still in flight.  The empty asm statements keep the compiler from
+// moving LDS accesses across.
+constexpr int LGKM0_IMM = 15 | (3 << 14) | (7 << 4);   // gfx9 waitcnt immediate: lgkmcnt 0 only
 __device__ __forceinline__ void step_barrier() {
     __builtin_amdgcn_s_waitcnt(LGKM0_IMM);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Workgroup barrier for a pipelined loop loading A straight into LDS: the
+// wave's loads into LDS and its own LDS stores are waited for (vmcnt 0,
+// lgkmcnt 0: the data of a global_load_lds is in LDS when it is counted),
+// then s_barrier.  The empty asm statements keep the compiler from moving
+// LDS accesses across.
+constexpr int VM0_LGKM0_IMM = 7 << 4;   // gfx9 waitcnt immediate, expcnt not waited
+__device__ __forceinline__ void load_barrier() {
+    __builtin_amdgcn_s_waitcnt(VM0_LGKM0_IMM);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -163,15 +190,20 @@ __global__ __launch_bounds__(64 * WN * KQ) void dq_gemm_kernel(const f16_t *A, c
 #pragma unroll
             for (int j = 0; j < NJ; ++j) acc[m][i][j] = (float4v){0.f, 0.f, 0.f, 0.f};
 
-    // A loader: piece (tid % 32) of rows tid / 32 + 16 u, u < 4 (rows past P
-    // re-read row P - 1, discarded at the store; k-steps past the end re-read
-    // the last one, never used).
+    // A loader: straight into LDS (global_load_lds_dwordx4: the 64 lanes of
+    // a wave instruction fill 64 consecutive 16-byte slots, no registers).
+    // Thread tid fills slot lp of rows lr + 16 u, u < A_LOADS, which holds
+    // piece lp ^ (r & 15) = lp ^ (lr & 15) of the row, so that is the piece
+    // it loads (rows past P re-read row P - 1, discarded at the store;
+    // k-steps past the end re-read the last one, never used).
     const int lp = tid & (PIECES - 1), lr = tid / PIECES;
     constexpr int A_ROW_STEP = THREADS / PIECES;   // rows between a thread's pieces
+    static_assert(A_ROW_STEP % 16 == 0, "a thread's rows share r & 15");
+    const int ap = lp ^ (lr & 15);                 // the piece this thread loads
     const f16_t *arow[A_LOADS];
 #pragma unroll
     for (int u = 0; u < A_LOADS; ++u)
-        arow[u] = A + (size_t)min(p0 + (uint32_t)(lr + A_ROW_STEP * u), P - 1) * K + (lp & 7) * 8;
+        arow[u] = A + (size_t)min(p0 + (uint32_t)(lr + A_ROW_STEP * u), P - 1) * K + (ap & 7) * 8;
     // W loader: thread t < 256 NMAT loads k-step t % 4 of the stage for row
     // (t / 4) % 64 of matrix t / 256: the step's two code words and its scale.
     const int wl_m = tid / (64 * KQ), wl_row = (tid / KQ) & 63, wl_q = tid % KQ;
@@ -182,28 +214,25 @@ __global__ __launch_bounds__(64 * WN * KQ) void dq_gemm_kernel(const f16_t *A, c
                                 (size_t)(n0 + wl_row) * groups_per_row;
     const int bsh = 8 * (lane >> 4);   // the lane's byte within a 32-k word
 
-    // One stage in flight: A pieces and this thread's W entry, loaded at the
-    // start of the previous stage and stored to LDS at its end.
-    u32x4 areg[A_LOADS];
+    // One stage in flight: the A pieces land in the other LDS buffer and this
+    // thread's W entry in registers (loaded first, so waiting for it leaves
+    // the A loads in flight), stored to LDS at the stage's end.
     u32x2 wreg = {0u, 0u};
     uint32_t sreg = 0;
+    const int wbase = wave * 64;   // the wave's first 16-byte slot of an instruction
     auto issue = [&](uint32_t st) __attribute__((always_inline)) {
-        const uint32_t ka = min(st * KQ + (uint32_t)(lp >> 3), nk - 1) * BK;
-#pragma unroll
-        for (int u = 0; u < A_LOADS; ++u) areg[u] = *(const u32x4 *)(arow[u] + ka);
         if (wl) {
             const uint32_t ks = min(st * KQ + (uint32_t)wl_q, nk - 1);
             wreg = *(const u32x2 *)(wl_codes + 2 * ks);
             sreg = wl_scales[(ks * BK) >> gs_log2];
         }
+        const uint32_t ka = min(st * KQ + (uint32_t)(ap >> 3), nk - 1) * BK;
+        const uint32_t lds = __builtin_amdgcn_readfirstlane(
+            (uint32_t)(size_t)(__attribute__((address_space(3))) f16_t *)(As[st & 1] + 8 * wbase));
+#pragma unroll
+        for (int u = 0; u < A_LOADS; ++u) global_load_lds16(arow[u] + ka, lds + 16u * (uint32_t)(u * THREADS));
     };
     auto stage = [&](uint32_t st) __attribute__((always_inline)) {
-        f16_t *buf = As[st & 1];
-#pragma unroll
-        for (int u = 0; u < A_LOADS; ++u) {
-            const int r = lr + A_ROW_STEP * u;
-            ((u32x4 *)(buf + r * SK))[lp ^ (r & 15)] = areg[u];
-        }
         if (wl) Ws[st & 1][wl_m][wl_row * WROW + wl_q] = (u32x4){wreg[0], wreg[1], sreg, 0u};
     };
     auto compute = [&](uint32_t st) __attribute__((always_inline)) {
@@ -245,12 +274,12 @@ __global__ __launch_bounds__(64 * WN * KQ) void dq_gemm_kernel(const f16_t *A, c
     // read in stage st - 1, before the previous barrier).
     issue(0);
     stage(0);
-    step_barrier();
+    load_barrier();
     for (uint32_t st = 0; st < nst; ++st) {
         if (st + 1 < nst) issue(st + 1);   // block-uniform
         compute(st);
         if (st + 1 < nst) stage(st + 1);
-        step_barrier();
+        load_barrier();
     }
 
     // k-phase reduction through LDS (the stage buffers are free): phases 2, 3
@@ -433,6 +462,8 @@ __global__ __launch_bounds__(128 * KQ) __attribute__((amdgpu_waves_per_eu(2))) v
 #pragma unroll
             for (int j = 0; j < 2; ++j) acc[m][i][j] = (float4v){0.f, 0.f, 0.f, 0.f};
 
+    // A through registers (loading it straight into LDS, as dq_gemm_kernel
+    // does, measured no faster here: 4-bit down 37.7 -> 38.6 us)
     const int lp = tid & (Q4_PIECES - 1), lr = tid / Q4_PIECES;
     constexpr int A_ROW_STEP = Q4_THREADS / Q4_PIECES;
     const f16_t *arow[A_LOADS];

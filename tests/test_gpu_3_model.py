@@ -87,6 +87,46 @@ def test_calls_during_decode_stream_are_refused(mdev, tiny):
         m.close()
 
 
+def test_decode_stream_across_step_graphs(mdev):
+    """A decode plan whose steps span ten 64-token attention-chunk counts
+    (prompt 40 + 600 steps): decode_begin captures five step graphs (two
+    chunk counts each) and decode_steps, called in uneven batches, replays
+    for each step the one sized for its length.  Tokens and margins equal
+    the uncaptured loop's (which sizes every step exactly; partials past the
+    live length are never read, so the arithmetic is the same) bit for bit,
+    and the oracle's tokens up to its first near-tie step."""
+    cfg = cf.DecoderConfig(**{**cf.TINY.__dict__, "max_context_length": 1024,
+                              "max_prefill_length": 512})
+    w = cf.decoder_weights(cfg, norm_mode="unit")
+    prompt = cf.prompt_ids(cfg, 40)
+    n = 600
+    ref, ref_m = OracleDecoder(w).generate(prompt, n + 1)
+    m = DecoderModel(mdev, cfg)
+    try:
+        m.load(w)
+        print("decode stream: 600 steps in batches 1, 7, 64, 200, 328", flush=True)
+        m.decode_begin(prompt, n)
+        for k in (1, 7, 64, 200, 328):
+            m.decode_steps(k)
+        toks, margins = m.decode_read(n + 1)
+        m.decode_end()
+        print("decode stream: uncaptured loop", flush=True)
+        eager, eager_m, _ = m.generate(prompt, n + 1, use_graph=False)
+    finally:
+        m.close()
+    assert np.array_equal(toks, eager[:n + 1])
+    assert np.array_equal(margins, eager_m[:n + 1])
+    # margins are logit differences: two logit errors of <= 1e-3 max|logit|
+    ties = np.flatnonzero(ref_m < 2e-3)
+    bad = np.flatnonzero(toks != ref)
+    first_tie = int(ties[0]) if len(ties) else n + 1
+    first_bad = int(bad[0]) if len(bad) else n + 1
+    print(f"decode stream: matches the oracle for {first_bad} of {n + 1} tokens "
+          f"(first oracle near-tie at {first_tie})", flush=True)
+    assert first_bad >= first_tie
+    assert np.max(np.abs(margins[:first_bad] - ref_m[:first_bad])) < 2e-3
+
+
 def test_tiny_prefill_chunks_match_single_prefill(mdev, tiny):
     """Two prefill calls (start 0, start 30) equal one call over the same tokens."""
     cfg, w = tiny

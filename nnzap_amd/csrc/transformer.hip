@@ -276,13 +276,45 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(
 // and the rotation needs no shuffle; frequencies from the model's table.
 // q goes out as float32 [nq][hq][D], or, with qsplit > 0, as the operands
 // of the MFMA prefill attention: x = q * qsplit as f16 hi = f16(x) and
-// lo = f16(x - hi), [nq][hq][2][D] (hi row, then lo row).
+// lo = f16(x - hi), [nq][hq][2][D] (hi row, then lo row).  V rows go to
+// the transposed cache from waves of their own, launched first, one per
+// (KV head, 64 tokens, 16 dims).  (Written by the k waves, two 2-byte stores
+// per lane to 64 different dim rows each, the V copy took 2.6 of the
+// kernel's 7.9 us at 512 tokens.)
 __global__ __launch_bounds__(256) void attn_prep_waves_kernel(
     const f16_t *q, const f16_t *kr, const f16_t *vr, const float *qn, const float *kn,
     void *qout, f16_t *kc, f16_t *vc, const float *inv_freq, uint32_t hq, uint32_t hkv,
     uint32_t head_dim, uint32_t pos0, uint32_t nq, uint32_t max_ctx, float eps, float qsplit) {
     const uint32_t heads = hq + hkv;
-    const uint32_t u = blockIdx.x * 4u + (threadIdx.x >> 6);
+    const uint32_t ng = (nq + 63u) / 64u, ns = (head_dim + 15u) / 16u;
+    const uint32_t v_units = hkv * ng * ns;
+    const uint32_t uu = blockIdx.x * 4u + (threadIdx.x >> 6);
+    if (uu < v_units) {
+        // V units first: (KV head, 64-token group, 16-dim slice).  Lane t
+        // copies dims 16 s .. 16 s + 15 of token 64 g + t's V row into the
+        // transposed cache, one dim row per store instruction, so a store
+        // covers 64 consecutive positions (128 bytes) rather than 64 rows.
+        const uint32_t sl = uu % ns, g = (uu / ns) % ng, h = uu / (ns * ng);
+        const uint32_t z = g * 64u + (threadIdx.x & 63u);
+        if (z >= nq) return;
+        const uint32_t *row = (const uint32_t *)(vr + ((size_t)z * hkv + h) * head_dim) + 8u * sl;
+        const __amdgpu_buffer_rsrc_t dst = __builtin_amdgcn_make_buffer_rsrc(
+            vc + (size_t)h * max_ctx * head_dim, (short)0, (int)(max_ctx * head_dim * 2u), 0x00020000);
+        const uint32_t voff = (pos0 + z) * 2u, rstride = max_ctx * 2u, nw = head_dim / 2u;
+        uint32_t w[8];
+#pragma unroll
+        for (uint32_t i = 0; i < 8u; ++i)
+            if (8u * sl + i < nw) w[i] = row[i];
+#pragma unroll
+        for (uint32_t i = 0; i < 8u; ++i)
+            if (8u * sl + i < nw) {
+                const uint32_t d = 2u * (8u * sl + i);
+                __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(w[i] & 0xFFFFu), dst, voff, d * rstride, 0);
+                __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(w[i] >> 16), dst, voff, (d + 1u) * rstride, 0);
+            }
+        return;
+    }
+    const uint32_t u = uu - v_units;
     if (u >= heads * nq) return;   // whole waves only
     const uint32_t z = u / heads, b = u % heads, p = threadIdx.x & 63u;
     const uint32_t pos = pos0 + z;
@@ -321,9 +353,6 @@ __global__ __launch_bounds__(256) void attn_prep_waves_kernel(
         const uint32_t kw = (uint32_t)__builtin_bit_cast(uint16_t, (f16_t)r0) |
                             (uint32_t)__builtin_bit_cast(uint16_t, (f16_t)r1) << 16;
         *(uint32_t *)(kc + h * stride + (size_t)pos * head_dim + 2u * p) = kw;
-        const f16_t *vs = vr + ((size_t)z * hkv + h) * head_dim + 2u * p;
-        vc[h * stride + (size_t)(2u * p) * max_ctx + pos] = vs[0];
-        vc[h * stride + (size_t)(2u * p + 1u) * max_ctx + pos] = vs[1];
     }
 }
 
@@ -2219,7 +2248,8 @@ int nnz_attn_prep_waves_launch(nnz_ctx *ctx, const void *q, const void *kr, cons
                                uint32_t pos0, uint32_t nq, uint32_t max_ctx, float eps, float qsplit) {
     NNZ_REQUIRE(ctx, head_dim % 2 == 0 && head_dim <= 128, NNZ_EUNSUPPORTED,
                 "attn_prep: head_dim %u (even, <= 128)", head_dim);
-    const uint32_t units = (hq + hkv) * nq;
+    // (KV head, 64-token group, 16-dim slice) units for V, then (token, head) units for q and k
+    const uint32_t units = hkv * ceil_div(nq, 64u) * ceil_div(head_dim, 16u) + (hq + hkv) * nq;
     attn_prep_waves_kernel<<<ceil_div(units, 4u), 256, 0, ctx->stream>>>(
         (const f16_t *)q, (const f16_t *)kr, (const f16_t *)vr, qn, kn, qout, (f16_t *)kc,
         (f16_t *)vc, inv_freq, hq, hkv, head_dim, pos0, nq, max_ctx, eps, qsplit);

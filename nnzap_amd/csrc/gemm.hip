@@ -653,9 +653,12 @@ __global__ __launch_bounds__(128 * KQ) __attribute__((amdgpu_waves_per_eu(2))) v
 }
 
 // k-phases and W-row groups of the single-matrix launches.  Measured at P =
-// 512: with a grid of at most one block per CU, 8 k-phases (16 waves, 149
-// KB of LDS) are 2-10 % faster than 4; larger grids run 4 (75 KB: two
-// blocks per CU; the fused Q/K/V launch, 512 blocks: 17.1 us against 20.6).
+// 512: with a grid of at most one block per CU and K > 2048 (the down
+// projection), 8 k-phases (16 waves, 149 KB of LDS) are faster than 4
+// (23.4 against 23.5-24.3 us); with A loaded straight into LDS, K = 2048
+// does better on 4 (O 11.5 -> 11.3, K/V 9.4 -> 8.8 us); larger grids run 4
+// (75 KB: two blocks per CU; the fused Q/K/V launch, 512 blocks: 17.1 us
+// against 20.6).
 // The gate/up pair runs 2 (4-wave blocks, 44 KB, 88 VGPRs: its 768 blocks
 // are all resident at once; 48.7 us with 4 k-phases, 39.5 us with 2).  One
 // W-row group (64 x 64 wave tiles, half the A reads from LDS, 8 waves) is
@@ -667,7 +670,7 @@ template <int MODE>
 void launch_single(nnz_ctx *ctx, uint32_t grid, const f16_t *A, const uint32_t *c0,
                    const uint16_t *s0, void *out, uint32_t P, uint32_t M, uint32_t K, uint32_t gl,
                    const GemmSegs &sg) {
-    if (grid <= ONE_ROUND_BLOCKS)
+    if (grid <= ONE_ROUND_BLOCKS && K > 2048)
         dq_gemm_kernel<MODE, 1, 8, WN1><<<grid, 64 * WN1 * 8, 0, ctx->stream>>>(
             A, c0, s0, nullptr, nullptr, out, P, M, K, gl, sg);
     else
